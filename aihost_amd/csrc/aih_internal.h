@@ -1,0 +1,70 @@
+// aih_internal.h -- shared definitions of libaihost_hip.so (not part of the ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <cstddef>
+#include <mutex>
+#include <unordered_map>
+
+#include "../../include/aihost_hip.h"
+
+// GGUF block geometry (AIHost/AIHost/GGUF/GGUFTensorInfo.cs:60-71,
+// AIHost/AIHost/Compute/QuantizationFormats.cs:6-12).
+struct aih_block_geom { int elems; int bytes; };
+
+static inline aih_block_geom aih_geom(int type)
+{
+    switch (type) {
+    case AIH_TYPE_Q8_0: return {32, 34};
+    case AIH_TYPE_Q4_0: return {32, 18};
+    case AIH_TYPE_Q4_K: return {256, 144};
+    case AIH_TYPE_Q6_K: return {256, 210};
+    case AIH_TYPE_F32:  return {1, 4};
+    default:            return {0, 0};
+    }
+}
+
+static inline bool aih_is_quant(int type)
+{
+    return type == AIH_TYPE_Q8_0 || type == AIH_TYPE_Q4_0 ||
+           type == AIH_TYPE_Q4_K || type == AIH_TYPE_Q6_K;
+}
+
+// One device + one in-order stream + a pinned staging ring for uploads.
+struct aih_ctx {
+    int device = -1;
+    hipStream_t stream = nullptr;
+    static constexpr int kStageSlots = 2;
+    static constexpr size_t kStageBytes = 16u << 20;   // 16 MiB per slot
+    void *stage[kStageSlots] = {nullptr, nullptr};
+    hipEvent_t stage_done[kStageSlots] = {nullptr, nullptr};
+    bool stage_pending[kStageSlots] = {false, false};
+    static constexpr int kEvents = 16;
+    hipEvent_t ev[kEvents] = {};
+    std::mutex lock;                                    // guards `allocs`
+    std::unordered_map<void *, size_t> allocs;
+    size_t tracked_bytes = 0;
+    int cu_count = 0;
+};
+
+#define AIH_TRY(expr)                                  \
+    do {                                               \
+        hipError_t aih_e_ = (expr);                    \
+        if (aih_e_ != hipSuccess) return (int)aih_e_;  \
+    } while (0)
+
+// Status of the most recent launch on this thread.
+static inline int aih_launch_status()
+{
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? AIH_OK : (int)e;
+}
+
+// Kernel launch entry points implemented per source file.
+int aih_launch_dequant(aih_ctx *ctx, int type, const void *q, float *out,
+                       uint64_t n_blocks, int f16_mode);
+int aih_launch_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
+                       const float *X, int64_t ldx, float *Y, int64_t ldy, int batch);
+int aih_launch_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
+                     const float *X, int64_t M, float *Y);

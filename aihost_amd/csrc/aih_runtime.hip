@@ -1,0 +1,373 @@
+// aih_runtime.hip -- device, buffers, transfers, queue and timing of
+// libaihost_hip.so.  This is the HIP device that replaces the reference's ROCm
+// backend (AIHost/AIHost/ICompute/ROCm/*.cs) for the quantized-matmul path.
+#include "aih_internal.h"
+
+#include <cstring>
+#include <cstdio>
+#include <new>
+
+namespace {
+
+int select_device(aih_ctx *ctx)
+{
+    int cur = -1;
+    AIH_TRY(hipGetDevice(&cur));
+    if (cur != ctx->device) AIH_TRY(hipSetDevice(ctx->device));
+    return AIH_OK;
+}
+
+int release(aih_ctx *ctx)
+{
+    // Dispose never fails (ROCmComputeBuffer.cs:81-93): errors are ignored here.
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    for (auto &kv : ctx->allocs) (void)hipFree(kv.first);
+    ctx->allocs.clear();
+    ctx->tracked_bytes = 0;
+    for (int i = 0; i < aih_ctx::kStageSlots; ++i) {
+        if (ctx->stage_done[i]) (void)hipEventDestroy(ctx->stage_done[i]);
+        if (ctx->stage[i]) (void)hipHostFree(ctx->stage[i]);
+    }
+    for (int i = 0; i < aih_ctx::kEvents; ++i)
+        if (ctx->ev[i]) (void)hipEventDestroy(ctx->ev[i]);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return AIH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int aih_abi_version(void) { return AIH_ABI_VERSION; }
+
+int aih_init(int device_index, aih_ctx **out)
+{
+    if (!out) return AIH_E_INVALID;
+    *out = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count <= 0) return AIH_E_NO_DEVICE;
+    if (device_index < 0 || device_index >= count) return AIH_E_NO_DEVICE;
+    hipDeviceProp_t prop;
+    AIH_TRY(hipGetDeviceProperties(&prop, device_index));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return AIH_E_NOT_GFX950;
+    AIH_TRY(hipSetDevice(device_index));
+
+    aih_ctx *ctx = new (std::nothrow) aih_ctx();
+    if (!ctx) return (int)hipErrorOutOfMemory;
+    ctx->device = device_index;
+    ctx->cu_count = prop.multiProcessorCount;
+    hipError_t err = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    for (int i = 0; err == hipSuccess && i < aih_ctx::kStageSlots; ++i) {
+        err = hipHostMalloc(&ctx->stage[i], aih_ctx::kStageBytes, hipHostMallocDefault);
+        if (err == hipSuccess) err = hipEventCreateWithFlags(&ctx->stage_done[i], hipEventDisableTiming);
+    }
+    for (int i = 0; err == hipSuccess && i < aih_ctx::kEvents; ++i)
+        err = hipEventCreate(&ctx->ev[i]);
+    if (err != hipSuccess) {
+        release(ctx);
+        return (int)err;
+    }
+    *out = ctx;
+    return AIH_OK;
+}
+
+int aih_destroy(aih_ctx *ctx)
+{
+    if (!ctx) return AIH_E_INVALID;
+    (void)select_device(ctx);
+    return release(ctx);
+}
+
+int aih_device_info_get(aih_ctx *ctx, aih_device_info *out)
+{
+    if (!ctx || !out) return AIH_E_INVALID;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    hipDeviceProp_t prop;
+    AIH_TRY(hipGetDeviceProperties(&prop, ctx->device));
+    std::memset(out, 0, sizeof(*out));
+    std::snprintf(out->name, sizeof(out->name), "%s", prop.name);
+    std::snprintf(out->arch, sizeof(out->arch), "%s", prop.gcnArchName);
+    out->device_index = ctx->device;
+    out->compute_units = prop.multiProcessorCount;
+    out->wavefront_size = prop.warpSize;
+    out->clock_khz = prop.clockRate;
+    out->memory_clock_khz = prop.memoryClockRate;
+    out->memory_bus_width = prop.memoryBusWidth;
+    size_t free_b = 0, total_b = 0;
+    AIH_TRY(hipMemGetInfo(&free_b, &total_b));
+    out->total_bytes = total_b;
+    out->free_bytes = free_b;
+    std::lock_guard<std::mutex> g(ctx->lock);
+    out->tracked_bytes = ctx->tracked_bytes;
+    out->tracked_buffers = (int64_t)ctx->allocs.size();
+    return AIH_OK;
+}
+
+int aih_malloc(aih_ctx *ctx, size_t bytes, void **dptr)
+{
+    if (!ctx || !dptr) return AIH_E_INVALID;
+    *dptr = nullptr;
+    if (bytes == 0) return AIH_E_INVALID;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();  // clear the sticky error so later calls are unaffected
+        return (int)e;
+    }
+    std::lock_guard<std::mutex> g(ctx->lock);
+    ctx->allocs[p] = bytes;
+    ctx->tracked_bytes += bytes;
+    *dptr = p;
+    return AIH_OK;
+}
+
+int aih_free(aih_ctx *ctx, void *dptr)
+{
+    if (!ctx || !dptr) return AIH_E_INVALID;
+    size_t bytes = 0;
+    {
+        std::lock_guard<std::mutex> g(ctx->lock);
+        auto it = ctx->allocs.find(dptr);
+        if (it == ctx->allocs.end()) return AIH_E_NOT_ALLOCATED;
+        bytes = it->second;
+        ctx->allocs.erase(it);
+        ctx->tracked_bytes -= bytes;
+    }
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    // hipFree synchronises with outstanding work that may still read the buffer.
+    AIH_TRY(hipFree(dptr));
+    return AIH_OK;
+}
+
+int aih_memset(aih_ctx *ctx, void *dptr, int value, size_t bytes)
+{
+    if (!ctx || (!dptr && bytes)) return AIH_E_INVALID;
+    if (!bytes) return AIH_OK;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    AIH_TRY(hipMemsetAsync(dptr, value, bytes, ctx->stream));
+    return AIH_OK;
+}
+
+int aih_memcpy_h2d(aih_ctx *ctx, void *dst, const void *src, size_t bytes)
+{
+    if (!ctx || ((!dst || !src) && bytes)) return AIH_E_INVALID;
+    if (!bytes) return AIH_OK;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    const char *s = static_cast<const char *>(src);
+    char *d = static_cast<char *>(dst);
+    size_t off = 0;
+    int slot = 0;
+    // Double-buffered: the CPU fills one pinned slot while the DMA engine
+    // drains the other.
+    while (off < bytes) {
+        size_t len = bytes - off < aih_ctx::kStageBytes ? bytes - off : aih_ctx::kStageBytes;
+        if (ctx->stage_pending[slot]) {
+            AIH_TRY(hipEventSynchronize(ctx->stage_done[slot]));
+            ctx->stage_pending[slot] = false;
+        }
+        std::memcpy(ctx->stage[slot], s + off, len);
+        AIH_TRY(hipMemcpyAsync(d + off, ctx->stage[slot], len, hipMemcpyHostToDevice, ctx->stream));
+        AIH_TRY(hipEventRecord(ctx->stage_done[slot], ctx->stream));
+        ctx->stage_pending[slot] = true;
+        off += len;
+        slot ^= 1;
+    }
+    return AIH_OK;
+}
+
+int aih_upload_tensor(aih_ctx *ctx, void *dst, const void *host_src, size_t bytes)
+{
+    return aih_memcpy_h2d(ctx, dst, host_src, bytes);
+}
+
+int aih_memcpy_d2h(aih_ctx *ctx, void *dst, const void *src, size_t bytes)
+{
+    if (!ctx || ((!dst || !src) && bytes)) return AIH_E_INVALID;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    if (bytes) AIH_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    AIH_TRY(hipStreamSynchronize(ctx->stream));
+    return AIH_OK;
+}
+
+int aih_memcpy_d2d(aih_ctx *ctx, void *dst, const void *src, size_t bytes)
+{
+    if (!ctx || ((!dst || !src) && bytes)) return AIH_E_INVALID;
+    if (!bytes) return AIH_OK;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    AIH_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+    return AIH_OK;
+}
+
+int aih_sync(aih_ctx *ctx)
+{
+    if (!ctx) return AIH_E_INVALID;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    AIH_TRY(hipStreamSynchronize(ctx->stream));
+    return AIH_OK;
+}
+
+void *aih_stream(aih_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+struct aih_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+int aih_capture_begin(aih_ctx *ctx)
+{
+    if (!ctx) return AIH_E_INVALID;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    AIH_TRY(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    return AIH_OK;
+}
+
+int aih_capture_end(aih_ctx *ctx, aih_graph **out)
+{
+    if (!ctx || !out) return AIH_E_INVALID;
+    *out = nullptr;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    hipGraph_t g = nullptr;
+    AIH_TRY(hipStreamEndCapture(ctx->stream, &g));
+    aih_graph *ag = new (std::nothrow) aih_graph();
+    if (!ag) {
+        (void)hipGraphDestroy(g);
+        return (int)hipErrorOutOfMemory;
+    }
+    ag->graph = g;
+    hipError_t e = hipGraphInstantiate(&ag->exec, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        delete ag;
+        return (int)e;
+    }
+    *out = ag;
+    return AIH_OK;
+}
+
+int aih_graph_launch(aih_ctx *ctx, aih_graph *graph)
+{
+    if (!ctx || !graph) return AIH_E_INVALID;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    AIH_TRY(hipGraphLaunch(graph->exec, ctx->stream));
+    return AIH_OK;
+}
+
+int aih_graph_destroy(aih_graph *graph)
+{
+    if (!graph) return AIH_E_INVALID;
+    if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
+    if (graph->graph) (void)hipGraphDestroy(graph->graph);
+    delete graph;
+    return AIH_OK;
+}
+
+int aih_event_record(aih_ctx *ctx, int slot)
+{
+    if (!ctx || slot < 0 || slot >= aih_ctx::kEvents) return AIH_E_INVALID;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    AIH_TRY(hipEventRecord(ctx->ev[slot], ctx->stream));
+    return AIH_OK;
+}
+
+int aih_event_elapsed(aih_ctx *ctx, int a, int b, float *ms)
+{
+    if (!ctx || !ms || a < 0 || b < 0 || a >= aih_ctx::kEvents || b >= aih_ctx::kEvents)
+        return AIH_E_INVALID;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    AIH_TRY(hipEventSynchronize(ctx->ev[b]));
+    AIH_TRY(hipEventElapsedTime(ms, ctx->ev[a], ctx->ev[b]));
+    return AIH_OK;
+}
+
+const char *aih_strerror(int status)
+{
+    switch (status) {
+    case AIH_OK: return "success";
+    case AIH_E_INVALID: return "invalid argument (null pointer, size or shape)";
+    case AIH_E_UNSUPPORTED: return "ggml tensor type not supported on this path";
+    case AIH_E_NOT_GFX950: return "device is not a gfx950 (MI355X) part";
+    case AIH_E_NOT_ALLOCATED: return "pointer not allocated by this context (double free?)";
+    case AIH_E_LIMIT: return "shape exceeds the kernel limits";
+    case AIH_E_NO_DEVICE: return "no HIP device at that index";
+    default: break;
+    }
+    if (status > 0) return hipGetErrorString((hipError_t)status);
+    return "unknown aihost_hip status";
+}
+
+int64_t aih_row_bytes(int type, int64_t k)
+{
+    aih_block_geom g = aih_geom(type);
+    if (g.elems == 0) return AIH_E_UNSUPPORTED;
+    if (k < 0 || k % g.elems) return AIH_E_INVALID;
+    return (k / g.elems) * g.bytes;
+}
+
+int aih_dequantize(aih_ctx *ctx, int type, const void *q, float *out,
+                   uint64_t n_elems, int f16_mode)
+{
+    if (!ctx) return AIH_E_INVALID;
+    if (!aih_is_quant(type)) return AIH_E_UNSUPPORTED;
+    if (f16_mode != AIH_F16_IEEE && f16_mode != AIH_F16_REFCPU) return AIH_E_INVALID;
+    aih_block_geom g = aih_geom(type);
+    if (n_elems % (uint64_t)g.elems) return AIH_E_INVALID;
+    if (!n_elems) return AIH_OK;
+    if (!q || !out) return AIH_E_INVALID;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    return aih_launch_dequant(ctx, type, q, out, n_elems / (uint64_t)g.elems, f16_mode);
+}
+
+int aih_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
+                const float *X, int64_t ldx, float *Y, int64_t ldy, int batch)
+{
+    if (!ctx) return AIH_E_INVALID;
+    if (!aih_is_quant(type)) return AIH_E_UNSUPPORTED;
+    aih_block_geom g = aih_geom(type);
+    if (N < 0 || K <= 0 || K % g.elems || batch < 1 || batch > 8) return AIH_E_INVALID;
+    if (ldx < K || ldy < N) return AIH_E_INVALID;
+    if (!N) return AIH_OK;
+    if (!W || !X || !Y) return AIH_E_INVALID;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    return aih_launch_qmatvec(ctx, type, W, N, K, X, ldx, Y, ldy, batch);
+}
+
+int aih_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
+              const float *X, int64_t M, float *Y)
+{
+    if (!ctx) return AIH_E_INVALID;
+    if (!aih_is_quant(type)) return AIH_E_UNSUPPORTED;
+    aih_block_geom g = aih_geom(type);
+    if (N < 0 || M < 0 || K <= 0 || K % g.elems) return AIH_E_INVALID;
+    if (!N || !M) return AIH_OK;
+    if (!W || !X || !Y) return AIH_E_INVALID;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    return aih_launch_qgemm(ctx, type, W, N, K, X, M, Y);
+}
+
+int aih_matmul_weights_q(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
+                         const float *X, int64_t M, float *Y)
+{
+    if (M >= 1 && M <= 8) return aih_qmatvec(ctx, type, W, N, K, X, K, Y, N, (int)M);
+    return aih_qgemm(ctx, type, W, N, K, X, M, Y);
+}
+
+}  // extern "C"

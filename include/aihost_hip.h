@@ -1,0 +1,214 @@
+/*
+ * aihost_hip.h -- C ABI of libaihost_hip.so, the gfx950 (MI355X) backend for
+ * AIHost's GGUF block-quantized matrix-product path.
+ *
+ * The library replaces, for this path, the reference's ROCm compute device and
+ * the two-pass "dequantize into an F32 scratch, then F32 SIMT matmul" sequence
+ * with fused HIP kernels compiled offline for gfx950.  Paths below are relative
+ * to the reference repository (Timka654/AIHost).
+ *
+ * Conventions (all entry points):
+ *   - return int status: AIH_OK (0); > 0 is a hipError_t value; < 0 is one of
+ *     the AIH_E_* codes.  Nothing throws or aborts.
+ *     (Replaces HipApi.CheckError, AIHost/AIHost/ICompute/ROCm/HipApi.cs:43-47,
+ *     which throws InvalidOperationException on the managed side.)
+ *   - one aih_ctx = one device + one in-order HIP stream.  A context is not
+ *     thread-safe; callers serialise, as InferenceEngine._gpuLock does today
+ *     (AIHost/AIHost/Inference/InferenceEngine.cs:70,251).
+ *   - device pointers are plain `void*` from aih_malloc.  Pointers passed in
+ *     stay owned by the caller; the library keeps no reference after a call.
+ *   - everything except aih_memcpy_d2h, aih_sync, aih_event_elapsed and the
+ *     aih_host_* utilities is asynchronous on the context stream.
+ *   - ggml type ids are GGUFTensorType values
+ *     (AIHost/AIHost/GGUF/GGUFValueType.cs:26-56).
+ *   - weights are GGUF tensors with dims [ne0 = K, ne1 = N]: row n is K/QK
+ *     consecutive packed blocks, exactly the on-disk byte order.
+ */
+#ifndef AIHOST_HIP_H
+#define AIHOST_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AIH_ABI_VERSION 1
+
+/* ---- status codes ------------------------------------------------------ */
+#define AIH_OK               0
+#define AIH_E_INVALID       -1  /* null pointer, bad size or shape            */
+#define AIH_E_UNSUPPORTED   -2  /* ggml type not handled by this path         */
+#define AIH_E_NOT_GFX950    -3  /* device is not a gfx950 part                */
+#define AIH_E_NOT_ALLOCATED -4  /* pointer not owned by this context (double free) */
+#define AIH_E_LIMIT         -5  /* shape beyond what the kernels support      */
+#define AIH_E_NO_DEVICE     -6  /* no HIP device at that index                */
+
+/* ---- ggml tensor types handled on this path ---------------------------- */
+#define AIH_TYPE_F32   0
+#define AIH_TYPE_Q4_0  2
+#define AIH_TYPE_Q8_0  8
+#define AIH_TYPE_Q4_K 12
+#define AIH_TYPE_Q6_K 14
+
+/* ---- fp16 scale decoding modes for aih_dequantize ---------------------- */
+/* IEEE: the reference's GPU decoder, QuantizationFormats.cs:147-152
+ *       (-0 decodes to +0, every NaN to 0x7FC00000).
+ * REFCPU: the reference's CPU decoder ComputeOps.F16ToF32,
+ *       AIHost/AIHost/Compute/ComputeOps.cs:1497-1522, bit for bit, including
+ *       its wrong exponent for fp16 subnormals. */
+#define AIH_F16_IEEE   0
+#define AIH_F16_REFCPU 1
+
+typedef struct aih_ctx aih_ctx;
+
+typedef struct aih_device_info {
+    char     name[256];
+    char     arch[64];          /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    int32_t  device_index;
+    int32_t  compute_units;
+    int32_t  wavefront_size;
+    int32_t  clock_khz;
+    int32_t  memory_clock_khz;
+    int32_t  memory_bus_width;
+    uint64_t total_bytes;       /* HBM capacity                               */
+    uint64_t free_bytes;        /* hipMemGetInfo at the time of the call      */
+    uint64_t tracked_bytes;     /* bytes currently held through aih_malloc    */
+    int64_t  tracked_buffers;   /* live aih_malloc allocations                */
+} aih_device_info;
+
+/* ---- device / context (IComputeDevice, AIHost/AIHost/ICompute/IComputeDevice.cs:27-72) */
+
+/* Open device `device_index`, create its stream and the pinned staging ring.
+ * Fails with AIH_E_NOT_GFX950 on any other architecture.
+ * Replaces ROCmComputeDevice's constructor (AIHost/AIHost/ICompute/ROCm/ROCmComputeDevice.cs:15-50). */
+int aih_init(int device_index, aih_ctx **out);
+
+/* Free every allocation still owned by the context, then the context.
+ * Replaces ROCmComputeDevice.Dispose. Never fails on a valid context. */
+int aih_destroy(aih_ctx *ctx);
+
+/* Fixed-size device description; replaces the truncated HipDeviceProp
+ * marshalling (HipApi.cs:71-99) and IComputeDevice.GetMemoryInfo (IComputeDevice.cs:71). */
+int aih_device_info_get(aih_ctx *ctx, aih_device_info *out);
+
+/* ---- buffers (IComputeBuffer, AIHost/AIHost/ICompute/IComputeBuffer.cs:6-42) */
+
+/* Device allocation.  Out of memory returns hipErrorOutOfMemory (2), which the
+ * managed side maps to InsufficientVramException
+ * (AIHost/AIHost/ICompute/InsufficientVramException.cs:10-29).
+ * Replaces IComputeDevice.CreateBuffer (IComputeDevice.cs:46) /
+ * ROCmComputeBuffer's constructor (ROCmComputeBuffer.cs:15-24). */
+int aih_malloc(aih_ctx *ctx, size_t bytes, void **dptr);
+
+/* Free an aih_malloc pointer; AIH_E_NOT_ALLOCATED for anything else, including
+ * a second free.  Replaces ROCmComputeBuffer.Dispose (ROCmComputeBuffer.cs:81-93). */
+int aih_free(aih_ctx *ctx, void *dptr);
+
+/* Asynchronous byte fill. */
+int aih_memset(aih_ctx *ctx, void *dptr, int value, size_t bytes);
+
+/* Host -> device through the pinned double-buffered staging ring; returns as
+ * soon as `src` may be reused.  Replaces IComputeBuffer.Write /
+ * IComputeCommandQueue.WriteBuffer (IComputeCommandQueue.cs:11). */
+int aih_memcpy_h2d(aih_ctx *ctx, void *dst, const void *src, size_t bytes);
+
+/* Device -> host, synchronous (waits for prior work on the stream).
+ * Replaces IComputeBuffer.Read / ReadRange (IComputeBuffer.cs:26-41). */
+int aih_memcpy_d2h(aih_ctx *ctx, void *dst, const void *src, size_t bytes);
+
+/* Device -> device, asynchronous. */
+int aih_memcpy_d2d(aih_ctx *ctx, void *dst, const void *src, size_t bytes);
+
+/* Upload one GGUF tensor's packed blocks verbatim (on-disk layout) from host
+ * memory (typically an mmap view of the file).  Same transfer as
+ * aih_memcpy_h2d; named separately because it replaces the host memcpy into
+ * a device pointer in LazyGGUFModel.LoadTensor
+ * (AIHost/AIHost/GGUF/LazyGGUFModel.cs:140-177) and GGUFModel.LoadTensor
+ * (AIHost/AIHost/GGUF/GGUFModel.cs:30-63). */
+int aih_upload_tensor(aih_ctx *ctx, void *dst, const void *host_src, size_t bytes);
+
+/* ---- operators (ComputeOps, AIHost/AIHost/Compute/ComputeOps.cs) ------- */
+
+/* Bytes of one row of k elements of `type`, or a negative status.
+ * (GGUFTensorInfo.SizeInBytes, AIHost/AIHost/GGUF/GGUFTensorInfo.cs:51-78.) */
+int64_t aih_row_bytes(int type, int64_t k);
+
+/* out[0..n_elems) = dequantized blocks of `q` (n_elems a whole number of
+ * blocks), bit-exact to the reference decoders for f16_mode.
+ * Replaces ComputeOps.Dequantize / DequantizeInto (ComputeOps.cs:733-745,
+ * 761-861) and their shaders (QuantizationFormats.cs:140-196, 269-321);
+ * adds Q8_0 and Q4_0, which the reference rejects (ComputeOps.cs:743,774). */
+int aih_dequantize(aih_ctx *ctx, int type, const void *q, float *out,
+                   uint64_t n_elems, int f16_mode);
+
+/* Decode matvec, dequantization fused:
+ *   Y[b*ldy + n] = sum_k X[b*ldx + k] * W[n, k],   b < batch (1..8), n < N.
+ * K must be a whole number of blocks.  fp32 accumulation.
+ * Replaces TempF32 + ComputeOps.MatMulWeights for M = batch <= 8
+ * (TransformerBase.cs:254-271, ComputeOps.cs:275-309, ComputeShaders.cs:93-129). */
+int aih_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
+                const float *X, int64_t ldx, float *Y, int64_t ldy, int batch);
+
+/* Prefill GEMM, dequantization fused:  Y[m*N + n] = sum_k X[m*K + k] * W[n, k].
+ * Tiles of W are dequantized into LDS and contracted on MFMA with fp32
+ * accumulation.  Replaces TempF32 + ComputeOps.MatMulWeights for M > 8. */
+int aih_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
+              const float *X, int64_t M, float *Y);
+
+/* ComputeOps.MatMulWeights semantics for a quantized weight: routes M <= 8 to
+ * aih_qmatvec and larger M to aih_qgemm. */
+int aih_matmul_weights_q(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
+                         const float *X, int64_t M, float *Y);
+
+/* ---- queue (IComputeCommandQueue, IComputeCommandQueue.cs:6-33) -------- */
+
+/* Wait for all work on the context stream.  Replaces Flush
+ * (ROCmComputeCommandQueue.cs:73-80); InsertMemoryBarrier needs no
+ * counterpart because the stream is in order. */
+int aih_sync(aih_ctx *ctx);
+
+/* The context's hipStream_t, for callers that interoperate with other HIP code. */
+void *aih_stream(aih_ctx *ctx);
+
+/* HIP graphs on the context stream: aih_capture_begin starts stream capture,
+ * every asynchronous aih_* call until aih_capture_end is recorded instead of
+ * run, and aih_graph_launch replays the recorded work (e.g. a whole decode
+ * step) with one launch.  Captured work must not include aih_memset, which
+ * records a memset node. */
+typedef struct aih_graph aih_graph;
+int aih_capture_begin(aih_ctx *ctx);
+int aih_capture_end(aih_ctx *ctx, aih_graph **out);
+int aih_graph_launch(aih_ctx *ctx, aih_graph *graph);
+int aih_graph_destroy(aih_graph *graph);
+
+/* GPU timestamps on the context stream (slots 0..15), replacing the host
+ * stopwatch of GlobalProfiler (AIHost/Compute/ComputeProfiler.cs:16-93). */
+int aih_event_record(aih_ctx *ctx, int slot);
+/* Milliseconds between two recorded slots; waits for the later one. */
+int aih_event_elapsed(aih_ctx *ctx, int slot_start, int slot_end, float *ms);
+
+/* Human-readable text for any status code.  Never returns NULL. */
+const char *aih_strerror(int status);
+
+/* ABI version of the loaded library (AIH_ABI_VERSION). */
+int aih_abi_version(void);
+
+/* ---- host utilities (no reference counterpart: the reference has no
+ *      quantizer; these create synthetic GGUF tensors for tests/benchmarks) */
+
+/* out[i] = mean + std * z_i, z ~ N(0,1) from splitmix64 + Box-Muller in
+ * double, cast to float.  Deterministic for a seed; multithreaded. */
+int aih_host_fill_normal(uint64_t seed, float mean, float std, float *out, uint64_t n);
+
+/* Quantize n_rows rows of k floats to `type` blocks following the GGUF rules
+ * (Q8_0: d = absmax/127; Q4_0: d = signed max / -8; Q4_K: 6-bit sub-block
+ * scales and mins; Q6_K: int8 sub-block scales).  dst holds
+ * n_rows * aih_row_bytes(type, k) bytes.  Multithreaded. */
+int aih_host_quantize(int type, const float *src, void *dst, int64_t n_rows, int64_t k);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* AIHOST_HIP_H */

@@ -1,0 +1,135 @@
+"""Fused decode matvec vs the oracle (fp32 sequential accumulation over the
+reference-decoded weights): normwise and max relative error <= 1e-3.
+
+Covers the benchmark shapes (Q8_0 4096x4096; Q4_0 and Q4_K 14336x4096; Q6_K
+4096x14336 at batch 1, 2, 4, 8), odd row counts (partial row groups), small K,
+multi-wave K (14336), K beyond 256 units (1024-thread variant), odd batch,
+padded strides, and argument errors.
+"""
+import numpy as np
+import pytest
+
+from aihost_amd import _native as nat
+from aihost_amd import compute as C
+from gpu_util import assert_close, qmatvec, synth_weight, upload
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3  # relative 1e-3 with fp32 accumulation
+
+
+def x_of(k, batch, seed=43):
+    return C.fill_normal(seed, batch * k, 0.0, 1.0).reshape(batch, k)
+
+
+@pytest.mark.parametrize("qtype,n,k,batch", [
+    (nat.Q8_0, 4096, 4096, 1),
+    (nat.Q4_0, 14336, 4096, 1),
+    (nat.Q4_K, 14336, 4096, 1),
+    (nat.Q6_K, 4096, 14336, 1),
+    (nat.Q6_K, 4096, 14336, 2),
+    (nat.Q6_K, 4096, 14336, 4),
+    (nat.Q6_K, 4096, 14336, 8),
+])
+def test_benchmark_shapes(device, orc, qtype, n, k, batch):
+    w = synth_weight(qtype, n, k)
+    x = x_of(k, batch)
+    y = qmatvec(device, qtype, w, n, k, x)
+    ref = orc.matvec(qtype, w, n, k, x, nthreads=8)
+    nrm, mx = assert_close(y, ref, TOL, "type %d %dx%d b%d" % (qtype, n, k, batch))
+    print("type=%d N=%d K=%d batch=%d normwise=%.3g max=%.3g" % (qtype, n, k, batch, nrm, mx))
+
+
+@pytest.mark.parametrize("qtype,n,k,batch", [
+    (nat.Q4_K, 1, 256, 1), (nat.Q4_K, 37, 256, 1), (nat.Q4_K, 101, 1024, 3), (nat.Q4_K, 64, 14336, 2),
+    (nat.Q6_K, 33, 512, 2), (nat.Q6_K, 7, 256, 5), (nat.Q6_K, 130, 4096, 1),
+    (nat.Q8_0, 19, 128, 1), (nat.Q8_0, 9, 64, 2), (nat.Q8_0, 8, 20480, 1), (nat.Q8_0, 5, 4160, 3),
+    (nat.Q4_0, 5, 64, 1), (nat.Q4_0, 66, 2048, 2), (nat.Q4_0, 3, 32768, 1),
+    (nat.Q4_K, 3, 65536, 1),
+])
+def test_edge_shapes(device, orc, qtype, n, k, batch):
+    w = synth_weight(qtype, n, k, seed=n * 1000 + k)
+    x = x_of(k, batch, seed=k + batch)
+    y = qmatvec(device, qtype, w, n, k, x)
+    ref = orc.matvec(qtype, w, n, k, x, nthreads=8)
+    assert_close(y, ref, TOL, "type %d %dx%d b%d" % (qtype, n, k, batch))
+
+
+def test_padded_strides_leave_gaps_untouched(device, orc):
+    n, k, batch = 50, 512, 3
+    w = synth_weight(nat.Q4_K, n, k)
+    x = x_of(k, batch)
+    y = qmatvec(device, nat.Q4_K, w, n, k, x, ldx=k + 64, ldy=n + 14)
+    assert_close(y[:, :n], orc.matvec(nat.Q4_K, w, n, k, x), TOL)
+    assert np.all(np.isnan(y[:, n:]))  # memset 0xFF pattern untouched
+
+
+def test_subnormal_and_extreme_scales(device, orc):
+    # random bytes with small finite scales: exercises every code value
+    rng = np.random.default_rng(5)
+    n, k = 64, 1024
+    for qtype, bb, offs in ((nat.Q4_K, 144, (0, 2)), (nat.Q6_K, 210, (208,)), (nat.Q8_0, 34, (0,)),
+                            (nat.Q4_0, 18, (0,))):
+        nb = n * k // (256 if bb in (144, 210) else 32)
+        data = rng.integers(0, 256, (nb, bb)).astype(np.uint8)
+        for off in offs:
+            h = rng.integers(0x0001, 0x2400, nb).astype(np.uint16)   # subnormal .. 2^-6
+            data[:, off:off + 2] = h.view(np.uint8).reshape(nb, 2)
+        data = data.reshape(-1)
+        x = x_of(k, 2, seed=qtype)
+        assert_close(qmatvec(device, qtype, data, n, k, x), orc.matvec(qtype, data, n, k, x), TOL,
+                     "type %d" % qtype)
+
+
+def test_linearity_at_full_size(device):
+    n, k = 14336, 4096
+    w = synth_weight(nat.Q4_K, n, k)
+    x1, x2 = x_of(k, 1, 1), x_of(k, 1, 2)
+    y1 = qmatvec(device, nat.Q4_K, w, n, k, x1)
+    y2 = qmatvec(device, nat.Q4_K, w, n, k, x2)
+    y12 = qmatvec(device, nat.Q4_K, w, n, k, np.vstack([x1, x2, x1 + x2]))
+    # batch columns are computed independently of each other
+    assert_close(y12[0], y1[0], 1e-6)
+    assert_close(y12[1], y2[0], 1e-6)
+    assert_close(y12[2], y1[0] + y2[0], 1e-3)
+
+
+def test_compute_ops_mirror(device, orc):
+    ops = C.ComputeOps(device)
+    n, k = 300, 2048
+    wq = synth_weight(nat.Q4_K, n, k)
+    w = C.Tensor.from_quantized(device, wq, k, n, C.DataType.Q4_K)
+    x = x_of(k, 2)
+    a = C.Tensor.from_data(device, x)
+    y = ops.matmul_weights(a, w)
+    assert y.shape == (2, n)
+    assert_close(y.read(), orc.matvec(nat.Q4_K, wq, n, k, x), TOL)
+    f = ops.dequantize(w)
+    assert np.array_equal(f.read().reshape(-1), orc.dequantize(nat.Q4_K, wq, n * k))
+    with pytest.raises(ValueError):
+        ops.matmul_weights(C.Tensor.from_data(device, x_of(k // 2, 1)), w)
+    for t in (w, a, y, f):
+        t.dispose()
+
+
+def test_argument_errors(device):
+    L = nat.lib()
+    h = device.handle
+    wb = upload(device, np.zeros(2304 * 4, np.uint8))
+    xb = upload(device, np.zeros(4096, np.float32))
+    yb = upload(device, np.zeros(64, np.float32))
+    W, X, Y = wb.get_pointer(), xb.get_pointer(), yb.get_pointer()
+    try:
+        assert L.aih_qmatvec(h, nat.Q4_K, W, 4, 4096, X, 4096, Y, 4, 1) == nat.AIH_OK
+        assert L.aih_qmatvec(h, nat.Q4_K, W, 0, 4096, X, 4096, Y, 4, 1) == nat.AIH_OK
+        assert L.aih_qmatvec(h, nat.Q4_K, W, 4, 100, X, 4096, Y, 4, 1) == nat.AIH_E_INVALID
+        assert L.aih_qmatvec(h, nat.Q4_K, W, 4, 4096, X, 4096, Y, 4, 9) == nat.AIH_E_INVALID
+        assert L.aih_qmatvec(h, nat.Q4_K, W, 4, 4096, X, 100, Y, 4, 1) == nat.AIH_E_INVALID
+        assert L.aih_qmatvec(h, nat.Q4_K, W + 8, 4, 4096, X, 4096, Y, 4, 1) == nat.AIH_E_INVALID
+        assert L.aih_qmatvec(h, nat.F32, W, 4, 4096, X, 4096, Y, 4, 1) == nat.AIH_E_UNSUPPORTED
+        assert L.aih_qmatvec(h, nat.Q4_K, W, 4, 256 * 260, X, 256 * 260, Y, 4, 1) == nat.AIH_E_LIMIT
+        assert L.aih_qmatvec(h, nat.Q8_0, W, 4, 96, X, 96, Y, 4, 1) == nat.AIH_E_LIMIT
+        device.synchronize()
+    finally:
+        for b in (wb, xb, yb):
+            b.dispose()

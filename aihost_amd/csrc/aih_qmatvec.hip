@@ -8,24 +8,28 @@
 // which writes and re-reads an F32 copy of every weight per token.  Here each
 // packed byte is read from HBM once and never materialised as F32.
 //
-// Work split.  K is cut into 64-element "units"; lane u of a workgroup owns
-// unit u of every row (a Q4_K (block, 64-group), a pair of Q8_0/Q4_0 blocks, or
-// a Q6_K (block, half, 16-column) slice).  Because that mapping is the same for
-// every row, a lane converts its 64 activations to fp16 pairs once and keeps
-// them in registers; each row then costs the lane one to four 16-byte loads of
-// packed bytes.  A workgroup is ceil(K/64 / 64) waves and handles R rows at a
-// time (all R rows' loads are issued before any arithmetic); partial sums are
-// reduced with DPP inside the wave and through LDS across waves.
+// Work split.  K is cut into 64-element "units"; lane u of a row team owns
+// unit u of every row it visits (a Q4_K (block, 64-group), a pair of Q8_0/Q4_0
+// blocks, or a Q6_K (block, half, 16-column) slice).  A team is
+// ceil(K/64 / 64) waves; a workgroup holds several teams that work on
+// different rows.  The workgroup converts the activations once into an fp16
+// "image" in LDS (every thread converts a few 16-byte pieces); per row a lane
+// then reads the 32 image dwords of its unit with eight 16-byte LDS reads.
+// Keeping the image out of registers leaves room for the packed bytes of
+// several rows per lane, so the host can size the launch such that every
+// workgroup issues all of its loads at once and the whole matrix is in
+// flight in one pass.  Partial sums are reduced with DPP inside a wave and
+// through LDS across the waves of a team.
 //
-// Arithmetic.  A 4-bit (or 6-bit, or biased 8-bit) code q is turned into the
-// fp16 value 1024 + q by OR-ing it into the mantissa of 0x6400, two codes per
-// 32-bit register, and contracted against fp16 activations with
+// Arithmetic.  A 4-bit (or 6-bit, or biased 8-bit) code q becomes the fp16
+// value 1024 + q by OR-ing it into the mantissa of 0x6400, two codes per
+// 32-bit register, and is contracted against fp16 activations with
 // v_dot2_f32_f16, which accumulates in fp32.  The 1024 * sum(x) bias (and the
-// format's own offset: -8 for Q4_0, -32 for Q6_K, +128 for biased Q8_0) is
-// removed by starting the accumulator at -(1024 + offset) * sum(x).  Codes that
-// sit in the high nibble are used in place (value 16*q) and the 1/16 goes into
-// the per-sub-block scale.  The sub-block scales/mins are applied once per
-// sub-block in fp32:
+// format offset: -8 for Q4_0, -32 for Q6_K, +128 for the biased Q8_0 code) is
+// removed by starting the accumulator at -(1024 + offset) * sum(x).  Codes in
+// a high nibble are used in place (value 16*q): the activations they meet
+// are stored pre-divided by 16.  Sub-block scales and mins are applied once
+// per sub-block in fp32:
 //   Q4_K: d*sc*S - dmin*mn*X      (S = sum q*x, X = sum x over the sub-block)
 //   Q6_K: d*sc*sum((q-32)*x)      Q8_0: d*sum(q*x)      Q4_0: d*sum((q-8)*x)
 // The only rounding beyond fp32 accumulation is that of x to fp16 (relative
@@ -39,14 +43,30 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-constexpr uint32_t kMagic = 0x64006400u;  // fp16 pair (1024, 1024)
-
 __device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
-__device__ __forceinline__ float dot2(uint32_t p, h2 x, float acc)
+__device__ __forceinline__ float dot2(uint32_t p, uint32_t x, float acc)
 {
-    return __builtin_amdgcn_fdot2(as_h2(p), x, acc, false);
+    return __builtin_amdgcn_fdot2(as_h2(p), as_h2(x), acc, false);
 }
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t b) { return (a & mask) | b; }
+// (a & mask) | b as one v_and_or_b32.  Written out because VOP3 encodings on
+// this architecture take no literal operand and read at most one scalar
+// register, so with a literal mask and a literal b the compiler emits a
+// v_and_b32 + v_or_b32 pair instead.  Here the mask travels in an SGPR and b
+// (the fp16 exponent pattern) in a VGPR.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t b)
+{
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(b));
+    return r;
+}
+// The fp16 exponent pattern (1024, 1024) in a VGPR, opaque to the optimiser so
+// it stays a register operand of v_and_or_b32.
+__device__ __forceinline__ uint32_t magic_vgpr()
+{
+    uint32_t r;
+    asm("v_mov_b32 %0, 0x64006400" : "=v"(r));
+    return r;
+}
 __device__ __forceinline__ float f16lo(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xFFFFu)); }
 __device__ __forceinline__ float f16hi(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16)); }
 __device__ __forceinline__ h2 pack2(float a, float b)
@@ -66,13 +86,34 @@ __device__ __forceinline__ T ldg(const void *p)
     return v;
 }
 
+// One prep step turns 4 consecutive activations x[src..src+3] (one 16-byte
+// load) into the fp16 pairs (x0, x2) and (x1, x3), stored at image dwords d0
+// and d0+1, and adds their sum to sum slot `slot`.  Steps with div16 feed
+// high-nibble codes: their activations are stored divided by 16 (the sum is
+// not).  A unit needs 16 steps; d0, slot and div16 depend only on the step.
+// The 32 image dwords form 8 groups of 4 that a format's dot product reads
+// one group (one 16-byte LDS read) at a time.
+struct Step {
+    int src;
+    int d0, slot;
+    bool div16;
+};
+
 // ---------------------------------------------------------------- Q4_K ----
 // Unit u: block u/4, 64-group g = u%4 -> qs bytes 32g..32g+31 of the block,
 // low nibbles are sub-block 2g (k0 + 0..31), high nibbles sub-block 2g+1
 // (k0 + 32..63), k0 = 64u.  (Element order: ComputeOps.cs:1642-1675.)
+// Image group i (i < 8): (x[k0+4i], x[k0+4i+2]), (x[k0+4i+1], x[k0+4i+3]),
+// then the same two pairs for k0+32+4i.. divided by 16.
+// Sums: 0 low sub-block, 1 high sub-block.
 struct Q4K {
     static constexpr int kRaw = 12;
-    struct X { h2 la[8], lb[8], ha[8], hb[8]; float slo, shi; };
+    static constexpr int kSums = 2;
+    __device__ static Step step(int u, int s)
+    {
+        if (s < 8) return {64 * u + 4 * s, 4 * s, 0, false};
+        return {64 * u + 32 + 4 * (s - 8), 4 * (s - 8) + 2, 1, true};
+    }
     __device__ static void load(const uint8_t *row, int u, uint32_t *raw)
     {
         const uint8_t *b = row + (u >> 2) * 144;
@@ -81,30 +122,10 @@ struct Q4K {
         raw[4] = qa.x; raw[5] = qa.y; raw[6] = qa.z; raw[7] = qa.w;
         raw[8] = qb.x; raw[9] = qb.y; raw[10] = qb.z; raw[11] = qb.w;
     }
-    __device__ static void prep(const float *x, int u, X &r)
+    template <int B, class XA>
+    __device__ static void dot(const uint32_t *raw, const XA &xa, int u, float *out)
     {
-        const float *p = x + 64 * u;
-        float lo[32], hi[32];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            f4 a = ldg<f4>(p + 4 * i), c = ldg<f4>(p + 32 + 4 * i);
-            lo[4 * i] = a.x; lo[4 * i + 1] = a.y; lo[4 * i + 2] = a.z; lo[4 * i + 3] = a.w;
-            hi[4 * i] = c.x; hi[4 * i + 1] = c.y; hi[4 * i + 2] = c.z; hi[4 * i + 3] = c.w;
-        }
-        r.slo = r.shi = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            r.la[i] = pack2(lo[4 * i], lo[4 * i + 2]);
-            r.lb[i] = pack2(lo[4 * i + 1], lo[4 * i + 3]);
-            r.ha[i] = pack2(hi[4 * i], hi[4 * i + 2]);
-            r.hb[i] = pack2(hi[4 * i + 1], hi[4 * i + 3]);
-            r.slo += hsum(r.la[i]) + hsum(r.lb[i]);
-            r.shi += hsum(r.ha[i]) + hsum(r.hb[i]);
-        }
-    }
-    template <int B>
-    __device__ static void dot(const uint32_t *raw, const X *xr, int u, float *out)
-    {
+        const uint32_t M = magic_vgpr();
         // 6-bit (scale, min) of sub-blocks 2g and 2g+1 (get_scale_min_k4,
         // QuantizationFormats.cs:157-165), branch-free per lane.
         const int g = u & 3;
@@ -112,32 +133,35 @@ struct Q4K {
         const uint32_t s0 = (g & 1) * 16;
         const uint32_t wlo = upper ? 4u : 6u, whi = upper ? 2u : 0u, moff = upper ? 4u : 0u;
         const uint32_t a_sc = upper ? raw[3] : raw[1], a_mn = upper ? raw[3] : raw[2];
-        uint32_t sc0 = __builtin_amdgcn_ubfe(a_sc, s0, wlo) | (__builtin_amdgcn_ubfe(raw[1], s0 + 6, whi) << 4);
-        uint32_t sc1 = __builtin_amdgcn_ubfe(a_sc, s0 + 8, wlo) | (__builtin_amdgcn_ubfe(raw[1], s0 + 14, whi) << 4);
-        uint32_t mn0 = __builtin_amdgcn_ubfe(a_mn, s0 + moff, wlo) | (__builtin_amdgcn_ubfe(raw[2], s0 + 6, whi) << 4);
-        uint32_t mn1 = __builtin_amdgcn_ubfe(a_mn, s0 + 8 + moff, wlo) | (__builtin_amdgcn_ubfe(raw[2], s0 + 14, whi) << 4);
+        const uint32_t sc0 = __builtin_amdgcn_ubfe(a_sc, s0, wlo) | (__builtin_amdgcn_ubfe(raw[1], s0 + 6, whi) << 4);
+        const uint32_t sc1 = __builtin_amdgcn_ubfe(a_sc, s0 + 8, wlo) | (__builtin_amdgcn_ubfe(raw[1], s0 + 14, whi) << 4);
+        const uint32_t mn0 = __builtin_amdgcn_ubfe(a_mn, s0 + moff, wlo) | (__builtin_amdgcn_ubfe(raw[2], s0 + 6, whi) << 4);
+        const uint32_t mn1 = __builtin_amdgcn_ubfe(a_mn, s0 + 8 + moff, wlo) | (__builtin_amdgcn_ubfe(raw[2], s0 + 14, whi) << 4);
         const float d = f16lo(raw[0]), dmin = f16hi(raw[0]);
-        const float c_lo = d * (float)sc0, c_hi = d * (float)sc1 * 0.0625f;
-        const float m_lo = dmin * (float)mn0, m_hi = dmin * (float)mn1;
+        const float fsc0 = (float)sc0, fsc1 = (float)sc1, fmn0 = (float)mn0, fmn1 = (float)mn1;
         float alo[B], ahi[B];
 #pragma unroll
-        for (int b = 0; b < B; ++b) { alo[b] = -1024.f * xr[b].slo; ahi[b] = -1024.f * xr[b].shi; }
+        for (int b = 0; b < B; ++b) { alo[b] = -1024.f * xa.sum(b, 0); ahi[b] = -64.f * xa.sum(b, 1); }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            uint32_t w = raw[4 + i], w8 = w >> 8;
-            uint32_t p0 = and_or(w, 0x000F000Fu, kMagic), p1 = and_or(w, 0x00F000F0u, kMagic);
-            uint32_t p2 = and_or(w8, 0x000F000Fu, kMagic), p3 = and_or(w8, 0x00F000F0u, kMagic);
+            const uint32_t w = raw[4 + i], w8 = w >> 8;
+            const uint32_t p0 = and_or(w, 0x000F000Fu, M), p1 = and_or(w, 0x00F000F0u, M);
+            const uint32_t p2 = and_or(w8, 0x000F000Fu, M), p3 = and_or(w8, 0x00F000F0u, M);
 #pragma unroll
             for (int b = 0; b < B; ++b) {
-                alo[b] = dot2(p0, xr[b].la[i], alo[b]);
-                alo[b] = dot2(p2, xr[b].lb[i], alo[b]);
-                ahi[b] = dot2(p1, xr[b].ha[i], ahi[b]);
-                ahi[b] = dot2(p3, xr[b].hb[i], ahi[b]);
+                const u4 x = xa.group(b, i);
+                alo[b] = dot2(p0, x.x, alo[b]);
+                alo[b] = dot2(p2, x.y, alo[b]);
+                ahi[b] = dot2(p1, x.z, ahi[b]);
+                ahi[b] = dot2(p3, x.w, ahi[b]);
             }
         }
 #pragma unroll
-        for (int b = 0; b < B; ++b)
-            out[b] += c_lo * alo[b] + c_hi * ahi[b] - (m_lo * xr[b].slo + m_hi * xr[b].shi);
+        for (int b = 0; b < B; ++b) {
+            const float s = fsc0 * alo[b] + fsc1 * ahi[b];
+            const float m = fmn0 * xa.sum(b, 0) + fmn1 * xa.sum(b, 1);
+            out[b] += d * s - dmin * m;
+        }
     }
 };
 
@@ -145,10 +169,12 @@ struct Q4K {
 // Unit u: blocks 2u and 2u+1 (68 bytes, 4-byte aligned), k0 = 64u.
 // Block A: d at byte 0, qs at 2..33 (realigned with alignbyte); block B: d at
 // 34..35, qs at 36..67.  Codes are biased by +128 (xor 0x80) to make them
-// unsigned before the fp16 trick.
+// unsigned before the fp16 trick.  Image group m (m < 8) holds, for i = 2m
+// and 2m+1: (x[4i], x[4i+2]), (x[4i+1], x[4i+3]).  Sums: block A, block B.
 struct Q80 {
     static constexpr int kRaw = 17;
-    struct X { h2 a[16], b[16]; float s0, s1; };  // a: (x[4i], x[4i+2]), b: (x[4i+1], x[4i+3]); i<8 block A, 8..15 block B
+    static constexpr int kSums = 2;
+    __device__ static Step step(int u, int s) { return {64 * u + 4 * s, 4 * (s >> 1) + 2 * (s & 1), s >> 3, false}; }
     __device__ static void load(const uint8_t *row, int u, uint32_t *raw)
     {
         const uint8_t *p = row + 68 * u;
@@ -159,40 +185,29 @@ struct Q80 {
         raw[12] = v3.x; raw[13] = v3.y; raw[14] = v3.z; raw[15] = v3.w;
         raw[16] = ldg<uint32_t>(p + 64);
     }
-    __device__ static void prep(const float *x, int u, X &r)
+    template <int B, class XA>
+    __device__ static void dot(const uint32_t *raw, const XA &xa, int, float *out)
     {
-        const float *p = x + 64 * u;
-        r.s0 = r.s1 = 0.f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            f4 v = ldg<f4>(p + 4 * i);
-            r.a[i] = pack2(v.x, v.z);
-            r.b[i] = pack2(v.y, v.w);
-            float s = hsum(r.a[i]) + hsum(r.b[i]);
-            if (i < 8) r.s0 += s; else r.s1 += s;
-        }
-    }
-    template <int B>
-    __device__ static void dot(const uint32_t *raw, const X *xr, int, float *out)
-    {
+        const uint32_t M = magic_vgpr();
         const float dA = f16lo(raw[0]), dB = f16hi(raw[8]);
         float aA[B], aB[B];
 #pragma unroll
-        for (int b = 0; b < B; ++b) { aA[b] = -1152.f * xr[b].s0; aB[b] = -1152.f * xr[b].s1; }
+        for (int b = 0; b < B; ++b) { aA[b] = -1152.f * xa.sum(b, 0); aB[b] = -1152.f * xa.sum(b, 1); }
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            uint32_t w = i < 8 ? __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], 2) : raw[i + 1];
-            uint32_t p0 = (w & 0x00FF00FFu) ^ 0x64806480u;
-            uint32_t p1 = ((w >> 8) & 0x00FF00FFu) ^ 0x64806480u;
+        for (int m = 0; m < 8; ++m) {
+            const int i0 = 2 * m, i1 = 2 * m + 1;
+            const uint32_t w0 = (i0 < 8 ? __builtin_amdgcn_alignbyte(raw[i0 + 1], raw[i0], 2) : raw[i0 + 1]) ^ 0x80808080u;
+            const uint32_t w1 = (i1 < 8 ? __builtin_amdgcn_alignbyte(raw[i1 + 1], raw[i1], 2) : raw[i1 + 1]) ^ 0x80808080u;
+            const uint32_t p0 = and_or(w0, 0x00FF00FFu, M), p1 = and_or(w0 >> 8, 0x00FF00FFu, M);
+            const uint32_t q0 = and_or(w1, 0x00FF00FFu, M), q1 = and_or(w1 >> 8, 0x00FF00FFu, M);
 #pragma unroll
             for (int b = 0; b < B; ++b) {
-                if (i < 8) {
-                    aA[b] = dot2(p0, xr[b].a[i], aA[b]);
-                    aA[b] = dot2(p1, xr[b].b[i], aA[b]);
-                } else {
-                    aB[b] = dot2(p0, xr[b].a[i], aB[b]);
-                    aB[b] = dot2(p1, xr[b].b[i], aB[b]);
-                }
+                const u4 x = xa.group(b, m);
+                float &a = m < 4 ? aA[b] : aB[b];
+                a = dot2(p0, x.x, a);
+                a = dot2(p1, x.y, a);
+                a = dot2(q0, x.z, a);
+                a = dot2(q1, x.w, a);
             }
         }
 #pragma unroll
@@ -203,9 +218,18 @@ struct Q80 {
 // ---------------------------------------------------------------- Q4_0 ----
 // Unit u: blocks 2u and 2u+1 (36 bytes, 4-byte aligned), k0 = 64u.  In each
 // block qs[j] holds element j (low nibble) and j+16 (high nibble).
+// Image group 4*blk + i (blk < 2, i < 4): (x[4i], x[4i+2]), (x[4i+1],
+// x[4i+3]) of the block, then the same for elements 16+4i.. divided by 16.
+// Sums: blk low half, then 2+blk high half.
 struct Q40 {
     static constexpr int kRaw = 9;
-    struct X { h2 la[8], lb[8], ha[8], hb[8]; float slo[2], shi[2]; };  // index 4*blk + i
+    static constexpr int kSums = 4;
+    __device__ static Step step(int u, int s)
+    {
+        const int blk = s >> 3, r = s & 7;
+        if (r < 4) return {64 * u + 32 * blk + 4 * r, 4 * (4 * blk + r), blk, false};
+        return {64 * u + 32 * blk + 16 + 4 * (r - 4), 4 * (4 * blk + r - 4) + 2, 2 + blk, true};
+    }
     __device__ static void load(const uint8_t *row, int u, uint32_t *raw)
     {
         const uint8_t *p = row + 36 * u;
@@ -214,49 +238,35 @@ struct Q40 {
         raw[4] = v1.x; raw[5] = v1.y; raw[6] = v1.z; raw[7] = v1.w;
         raw[8] = ldg<uint32_t>(p + 32);
     }
-    __device__ static void prep(const float *x, int u, X &r)
+    template <int B, class XA>
+    __device__ static void dot(const uint32_t *raw, const XA &xa, int, float *out)
     {
-#pragma unroll
-        for (int blk = 0; blk < 2; ++blk) {
-            const float *p = x + 64 * u + 32 * blk;
-            r.slo[blk] = r.shi[blk] = 0.f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                f4 lo = ldg<f4>(p + 4 * i), hi = ldg<f4>(p + 16 + 4 * i);
-                r.la[4 * blk + i] = pack2(lo.x, lo.z);
-                r.lb[4 * blk + i] = pack2(lo.y, lo.w);
-                r.ha[4 * blk + i] = pack2(hi.x, hi.z);
-                r.hb[4 * blk + i] = pack2(hi.y, hi.w);
-                r.slo[blk] += hsum(r.la[4 * blk + i]) + hsum(r.lb[4 * blk + i]);
-                r.shi[blk] += hsum(r.ha[4 * blk + i]) + hsum(r.hb[4 * blk + i]);
-            }
-        }
-    }
-    template <int B>
-    __device__ static void dot(const uint32_t *raw, const X *xr, int, float *out)
-    {
+        const uint32_t M = magic_vgpr();
         const float d[2] = {f16lo(raw[0]), f16hi(raw[4])};
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
-            float alo[B], ahi[B];
+            float a[B];
+            // sum((q-8)*x) over the block: low-nibble codes meet x, high-nibble
+            // codes (value 16q) meet x/16; the bias of both halves is removed here.
 #pragma unroll
-            for (int b = 0; b < B; ++b) { alo[b] = -1032.f * xr[b].slo[blk]; ahi[b] = -1152.f * xr[b].shi[blk]; }
+            for (int b = 0; b < B; ++b) a[b] = -1032.f * xa.sum(b, blk) - 72.f * xa.sum(b, 2 + blk);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                uint32_t w = blk == 0 ? __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], 2) : raw[5 + i];
-                uint32_t w8 = w >> 8;
-                uint32_t p0 = and_or(w, 0x000F000Fu, kMagic), p1 = and_or(w, 0x00F000F0u, kMagic);
-                uint32_t p2 = and_or(w8, 0x000F000Fu, kMagic), p3 = and_or(w8, 0x00F000F0u, kMagic);
+                const uint32_t w = blk == 0 ? __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], 2) : raw[5 + i];
+                const uint32_t w8 = w >> 8;
+                const uint32_t p0 = and_or(w, 0x000F000Fu, M), p1 = and_or(w, 0x00F000F0u, M);
+                const uint32_t p2 = and_or(w8, 0x000F000Fu, M), p3 = and_or(w8, 0x00F000F0u, M);
 #pragma unroll
                 for (int b = 0; b < B; ++b) {
-                    alo[b] = dot2(p0, xr[b].la[4 * blk + i], alo[b]);
-                    alo[b] = dot2(p2, xr[b].lb[4 * blk + i], alo[b]);
-                    ahi[b] = dot2(p1, xr[b].ha[4 * blk + i], ahi[b]);
-                    ahi[b] = dot2(p3, xr[b].hb[4 * blk + i], ahi[b]);
+                    const u4 x = xa.group(b, 4 * blk + i);
+                    a[b] = dot2(p0, x.x, a[b]);
+                    a[b] = dot2(p2, x.y, a[b]);
+                    a[b] = dot2(p1, x.z, a[b]);
+                    a[b] = dot2(p3, x.w, a[b]);
                 }
             }
 #pragma unroll
-            for (int b = 0; b < B; ++b) out[b] += d[blk] * (alo[b] + 0.0625f * ahi[b]);
+            for (int b = 0; b < B; ++b) out[b] += d[blk] * a[b];
         }
     }
 };
@@ -267,9 +277,18 @@ struct Q40 {
 // and 3) and qh[32h+16t .. +15] (high 2 bits of all four quarters), i.e.
 // elements 128h + 32*quarter + 16t + i, i < 16 (ComputeOps.cs:1748-1771).
 // Each quarter's 16 elements form one sub-block with an int8 scale.
+// Image group 2m + (q >> 1) (m < 4) holds quarters q = 0, 1 (or 2, 3):
+// (x[4m], x[4m+2]), (x[4m+1], x[4m+3]) of each, quarters 2 and 3 divided by
+// 16.  Sums: one per quarter.
 struct Q6K {
     static constexpr int kRaw = 15;
-    struct X { h2 a[4][8]; float s[4]; };  // per quarter: i-th pair ((x[4m], x[4m+2]) for i=2m, (x[4m+1], x[4m+3]) for i=2m+1)
+    static constexpr int kSums = 4;
+    __device__ static Step step(int u, int s)
+    {
+        const int q = s >> 2, m = s & 3;
+        const int base = (u >> 2) * 256 + 128 * ((u >> 1) & 1) + 16 * (u & 1);
+        return {base + 32 * q + 4 * m, 4 * (2 * m + (q >> 1)) + 2 * (q & 1), q, q >= 2};
+    }
     __device__ static void load(const uint8_t *row, int u, uint32_t *raw)
     {
         const uint8_t *b = row + (u >> 2) * 210;
@@ -283,36 +302,22 @@ struct Q6K {
         raw[12] = (uint32_t)sc; raw[13] = (uint32_t)(sc >> 32);
         raw[14] = ldg<uint16_t>(b + 208);
     }
-    __device__ static void prep(const float *x, int u, X &r)
+    template <int B, class XA>
+    __device__ static void dot(const uint32_t *raw, const XA &xa, int u, float *out)
     {
-        const int h = (u >> 1) & 1, t = u & 1;
-        const float *p = x + (u >> 2) * 256 + 128 * h + 16 * t;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            r.s[q] = 0.f;
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                f4 v = ldg<f4>(p + 32 * q + 4 * m);
-                r.a[q][2 * m] = pack2(v.x, v.z);
-                r.a[q][2 * m + 1] = pack2(v.y, v.w);
-                r.s[q] += hsum(r.a[q][2 * m]) + hsum(r.a[q][2 * m + 1]);
-            }
-        }
-    }
-    template <int B>
-    __device__ static void dot(const uint32_t *raw, const X *xr, int u, float *out)
-    {
+        const uint32_t M = magic_vgpr();
         const uint32_t t8 = (u & 1) * 8;
+        // int8 sub-block scales (signed extract, then signed conversion)
         const float sc0 = (float)(int)__builtin_amdgcn_sbfe((int)raw[12], t8, 8);
         const float sc1 = (float)(int)__builtin_amdgcn_sbfe((int)raw[12], t8 + 16, 8);
-        const float sc2 = (float)(int)__builtin_amdgcn_sbfe((int)raw[13], t8, 8) * 0.0625f;
-        const float sc3 = (float)(int)__builtin_amdgcn_sbfe((int)raw[13], t8 + 16, 8) * 0.0625f;
+        const float sc2 = (float)(int)__builtin_amdgcn_sbfe((int)raw[13], t8, 8);
+        const float sc3 = (float)(int)__builtin_amdgcn_sbfe((int)raw[13], t8 + 16, 8);
         const float d = f16lo(raw[14]);
         float a0[B], a1[B], a2[B], a3[B];
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            a0[b] = -1056.f * xr[b].s[0]; a1[b] = -1056.f * xr[b].s[1];
-            a2[b] = -1536.f * xr[b].s[2]; a3[b] = -1536.f * xr[b].s[3];
+            a0[b] = -1056.f * xa.sum(b, 0); a1[b] = -1056.f * xa.sum(b, 1);
+            a2[b] = -96.f * xa.sum(b, 2);   a3[b] = -96.f * xa.sum(b, 3);
         }
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
@@ -320,26 +325,69 @@ struct Q6K {
             const uint32_t w8 = w >> 8, v8 = v >> 8, hb4 = hb << 4, hb2 = hb << 2, hr4 = hb >> 4, hr6 = hb >> 6;
             // quarter 0: low nibble of ql[A] + qh bits 0-1; quarter 2: high nibble of ql[A] + bits 4-5 (x16)
             // quarter 1: low nibble of ql[B] + qh bits 2-3; quarter 3: high nibble of ql[B] + bits 6-7 (x16)
-            const uint32_t q0e = and_or(hb4, 0x00300030u, and_or(w, 0x000F000Fu, kMagic));
-            const uint32_t q2e = and_or(hb4, 0x03000300u, and_or(w, 0x00F000F0u, kMagic));
-            const uint32_t q1e = and_or(hb2, 0x00300030u, and_or(v, 0x000F000Fu, kMagic));
-            const uint32_t q3e = and_or(hb2, 0x03000300u, and_or(v, 0x00F000F0u, kMagic));
-            const uint32_t q0o = and_or(hr4, 0x00300030u, and_or(w8, 0x000F000Fu, kMagic));
-            const uint32_t q2o = and_or(hr4, 0x03000300u, and_or(w8, 0x00F000F0u, kMagic));
-            const uint32_t q1o = and_or(hr6, 0x00300030u, and_or(v8, 0x000F000Fu, kMagic));
-            const uint32_t q3o = and_or(hr6, 0x03000300u, and_or(v8, 0x00F000F0u, kMagic));
+            const uint32_t q0e = and_or(hb4, 0x00300030u, and_or(w, 0x000F000Fu, M));
+            const uint32_t q2e = and_or(hb4, 0x03000300u, and_or(w, 0x00F000F0u, M));
+            const uint32_t q1e = and_or(hb2, 0x00300030u, and_or(v, 0x000F000Fu, M));
+            const uint32_t q3e = and_or(hb2, 0x03000300u, and_or(v, 0x00F000F0u, M));
+            const uint32_t q0o = and_or(hr4, 0x00300030u, and_or(w8, 0x000F000Fu, M));
+            const uint32_t q2o = and_or(hr4, 0x03000300u, and_or(w8, 0x00F000F0u, M));
+            const uint32_t q1o = and_or(hr6, 0x00300030u, and_or(v8, 0x000F000Fu, M));
+            const uint32_t q3o = and_or(hr6, 0x03000300u, and_or(v8, 0x00F000F0u, M));
 #pragma unroll
             for (int b = 0; b < B; ++b) {
-                a0[b] = dot2(q0o, xr[b].a[0][2 * m + 1], dot2(q0e, xr[b].a[0][2 * m], a0[b]));
-                a1[b] = dot2(q1o, xr[b].a[1][2 * m + 1], dot2(q1e, xr[b].a[1][2 * m], a1[b]));
-                a2[b] = dot2(q2o, xr[b].a[2][2 * m + 1], dot2(q2e, xr[b].a[2][2 * m], a2[b]));
-                a3[b] = dot2(q3o, xr[b].a[3][2 * m + 1], dot2(q3e, xr[b].a[3][2 * m], a3[b]));
+                const u4 xl = xa.group(b, 2 * m), xh = xa.group(b, 2 * m + 1);
+                a0[b] = dot2(q0o, xl.y, dot2(q0e, xl.x, a0[b]));
+                a1[b] = dot2(q1o, xl.w, dot2(q1e, xl.z, a1[b]));
+                a2[b] = dot2(q2o, xh.y, dot2(q2e, xh.x, a2[b]));
+                a3[b] = dot2(q3o, xh.w, dot2(q3e, xh.z, a3[b]));
             }
         }
 #pragma unroll
         for (int b = 0; b < B; ++b)
-            out[b] += d * (sc0 * a0[b] + sc1 * a1[b] + (sc2 * a2[b] + sc3 * a3[b]));
+            out[b] += d * (sc0 * a0[b] + sc1 * a1[b] + sc2 * a2[b] + sc3 * a3[b]);
     }
+};
+
+// Convert one step's 4 activations: two fp16 pairs and their (unscaled) sum.
+__device__ __forceinline__ float convert_step(f4 v, bool div16, uint32_t &p0, uint32_t &p1)
+{
+    const float f = div16 ? 0.0625f : 1.0f;
+    const h2 a = pack2(v.x * f, v.z * f), c = pack2(v.y * f, v.w * f);
+    p0 = __builtin_bit_cast(uint32_t, a);
+    p1 = __builtin_bit_cast(uint32_t, c);
+    const float s = hsum(a) + hsum(c);
+    return div16 ? 16.f * s : s;
+}
+
+// Activation image of one unit in registers (used when a workgroup is a
+// single row team and nothing is shared).
+template <int B, int S>
+struct XRegs {
+    u4 g[B][8];
+    float s[B][S];
+    __device__ __forceinline__ u4 group(int b, int i) const { return g[b][i]; }
+    __device__ __forceinline__ float sum(int b, int k) const { return s[b][k]; }
+};
+
+// 16 bytes of LDS written as dwords, read through the same dword type
+// (memcpy keeps the access type-neutral: reading dword-written memory
+// through a vector type would let the optimiser treat the two as unrelated).
+__device__ __forceinline__ u4 lds_ld16(const uint32_t *p)
+{
+    u4 v;
+    __builtin_memcpy(&v, __builtin_assume_aligned(p, 16), 16);
+    return v;
+}
+
+// Activation image of one unit in LDS (kImg dwords per unit and column);
+// the sums are read once into registers.
+constexpr int kImg = 52;   // 32 image dwords + 16 step sums + 4 pad
+template <int B, int S>
+struct XLds {
+    const uint32_t *img[B];
+    float s[B][S];
+    __device__ __forceinline__ u4 group(int b, int i) const { return lds_ld16(img[b] + 4 * i); }
+    __device__ __forceinline__ float sum(int b, int k) const { return s[b][k]; }
 };
 
 // Sum over the 64 lanes of a wave; the total lands in lane 63.
@@ -354,92 +402,234 @@ __device__ __forceinline__ float wave_sum_to_lane63(float v)
     return v;
 }
 
-template <class T, int B, int R, int MAXT>
+// Launch geometry shared by host and device.
+struct Geom {
+    int units;     // K / 64
+    int wr;        // waves per row team = ceil(units / 64)
+    int teams;     // row teams per workgroup (1, 2, 4 or 8)
+};
+
+// A workgroup is TEAMS * wr waves; in row group c (c = blockIdx.x, then
+// += gridDim.x) team t handles the R consecutive rows (c*TEAMS + t)*R + j.
+// All R rows' loads are issued before the first is computed; the host picks
+// R so that the whole matrix is covered in about one pass of the grid.
+//
+// No load sits behind a data-dependent branch: row indices are clamped into
+// the matrix instead (surplus loads re-read the last row and are never used),
+// so the compiler can count outstanding loads exactly and wait only for the
+// ones a computation needs.  Loads complete in issue order, so the activation
+// loads are issued before the weight loads.  W is deliberately not
+// __restrict__: that would let the compiler sink the weight loads below the
+// LDS barrier, leaving HBM idle during the activation exchange.
+template <class T, int B, int R, int TEAMS, int MAXT, bool ONESHOT>
 __global__ void __launch_bounds__(MAXT)
-qmatvec_kernel(const uint8_t *__restrict__ W, int64_t N, int64_t row_bytes, int units,
+qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
                const float *__restrict__ X, int64_t ldx, float *__restrict__ Y, int64_t ldy)
 {
+    extern __shared__ uint32_t xs[];
     __shared__ float red[MAXT / 64][R * B];
+
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
-    const bool active = tid < units;
-    const int u = active ? tid : 0;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int team_threads = geo.wr * 64;
+    const int team = TEAMS == 1 ? 0 : tid / team_threads;
+    const int ut = tid - team * team_threads;   // unit index within the team
+    const bool active = ut < geo.units;
+    const int u = active ? ut : 0;
+    const int64_t ngroups = (N + (int64_t)TEAMS * R - 1) / ((int64_t)TEAMS * R);
+    const int64_t g = gridDim.x;
+    const int64_t c0 = blockIdx.x;
 
-    typename T::X xr[B];
+    uint32_t raw[R][T::kRaw];
+    auto load_rows = [&](int64_t c) {
 #pragma unroll
-    for (int b = 0; b < B; ++b) T::prep(X + b * ldx, u, xr[b]);
-
-    const int64_t nchunks = (N + R - 1) / R;
-    for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
-        const int64_t n0 = c * R;
-        uint32_t raw[R][T::kRaw];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            int64_t n = n0 + r < N ? n0 + r : N - 1;
-            T::load(W + n * row_bytes, u, raw[r]);
+        for (int j = 0; j < R; ++j) {
+            int64_t n = (c * TEAMS + team) * R + j;
+            n = n < N ? n : N - 1;
+            T::load(W + n * row_bytes, u, raw[j]);
         }
+    };
+
+    // The 16 conversion steps of every unit are spread over the teams; a
+    // single team converts all 16 itself.
+    constexpr int NST = 16 / TEAMS;
+    f4 xv[B][NST];
+#pragma unroll
+    for (int b = 0; b < B; ++b)
+#pragma unroll
+        for (int k = 0; k < NST; ++k) xv[b][k] = ldg<f4>(X + b * ldx + T::step(u, team * NST + k).src);
+    load_rows(c0);
+    // keep the weight loads here, in flight during the conversion below
+    __builtin_amdgcn_sched_barrier(0);
+
+    typedef typename std::conditional<TEAMS == 1, XRegs<B, T::kSums>, XLds<B, T::kSums>>::type XA;
+    XA xa;
+    if constexpr (TEAMS == 1) {
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            uint32_t img[32];
+#pragma unroll
+            for (int k = 0; k < T::kSums; ++k) xa.s[b][k] = 0.f;
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                const Step st = T::step(u, s);
+                xa.s[b][st.slot] += convert_step(xv[b][s], st.div16, img[st.d0], img[st.d0 + 1]);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xa.g[b][i] = u4{img[4 * i], img[4 * i + 1], img[4 * i + 2], img[4 * i + 3]};
+        }
+    } else {
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            uint32_t *img = xs + ((size_t)b * team_threads + ut) * kImg;
+#pragma unroll
+            for (int k = 0; k < NST; ++k) {
+                const int s = team * NST + k;
+                const Step st = T::step(u, s);
+                uint32_t p0, p1;
+                const float sum = convert_step(xv[b][k], st.div16, p0, p1);
+                img[st.d0] = p0;
+                img[st.d0 + 1] = p1;
+                img[32 + s] = __builtin_bit_cast(uint32_t, sum);
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            xa.img[b] = xs + ((size_t)b * team_threads + ut) * kImg;
+#pragma unroll
+            for (int k = 0; k < T::kSums; ++k) xa.s[b][k] = 0.f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                // Copy the elements into scalars before reinterpreting them:
+                // hipcc resolves __builtin_bit_cast applied directly to an
+                // ext_vector element (v.y) to element 0 of the vector.
+                const u4 v = lds_ld16(xa.img[b] + 32 + 4 * q);
+                const uint32_t e0 = v.x, e1 = v.y, e2 = v.z, e3 = v.w;
+                xa.s[b][T::step(u, 4 * q).slot] += __uint_as_float(e0);
+                xa.s[b][T::step(u, 4 * q + 1).slot] += __uint_as_float(e1);
+                xa.s[b][T::step(u, 4 * q + 2).slot] += __uint_as_float(e2);
+                xa.s[b][T::step(u, 4 * q + 3).slot] += __uint_as_float(e3);
+            }
+        }
+    }
+
+    // ONESHOT: the grid holds exactly one row group per workgroup, so the
+    // loop body runs once and never reloads.
+    for (int64_t c = c0; c < ngroups; c += g) {
+        if (!ONESHOT && c != c0) load_rows(c);
+        const int64_t n0 = (c * TEAMS + team) * R;
         float acc[R][B];
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
+        for (int j = 0; j < R; ++j) {
 #pragma unroll
-            for (int b = 0; b < B; ++b) acc[r][b] = 0.f;
-            T::template dot<B>(raw[r], xr, u, acc[r]);
+            for (int b = 0; b < B; ++b) acc[j][b] = 0.f;
+            T::template dot<B>(raw[j], xa, u, acc[j]);
+            // rows one after another: interleaving them gains nothing (each
+            // waits for its own loads) and would multiply live registers
+            __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
+        for (int j = 0; j < R; ++j) {
 #pragma unroll
             for (int b = 0; b < B; ++b) {
-                float v = wave_sum_to_lane63(active ? acc[r][b] : 0.f);
-                if (nwaves == 1) {
-                    if (lane == 63 && n0 + r < N) Y[b * ldy + n0 + r] = v;
+                const float v = wave_sum_to_lane63(active ? acc[j][b] : 0.f);
+                if (geo.wr == 1) {
+                    if (lane == 63 && n0 + j < N) Y[b * ldy + n0 + j] = v;
                 } else if (lane == 63) {
-                    red[wave][r * B + b] = v;
+                    red[wave][j * B + b] = v;
                 }
             }
         }
-        if (nwaves > 1) {
+        if (geo.wr > 1) {
             __syncthreads();
-            if (tid < R * B) {
-                const int r = tid / B, b = tid % B;
+            if (ut < R * B) {
+                const int j = ut / B, b = ut % B;
                 float s = 0.f;
-                for (int w = 0; w < nwaves; ++w) s += red[w][tid];
-                if (n0 + r < N) Y[b * ldy + n0 + r] = s;
+                for (int w = 0; w < geo.wr; ++w) s += red[team * geo.wr + w][ut];
+                if (n0 + j < N) Y[b * ldy + n0 + j] = s;
             }
             __syncthreads();
         }
+        if (ONESHOT) break;
     }
 }
 
-template <class T, int B, int R, int MAXT>
-int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t row_bytes, int units,
-           const float *X, int64_t ldx, float *Y, int64_t ldy)
+template <class T, int B, int R, int TEAMS, int MAXT>
+int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
+           const float *X, int64_t ldx, float *Y, int64_t ldy, int64_t grid_cap)
 {
-    const int threads = ((units + 63) / 64) * 64;
-    const int64_t nchunks = (N + R - 1) / R;
-    const int64_t cap = (int64_t)1 << 30;
-    const unsigned grid = (unsigned)(nchunks < cap ? nchunks : cap);
-    hipLaunchKernelGGL((qmatvec_kernel<T, B, R, MAXT>), dim3(grid), dim3(threads), 0, ctx->stream,
-                       W, N, row_bytes, units, X, ldx, Y, ldy);
+    const int threads = TEAMS * geo.wr * 64;
+    const size_t lds = TEAMS > 1 ? (size_t)B * kImg * geo.wr * 64 * 4 : 0;
+    const int64_t ngroups = (N + (int64_t)TEAMS * R - 1) / ((int64_t)TEAMS * R);
+    if (ngroups <= grid_cap)
+        hipLaunchKernelGGL((qmatvec_kernel<T, B, R, TEAMS, MAXT, true>), dim3((unsigned)ngroups), dim3(threads),
+                           lds, ctx->stream, W, N, row_bytes, geo, X, ldx, Y, ldy);
+    else
+        hipLaunchKernelGGL((qmatvec_kernel<T, B, R, TEAMS, MAXT, false>), dim3((unsigned)grid_cap), dim3(threads),
+                           lds, ctx->stream, W, N, row_bytes, geo, X, ldx, Y, ldy);
     return aih_launch_status();
+}
+
+Geom make_geom(int64_t K)
+{
+    Geom g;
+    g.units = (int)(K / 64);
+    g.wr = (g.units + 63) / 64;
+    g.teams = g.wr == 1 ? 8 : g.wr == 2 ? 4 : g.wr <= 4 ? 2 : 1;
+    return g;
+}
+
+// Rows per team per iteration.  One row per team with three resident
+// workgroups per CU measured fastest on MI355X for the 14336 x 4096 Q4_K
+// matvec (several rows per team raise register use and lower occupancy more
+// than they add loads in flight); R stays a template parameter for tuning.
+int pick_rows(int64_t, int, int64_t) { return 1; }
+
+template <class T, int B, int TEAMS>
+int launch_r(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
+             const float *X, int64_t ldx, float *Y, int64_t ldy, int64_t cap)
+{
+    switch (pick_rows(N, TEAMS, cap)) {
+    case 1: return launch<T, B, 1, TEAMS, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, cap);
+    case 2: return launch<T, B, 2, TEAMS, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, cap);
+    default: return launch<T, B, 4, TEAMS, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, cap);
+    }
+}
+
+// One pass over W for `two` ? 2 : 1 activation columns.
+template <class T>
+int launch_pass(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
+                const float *X, int64_t ldx, float *Y, int64_t ldy, bool two, int64_t cap)
+{
+    switch (geo.teams) {
+    case 8: return two ? launch_r<T, 2, 8>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, cap)
+                       : launch_r<T, 1, 8>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, cap);
+    case 4: return two ? launch_r<T, 2, 4>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, cap)
+                       : launch_r<T, 1, 4>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, cap);
+    case 2: return two ? launch_r<T, 2, 2>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, cap)
+                       : launch_r<T, 1, 2>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, cap);
+    default: {  // one team of up to 16 waves: one column per pass within 128 VGPRs
+        int rc = launch<T, 1, 1, 1, 1024>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, cap);
+        if (!rc && two) rc = launch<T, 1, 1, 1, 1024>(ctx, W, N, row_bytes, geo, X + ldx, ldx, Y + ldy, ldy, cap);
+        return rc;
+    }
+    }
 }
 
 template <class T>
 int launch_type(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
                 const float *X, int64_t ldx, float *Y, int64_t ldy, int batch)
 {
-    const int units = (int)(K / 64);
+    const Geom geo = make_geom(K);
+    const int threads = geo.teams * geo.wr * 64;
+    // Three workgroups of up to eight waves per CU.
+    const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    const int64_t cap = cus * (threads <= 512 ? 3 : 1);
     // Columns are processed in passes of at most two; each pass re-reads W.
     for (int b0 = 0; b0 < batch; b0 += 2) {
-        const float *xb = X + b0 * ldx;
-        float *yb = Y + b0 * ldy;
-        const bool two = batch - b0 >= 2;
-        int rc;
-        if (units <= 256)
-            rc = two ? launch<T, 2, 4, 256>(ctx, W, N, row_bytes, units, xb, ldx, yb, ldy)
-                     : launch<T, 1, 4, 256>(ctx, W, N, row_bytes, units, xb, ldx, yb, ldy);
-        else  // up to 16 waves per workgroup: fewer rows in flight to stay within 128 VGPRs
-            rc = two ? launch<T, 2, 1, 1024>(ctx, W, N, row_bytes, units, xb, ldx, yb, ldy)
-                     : launch<T, 1, 1, 1024>(ctx, W, N, row_bytes, units, xb, ldx, yb, ldy);
+        const int rc = launch_pass<T>(ctx, W, N, row_bytes, geo, X + b0 * ldx, ldx, Y + b0 * ldy, ldy,
+                                      batch - b0 >= 2, cap);
         if (rc) return rc;
     }
     return AIH_OK;
@@ -450,8 +640,8 @@ int launch_type(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t ro
 int aih_launch_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
                        const float *X, int64_t ldx, float *Y, int64_t ldy, int batch)
 {
-    // Every kernel reads 64-element units: K must be a multiple of 64, and the
-    // workgroup (one lane per unit) holds at most 1024 lanes.
+    // Every kernel reads 64-element units: K must be a multiple of 64, and a
+    // row team (one lane per unit) holds at most 1024 lanes.
     if (K % 64 != 0) return AIH_E_LIMIT;
     if (K / 64 > 1024) return AIH_E_LIMIT;
     const uintptr_t wa = reinterpret_cast<uintptr_t>(W);

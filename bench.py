@@ -134,6 +134,14 @@ def main():
     dev = C.HipComputeDevice(0)
     n, k = 14336, 4096
     main_b = MatvecBench(dev, nat.Q4_K, n, k, 1)
+    # Untimed copy of one weight copy: a kernel of known traffic, so that a
+    # counter run (FETCH_SIZE / WRITE_SIZE) over this script can be scaled by
+    # what the counters read for it.
+    probe = dev.create_buffer(main_b.packed.nbytes)
+    nat.check(nat.lib().aih_memcpy_d2d(dev.handle, probe.get_pointer(), main_b.w[0].get_pointer(),
+                                       main_b.packed.nbytes), "aih_memcpy_d2d")
+    dev.synchronize()
+    probe.dispose()
     ms_step, ms_kernel = main_b.time(args.steps, args.warmup)
     nbytes = algorithmic_bytes(nat.Q4_K, n, k, 1)
     gbs = nbytes / (ms_step * 1e-3) / 1e9

@@ -12,14 +12,14 @@
 // unit u of every row it visits (a Q4_K (block, 64-group), a pair of Q8_0/Q4_0
 // blocks, or a Q6_K (block, half, 16-column) slice).  A team is
 // ceil(K/64 / 64) waves; a workgroup holds several teams that work on
-// different rows.  The workgroup converts the activations once into an fp16
-// "image" in LDS (every thread converts a few 16-byte pieces); per row a lane
-// then reads the 32 image dwords of its unit with eight 16-byte LDS reads.
-// Keeping the image out of registers leaves room for the packed bytes of
-// several rows per lane, so the host can size the launch such that every
-// workgroup issues all of its loads at once and the whole matrix is in
-// flight in one pass.  Partial sums are reduced with DPP inside a wave and
-// through LDS across the waves of a team.
+// different rows, and the host launches one workgroup per CU.  The workgroup
+// converts the activations once into an fp16 "image" in LDS (every thread
+// converts a few 16-byte pieces); per row a lane reads the 32 image dwords of
+// its unit with eight conflict-free 16-byte LDS reads.  Each wave walks its
+// rows with a two-deep register pipeline (the next row's packed bytes are in
+// flight while the current row is computed).  Partial sums are reduced with
+// DPP inside a wave and through LDS across the waves of a team; row results
+// stay in registers until the end of the launch.
 //
 // Arithmetic.  A 4-bit (or 6-bit, or biased 8-bit) code q becomes the fp16
 // value 1024 + q by OR-ing it into the mantissa of 0x6400, two codes per
@@ -369,24 +369,20 @@ struct XRegs {
     __device__ __forceinline__ float sum(int b, int k) const { return s[b][k]; }
 };
 
-// 16 bytes of LDS written as dwords, read through the same dword type
-// (memcpy keeps the access type-neutral: reading dword-written memory
-// through a vector type would let the optimiser treat the two as unrelated).
-__device__ __forceinline__ u4 lds_ld16(const uint32_t *p)
-{
-    u4 v;
-    __builtin_memcpy(&v, __builtin_assume_aligned(p, 16), 16);
-    return v;
-}
-
-// Activation image of one unit in LDS (kImg dwords per unit and column);
-// the sums are read once into registers.
-constexpr int kImg = 52;   // 32 image dwords + 16 step sums + 4 pad
+// Activation image in LDS, shared by the teams of a workgroup (one entry per
+// unit, i.e. per lane of a team).  Laid out unit-minor so that the lanes of a
+// wave touch consecutive LDS words: group i (16 bytes) of unit u for column b
+// is entry (b*8 + i)*tt + u of the group array, and step sum s is entry
+// (b*16 + s)*tt + u of the sum array that follows (tt = lanes per team).  A
+// unit-major layout (each lane's image contiguous) would put the lanes of a
+// read on a few banks and serialise every LDS access several-fold.
+constexpr int kLdsBytesPerUnit = 8 * 16 + 16 * 4;   // groups + step sums, per column
 template <int B, int S>
 struct XLds {
-    const uint32_t *img[B];
+    const u4 *grp;   // group 0 of column 0 of this lane's unit
+    int tt;          // lanes per team
     float s[B][S];
-    __device__ __forceinline__ u4 group(int b, int i) const { return lds_ld16(img[b] + 4 * i); }
+    __device__ __forceinline__ u4 group(int b, int i) const { return grp[(b * 8 + i) * tt]; }
     __device__ __forceinline__ float sum(int b, int k) const { return s[b][k]; }
 };
 
@@ -409,45 +405,43 @@ struct Geom {
     int teams;     // row teams per workgroup (1, 2, 4 or 8)
 };
 
-// A workgroup is TEAMS * wr waves; in row group c (c = blockIdx.x, then
-// += gridDim.x) team t handles the R consecutive rows (c*TEAMS + t)*R + j.
-// All R rows' loads are issued before the first is computed; the host picks
-// R so that the whole matrix is covered in about one pass of the grid.
+// A workgroup is TEAMS row teams of geo.wr waves (ONEWAVE: geo.wr == 1).
+// Team t of workgroup w visits the row groups c = w, w + gridDim.x, ... and
+// computes row c*TEAMS + t of each.
 //
-// No load sits behind a data-dependent branch: row indices are clamped into
-// the matrix instead (surplus loads re-read the last row and are never used),
-// so the compiler can count outstanding loads exactly and wait only for the
-// ones a computation needs.  Loads complete in issue order, so the activation
-// loads are issued before the weight loads.  W is deliberately not
-// __restrict__: that would let the compiler sink the weight loads below the
-// LDS barrier, leaving HBM idle during the activation exchange.
-template <class T, int B, int R, int TEAMS, int MAXT, bool ONESHOT>
+// Software pipeline: before a row is computed, the packed bytes of the
+// team's next row are loaded into the other of two register buffers, so a
+// wave always has one row of loads in flight while it computes.  The loop is
+// unrolled twice so that each buffer keeps fixed registers.
+//
+// No load sits behind a data-dependent branch (the compiler could then no
+// longer count outstanding loads and would wait for all of them): after the
+// last row group the prefetch re-reads the team's current row, which is
+// still in L2.  Loads complete in issue order, so waiting for the current
+// row leaves the prefetch in flight; the activation loads are issued first.
+// W is deliberately not __restrict__: that would let the compiler sink the
+// first weight loads below the LDS barrier of the activation exchange.
+template <class T, int B, int TEAMS, bool ONEWAVE, int MAXT>
 __global__ void __launch_bounds__(MAXT)
 qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
                const float *__restrict__ X, int64_t ldx, float *__restrict__ Y, int64_t ldy)
 {
-    extern __shared__ uint32_t xs[];
-    __shared__ float red[MAXT / 64][R * B];
+    extern __shared__ __align__(16) uint32_t xs[];
+    __shared__ float red[2][MAXT / 64][B];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int team_threads = geo.wr * 64;
+    const int wr = ONEWAVE ? 1 : geo.wr;
+    const int team_threads = wr * 64;
     const int team = TEAMS == 1 ? 0 : tid / team_threads;
     const int ut = tid - team * team_threads;   // unit index within the team
     const bool active = ut < geo.units;
     const int u = active ? ut : 0;
-    const int64_t ngroups = (N + (int64_t)TEAMS * R - 1) / ((int64_t)TEAMS * R);
+    const int64_t ngroups = (N + TEAMS - 1) / TEAMS;
     const int64_t g = gridDim.x;
-    const int64_t c0 = blockIdx.x;
-
-    uint32_t raw[R][T::kRaw];
-    auto load_rows = [&](int64_t c) {
-#pragma unroll
-        for (int j = 0; j < R; ++j) {
-            int64_t n = (c * TEAMS + team) * R + j;
-            n = n < N ? n : N - 1;
-            T::load(W + n * row_bytes, u, raw[j]);
-        }
+    auto row_of = [&](int64_t c) {
+        const int64_t n = c * TEAMS + team;
+        return n < N ? n : N - 1;
     };
 
     // The 16 conversion steps of every unit are spread over the teams; a
@@ -458,7 +452,10 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
     for (int b = 0; b < B; ++b)
 #pragma unroll
         for (int k = 0; k < NST; ++k) xv[b][k] = ldg<f4>(X + b * ldx + T::step(u, team * NST + k).src);
-    load_rows(c0);
+    int64_t c = blockIdx.x;
+    int64_t n_cur = row_of(c);
+    uint32_t ra[T::kRaw], rb[T::kRaw];
+    T::load(W + n_cur * row_bytes, u, ra);
     // keep the weight loads here, in flight during the conversion below
     __builtin_amdgcn_sched_barrier(0);
 
@@ -479,96 +476,114 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
             for (int i = 0; i < 8; ++i) xa.g[b][i] = u4{img[4 * i], img[4 * i + 1], img[4 * i + 2], img[4 * i + 3]};
         }
     } else {
+        // uint32 view of the group array and float view of the sum array
+        uint32_t *gw = xs;
+        float *sums = reinterpret_cast<float *>(xs + (size_t)B * 8 * 4 * team_threads);
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            uint32_t *img = xs + ((size_t)b * team_threads + ut) * kImg;
 #pragma unroll
             for (int k = 0; k < NST; ++k) {
                 const int s = team * NST + k;
                 const Step st = T::step(u, s);
                 uint32_t p0, p1;
                 const float sum = convert_step(xv[b][k], st.div16, p0, p1);
-                img[st.d0] = p0;
-                img[st.d0 + 1] = p1;
-                img[32 + s] = __builtin_bit_cast(uint32_t, sum);
+                uint32_t *e = gw + ((size_t)(b * 8 + st.d0 / 4) * team_threads + ut) * 4 + st.d0 % 4;
+                e[0] = p0;
+                e[1] = p1;
+                sums[(b * 16 + s) * team_threads + ut] = sum;
             }
         }
         __syncthreads();
+        xa.grp = reinterpret_cast<const u4 *>(xs) + ut;
+        xa.tt = team_threads;
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            xa.img[b] = xs + ((size_t)b * team_threads + ut) * kImg;
 #pragma unroll
             for (int k = 0; k < T::kSums; ++k) xa.s[b][k] = 0.f;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                // Copy the elements into scalars before reinterpreting them:
-                // hipcc resolves __builtin_bit_cast applied directly to an
-                // ext_vector element (v.y) to element 0 of the vector.
-                const u4 v = lds_ld16(xa.img[b] + 32 + 4 * q);
-                const uint32_t e0 = v.x, e1 = v.y, e2 = v.z, e3 = v.w;
-                xa.s[b][T::step(u, 4 * q).slot] += __uint_as_float(e0);
-                xa.s[b][T::step(u, 4 * q + 1).slot] += __uint_as_float(e1);
-                xa.s[b][T::step(u, 4 * q + 2).slot] += __uint_as_float(e2);
-                xa.s[b][T::step(u, 4 * q + 3).slot] += __uint_as_float(e3);
-            }
+            for (int q = 0; q < 16; ++q) xa.s[b][T::step(u, q).slot] += sums[(b * 16 + q) * team_threads + ut];
         }
     }
 
-    // ONESHOT: the grid holds exactly one row group per workgroup, so the
-    // loop body runs once and never reloads.
-    for (int64_t c = c0; c < ngroups; c += g) {
-        if (!ONESHOT && c != c0) load_rows(c);
-        const int64_t n0 = (c * TEAMS + team) * R;
-        float acc[R][B];
+    // Row results are not stored inside the loop: lane i of the team's first
+    // wave keeps the result of the team's i-th row in `yb` (the host limits a
+    // launch to 64 rows per team), and the wave writes them out at the end.
+    // With no stores between the loads, the compiler's count of outstanding
+    // memory operations covers loads only, so waiting for the current row
+    // never waits for the prefetch.
+    const bool leader = ut < 64;   // the team's first wave
+    float yb[B];
 #pragma unroll
-        for (int j = 0; j < R; ++j) {
+    for (int b = 0; b < B; ++b) yb[b] = 0.f;
+    const int64_t c_first = c;
+    int kept = 0;
+
+    // Dot product of one row, reduced over the team into yb.  `par`
+    // alternates the cross-wave scratch so one barrier per row suffices: a
+    // wave that writes red[par] again has passed the barrier of the row in
+    // between, which every wave reaches only after its reads of red[par].
+    auto row = [&](const uint32_t *raw, int par) {
+        float acc[B];
 #pragma unroll
-            for (int b = 0; b < B; ++b) acc[j][b] = 0.f;
-            T::template dot<B>(raw[j], xa, u, acc[j]);
-            // rows one after another: interleaving them gains nothing (each
-            // waits for its own loads) and would multiply live registers
-            __builtin_amdgcn_sched_barrier(0);
+        for (int b = 0; b < B; ++b) acc[b] = 0.f;
+        T::template dot<B>(raw, xa, u, acc);
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const float v = wave_sum_to_lane63(active ? acc[b] : 0.f);
+            if (ONEWAVE) {
+                const float tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+                yb[b] = lane == kept ? tot : yb[b];
+            } else if (lane == 63) {
+                red[par][wave][b] = v;
+            }
         }
-#pragma unroll
-        for (int j = 0; j < R; ++j) {
+        if (!ONEWAVE) {
+            __syncthreads();
 #pragma unroll
             for (int b = 0; b < B; ++b) {
-                const float v = wave_sum_to_lane63(active ? acc[j][b] : 0.f);
-                if (geo.wr == 1) {
-                    if (lane == 63 && n0 + j < N) Y[b * ldy + n0 + j] = v;
-                } else if (lane == 63) {
-                    red[wave][j * B + b] = v;
-                }
+                float tot = 0.f;
+                for (int w = 0; w < wr; ++w) tot += red[par][team * wr + w][b];
+                yb[b] = lane == kept ? tot : yb[b];
             }
         }
-        if (geo.wr > 1) {
-            __syncthreads();
-            if (ut < R * B) {
-                const int j = ut / B, b = ut % B;
-                float s = 0.f;
-                for (int w = 0; w < geo.wr; ++w) s += red[team * geo.wr + w][ut];
-                if (n0 + j < N) Y[b * ldy + n0 + j] = s;
-            }
-            __syncthreads();
-        }
-        if (ONESHOT) break;
-    }
-}
+        ++kept;
+    };
 
-template <class T, int B, int R, int TEAMS, int MAXT>
-int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
-           const float *X, int64_t ldx, float *Y, int64_t ldy, int64_t grid_cap)
-{
-    const int threads = TEAMS * geo.wr * 64;
-    const size_t lds = TEAMS > 1 ? (size_t)B * kImg * geo.wr * 64 * 4 : 0;
-    const int64_t ngroups = (N + (int64_t)TEAMS * R - 1) / ((int64_t)TEAMS * R);
-    if (ngroups <= grid_cap)
-        hipLaunchKernelGGL((qmatvec_kernel<T, B, R, TEAMS, MAXT, true>), dim3((unsigned)ngroups), dim3(threads),
-                           lds, ctx->stream, W, N, row_bytes, geo, X, ldx, Y, ldy);
-    else
-        hipLaunchKernelGGL((qmatvec_kernel<T, B, R, TEAMS, MAXT, false>), dim3((unsigned)grid_cap), dim3(threads),
-                           lds, ctx->stream, W, N, row_bytes, geo, X, ldx, Y, ldy);
-    return aih_launch_status();
+    // The address of each prefetch is computed half an iteration ahead, while
+    // both register buffers are live, so the loop head holds nothing but the
+    // loads (temporaries placed in a just-consumed buffer would make the
+    // compiler wait for that buffer's earlier loads).
+    auto next_ptr = [&](int64_t cc, int64_t n_now) {
+        const int64_t cn = cc + g;
+        return W + (cn < ngroups ? row_of(cn) : n_now) * row_bytes;
+    };
+    int64_t n_next = c + g < ngroups ? row_of(c + g) : n_cur;
+    const uint8_t *p_next = W + n_next * row_bytes;
+    for (;;) {
+        T::load(p_next, u, rb);
+        __builtin_amdgcn_sched_barrier(0);   // prefetch issued before the row is consumed
+        const int64_t cn = c + g;
+        const int64_t n_after = cn < ngroups ? row_of(cn) : n_cur;
+        p_next = next_ptr(cn, n_after);
+        row(ra, 0);
+        if (cn >= ngroups) break;
+        c = cn;
+        n_cur = n_after;
+        T::load(p_next, u, ra);
+        __builtin_amdgcn_sched_barrier(0);
+        const int64_t cn2 = c + g;
+        const int64_t n_after2 = cn2 < ngroups ? row_of(cn2) : n_cur;
+        p_next = next_ptr(cn2, n_after2);
+        row(rb, 1);
+        if (cn2 >= ngroups) break;
+        c = cn2;
+        n_cur = n_after2;
+    }
+    const int64_t n = (c_first + (int64_t)lane * g) * TEAMS + team;
+    if (leader && lane < kept && n < N) {
+#pragma unroll
+        for (int b = 0; b < B; ++b) Y[b * ldy + n] = yb[b];
+    }
 }
 
 Geom make_geom(int64_t K)
@@ -580,38 +595,48 @@ Geom make_geom(int64_t K)
     return g;
 }
 
-// Rows per team per iteration.  One row per team with three resident
-// workgroups per CU measured fastest on MI355X for the 14336 x 4096 Q4_K
-// matvec (several rows per team raise register use and lower occupancy more
-// than they add loads in flight); R stays a template parameter for tuning.
-int pick_rows(int64_t, int, int64_t) { return 1; }
-
-template <class T, int B, int TEAMS>
-int launch_r(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
-             const float *X, int64_t ldx, float *Y, int64_t ldy, int64_t cap)
+// One launch of one workgroup per CU: every workgroup pays the activation
+// conversion once, so fewer, longer-lived workgroups win.  On MI355X
+// (14336 x 4096 Q4_K) one workgroup of eight single-wave teams per CU ran
+// 7.9 us, against 8.2 us with two per CU, 9.5 us with one 16-team
+// workgroup per CU and 9.5-11.7 us with 4-7 workgroups per CU.
+template <class T, int B, int TEAMS, bool ONEWAVE, int MAXT>
+int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
+           const float *X, int64_t ldx, float *Y, int64_t ldy)
 {
-    switch (pick_rows(N, TEAMS, cap)) {
-    case 1: return launch<T, B, 1, TEAMS, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, cap);
-    case 2: return launch<T, B, 2, TEAMS, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, cap);
-    default: return launch<T, B, 4, TEAMS, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, cap);
+    const int threads = TEAMS * geo.wr * 64;
+    const size_t lds = TEAMS > 1 ? (size_t)B * kLdsBytesPerUnit * geo.wr * 64 : 0;
+    const int64_t cap = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    // A workgroup computes at most 64 row groups per launch (its results are
+    // held in one register per lane); taller matrices take several launches.
+    const int64_t rows_per_launch = cap * 64 * TEAMS;
+    for (int64_t r0 = 0; r0 < N; r0 += rows_per_launch) {
+        const int64_t nr = N - r0 < rows_per_launch ? N - r0 : rows_per_launch;
+        const int64_t ng = (nr + TEAMS - 1) / TEAMS;
+        const int64_t grid = ng < cap ? ng : cap;
+        hipLaunchKernelGGL((qmatvec_kernel<T, B, TEAMS, ONEWAVE, MAXT>), dim3((unsigned)grid), dim3(threads), lds,
+                           ctx->stream, W + r0 * row_bytes, nr, row_bytes, geo, X, ldx, Y + r0, ldy);
+        const int rc = aih_launch_status();
+        if (rc) return rc;
     }
+    return AIH_OK;
 }
 
 // One pass over W for `two` ? 2 : 1 activation columns.
 template <class T>
 int launch_pass(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
-                const float *X, int64_t ldx, float *Y, int64_t ldy, bool two, int64_t cap)
+                const float *X, int64_t ldx, float *Y, int64_t ldy, bool two)
 {
     switch (geo.teams) {
-    case 8: return two ? launch_r<T, 2, 8>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, cap)
-                       : launch_r<T, 1, 8>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, cap);
-    case 4: return two ? launch_r<T, 2, 4>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, cap)
-                       : launch_r<T, 1, 4>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, cap);
-    case 2: return two ? launch_r<T, 2, 2>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, cap)
-                       : launch_r<T, 1, 2>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, cap);
+    case 8: return two ? launch<T, 2, 8, true, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy)
+                       : launch<T, 1, 8, true, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy);
+    case 4: return two ? launch<T, 2, 4, false, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy)
+                       : launch<T, 1, 4, false, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy);
+    case 2: return two ? launch<T, 2, 2, false, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy)
+                       : launch<T, 1, 2, false, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy);
     default: {  // one team of up to 16 waves: one column per pass within 128 VGPRs
-        int rc = launch<T, 1, 1, 1, 1024>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, cap);
-        if (!rc && two) rc = launch<T, 1, 1, 1, 1024>(ctx, W, N, row_bytes, geo, X + ldx, ldx, Y + ldy, ldy, cap);
+        int rc = launch<T, 1, 1, false, 1024>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy);
+        if (!rc && two) rc = launch<T, 1, 1, false, 1024>(ctx, W, N, row_bytes, geo, X + ldx, ldx, Y + ldy, ldy);
         return rc;
     }
     }
@@ -622,14 +647,10 @@ int launch_type(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t ro
                 const float *X, int64_t ldx, float *Y, int64_t ldy, int batch)
 {
     const Geom geo = make_geom(K);
-    const int threads = geo.teams * geo.wr * 64;
-    // Three workgroups of up to eight waves per CU.
-    const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-    const int64_t cap = cus * (threads <= 512 ? 3 : 1);
     // Columns are processed in passes of at most two; each pass re-reads W.
     for (int b0 = 0; b0 < batch; b0 += 2) {
         const int rc = launch_pass<T>(ctx, W, N, row_bytes, geo, X + b0 * ldx, ldx, Y + b0 * ldy, ldy,
-                                      batch - b0 >= 2, cap);
+                                      batch - b0 >= 2);
         if (rc) return rc;
     }
     return AIH_OK;

@@ -4,7 +4,7 @@ reference-decoded weights): normwise and max relative error <= 1e-3.
 Covers the benchmark shapes (Q8_0 4096x4096; Q4_0 and Q4_K 14336x4096; Q6_K
 4096x14336 at batch 1, 2, 4, 8), odd row counts (partial row groups), small K,
 multi-wave K (14336), K beyond 256 units (1024-thread variant), odd batch,
-padded strides, and argument errors.
+matrices taller than one launch, padded strides, and argument errors.
 """
 import numpy as np
 import pytest
@@ -50,6 +50,19 @@ def test_benchmark_shapes(device, orc, qtype, n, k, batch):
 def test_edge_shapes(device, orc, qtype, n, k, batch):
     w = synth_weight(qtype, n, k, seed=n * 1000 + k)
     x = x_of(k, batch, seed=k + batch)
+    y = qmatvec(device, qtype, w, n, k, x)
+    ref = orc.matvec(qtype, w, n, k, x, nthreads=8)
+    assert_close(y, ref, TOL, "type %d %dx%d b%d" % (qtype, n, k, batch))
+
+
+@pytest.mark.parametrize("qtype,n,k,batch", [
+    (nat.Q8_0, 140001, 64, 2),     # more rows than one launch holds (64 row groups per workgroup)
+    (nat.Q4_K, 140001, 256, 1),
+    (nat.Q6_K, 32000, 4096, 1),    # output-projection shape: many rows per team
+])
+def test_tall_matrices(device, orc, qtype, n, k, batch):
+    w = synth_weight(qtype, n, k, seed=7)
+    x = x_of(k, batch, seed=11)
     y = qmatvec(device, qtype, w, n, k, x)
     ref = orc.matvec(qtype, w, n, k, x, nthreads=8)
     assert_close(y, ref, TOL, "type %d %dx%d b%d" % (qtype, n, k, batch))

@@ -46,7 +46,17 @@ struct aih_ctx {
     std::unordered_map<void *, size_t> allocs;
     size_t tracked_bytes = 0;
     int cu_count = 0;
+    // Grow-only device workspace for kernels that stage data (the GEMM's fp16
+    // copy of X).  Not counted in tracked_bytes; freed by aih_destroy.
+    void *work = nullptr;
+    size_t work_bytes = 0;
 };
+
+// Device workspace of at least `bytes` on the context's device.  Grows by
+// reallocating (hipFree waits for the device), which is refused while the
+// stream is being captured into a graph: run the operation once outside the
+// capture first.  Returns AIH_OK or a status.
+int aih_workspace(aih_ctx *ctx, size_t bytes, void **out);
 
 #define AIH_TRY(expr)                                  \
     do {                                               \

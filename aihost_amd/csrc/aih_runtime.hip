@@ -30,12 +30,39 @@ int release(aih_ctx *ctx)
     }
     for (int i = 0; i < aih_ctx::kEvents; ++i)
         if (ctx->ev[i]) (void)hipEventDestroy(ctx->ev[i]);
+    if (ctx->work) (void)hipFree(ctx->work);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return AIH_OK;
 }
 
 }  // namespace
+
+int aih_workspace(aih_ctx *ctx, size_t bytes, void **out)
+{
+    if (bytes <= ctx->work_bytes) {
+        *out = ctx->work;
+        return AIH_OK;
+    }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    AIH_TRY(hipStreamIsCapturing(ctx->stream, &cs));
+    if (cs != hipStreamCaptureStatusNone) return AIH_E_LIMIT;
+    if (ctx->work) {
+        AIH_TRY(hipFree(ctx->work));
+        ctx->work = nullptr;
+        ctx->work_bytes = 0;
+    }
+    const size_t sz = (bytes + ((size_t)1 << 20) - 1) & ~(((size_t)1 << 20) - 1);   // whole MiB
+    hipError_t e = hipMalloc(&ctx->work, sz);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        ctx->work = nullptr;
+        return (int)e;
+    }
+    ctx->work_bytes = sz;
+    *out = ctx->work;
+    return AIH_OK;
+}
 
 extern "C" {
 

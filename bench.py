@@ -31,6 +31,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "quant matvec GB/s (% HBM peak) + decode tokens/s, Q4_K 4096x14336, 1 GPU"
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK = 2.5e15     # dense fp16 MFMA FLOP/s
 COPIES = 12
 GRAPH_LAUNCHES = 120
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "qmatvec_q4k_14336x4096_b1_hbm_traffic.md")
@@ -101,6 +102,56 @@ class MatvecBench:
     def close(self):
         self.nat.lib().aih_graph_destroy(self.graph)
         for b in self.w + [self.x, self.y]:
+            b.dispose()
+
+
+class GemmBench:
+    """Prefill GEMM on one weight copy: a graph of `launches` aih_qgemm calls."""
+
+    def __init__(self, dev, qtype, n, k, m, launches=20, seed_w=42, seed_x=43):
+        from aihost_amd import _native as nat
+        from aihost_amd import compute as C
+        self.nat, self.dev = nat, dev
+        self.qtype, self.n, self.k, self.m = qtype, n, k, m
+        packed = C.quantize(qtype, C.fill_normal(seed_w, n * k, 0.0, 0.02), n, k)
+        xh = C.fill_normal(seed_x, m * k, 0.0, 1.0)
+        self.w = dev.create_buffer(packed.nbytes)
+        self.w.write(packed)
+        self.x = dev.create_buffer(xh.nbytes)
+        self.x.write(xh)
+        self.y = dev.create_buffer(m * n * 4)
+        self._launch()   # sizes the library's workspace, which cannot grow during capture
+        dev.synchronize()
+        L, h = nat.lib(), dev.handle
+        nat.check(L.aih_capture_begin(h), "aih_capture_begin")
+        for _ in range(launches):
+            self._launch()
+        g = ctypes.c_void_p()
+        nat.check(L.aih_capture_end(h, ctypes.byref(g)), "aih_capture_end")
+        self.graph, self.launches = g.value, launches
+
+    def _launch(self):
+        st = self.nat.lib().aih_qgemm(self.dev.handle, self.qtype, self.w.get_pointer(), self.n, self.k,
+                                      self.x.get_pointer(), self.m, self.y.get_pointer())
+        self.nat.check(st, "aih_qgemm")
+
+    def time(self, graphs, warmup=2):
+        L, h = self.nat.lib(), self.dev.handle
+        for _ in range(warmup):
+            self.nat.check(L.aih_graph_launch(h, self.graph), "aih_graph_launch")
+        self.dev.synchronize()
+        self.nat.check(L.aih_event_record(h, 0), "event")
+        for _ in range(graphs):
+            self.nat.check(L.aih_graph_launch(h, self.graph), "aih_graph_launch")
+        self.nat.check(L.aih_event_record(h, 1), "event")
+        self.dev.synchronize()
+        ev = ctypes.c_float()
+        self.nat.check(L.aih_event_elapsed(h, 0, 1, ctypes.byref(ev)), "event")
+        return ev.value / (graphs * self.launches)
+
+    def close(self):
+        self.nat.lib().aih_graph_destroy(self.graph)
+        for b in (self.w, self.x, self.y):
             b.dispose()
 
 
@@ -183,6 +234,14 @@ def main():
                            "us_per_call": round(s * 1e3, 3),
                            "frac_hbm_peak": round(by / (kern * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
             mb.close()
+        # prefill GEMM: Q4_K W 4096x4096, X 512x4096 (MFMA-bound; fp16 operands, fp32 accumulation)
+        gb = GemmBench(dev, nat.Q4_K, 4096, 4096, 512)
+        ms = gb.time(10)
+        flops = 2.0 * 512 * 4096 * 4096
+        extra["q4_k_gemm_4096x4096_m512"] = {"TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
+                                             "us_per_call": round(ms * 1e3, 2),
+                                             "frac_mfma_peak": round(flops / (ms * 1e-3) / MFMA_F16_PEAK, 4)}
+        gb.close()
 
     cpu = None
     if not args.no_cpu_baseline:

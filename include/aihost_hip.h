@@ -152,8 +152,12 @@ int aih_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
                 const float *X, int64_t ldx, float *Y, int64_t ldy, int batch);
 
 /* Prefill GEMM, dequantization fused:  Y[m*N + n] = sum_k X[m*K + k] * W[n, k].
- * Tiles of W are dequantized into LDS and contracted on MFMA with fp32
- * accumulation.  Replaces TempF32 + ComputeOps.MatMulWeights for M > 8. */
+ * X is converted once to fp16 in a context workspace (M*K*2 bytes, grown on
+ * demand and kept until aih_destroy); tiles of W are dequantized into LDS as
+ * fp16 and contracted on MFMA with fp32 accumulation.  K must be a multiple
+ * of 64 (else AIH_E_LIMIT) and X 16-byte aligned.  The workspace cannot grow
+ * while the stream is being captured (AIH_E_LIMIT): run the largest GEMM once
+ * before capturing.  Replaces TempF32 + ComputeOps.MatMulWeights for M > 8. */
 int aih_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
               const float *X, int64_t M, float *Y);
 

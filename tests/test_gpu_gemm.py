@@ -1,0 +1,110 @@
+"""Fused prefill GEMM (MFMA) vs the oracle (fp32 sequential accumulation over
+the reference-decoded weights): normwise and max relative error <= 1e-3.
+
+Covers the prefill workload (Q4_K W 4096x4096, X 512x4096), every format,
+partial tiles in M and N, K of one step, the ComputeOps-style routing
+(M <= 8 -> matvec, larger -> GEMM) and argument errors.
+"""
+import numpy as np
+import pytest
+
+from aihost_amd import _native as nat
+from aihost_amd import compute as C
+from gpu_util import assert_close, qgemm, synth_weight, upload
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3  # relative 1e-3 with fp32 accumulation
+
+
+def x_of(m, k, seed=43):
+    return C.fill_normal(seed, m * k, 0.0, 1.0).reshape(m, k)
+
+
+def test_prefill_workload(device, orc):
+    n, k, m = 4096, 4096, 512
+    w = synth_weight(nat.Q4_K, n, k)
+    x = x_of(m, k)
+    y = qgemm(device, nat.Q4_K, w, n, k, x)
+    ref = orc.matvec(nat.Q4_K, w, n, k, x, nthreads=16)
+    nrm, mx = assert_close(y, ref, TOL, "Q4_K 4096x4096 M=512")
+    print("Q4_K prefill normwise=%.3g max=%.3g" % (nrm, mx))
+
+
+@pytest.mark.parametrize("qtype,n,k,m", [
+    (nat.Q4_K, 64, 256, 128), (nat.Q4_K, 65, 512, 129), (nat.Q4_K, 1, 256, 9), (nat.Q4_K, 200, 1024, 300),
+    (nat.Q6_K, 64, 256, 128), (nat.Q6_K, 100, 768, 77), (nat.Q6_K, 130, 4096, 40),
+    (nat.Q8_0, 64, 64, 128), (nat.Q8_0, 63, 320, 200), (nat.Q8_0, 257, 128, 17),
+    (nat.Q4_0, 64, 64, 128), (nat.Q4_0, 99, 2048, 65), (nat.Q4_0, 5, 192, 130),
+])
+def test_shapes(device, orc, qtype, n, k, m):
+    w = synth_weight(qtype, n, k, seed=n * 7 + k)
+    x = x_of(m, k, seed=m + k)
+    y = qgemm(device, qtype, w, n, k, x)
+    assert_close(y, orc.matvec(qtype, w, n, k, x, nthreads=8), TOL, "type %d %dx%d M=%d" % (qtype, n, k, m))
+
+
+def test_subnormal_scales(device, orc):
+    rng = np.random.default_rng(9)
+    n, k, m = 70, 512, 33
+    for qtype, bb, offs in ((nat.Q4_K, 144, (0, 2)), (nat.Q6_K, 210, (208,)), (nat.Q8_0, 34, (0,)),
+                            (nat.Q4_0, 18, (0,))):
+        nb = n * k // (256 if bb in (144, 210) else 32)
+        data = rng.integers(0, 256, (nb, bb)).astype(np.uint8)
+        for off in offs:
+            h = rng.integers(0x0001, 0x2400, nb).astype(np.uint16)
+            data[:, off:off + 2] = h.view(np.uint8).reshape(nb, 2)
+        data = data.reshape(-1)
+        x = x_of(m, k, seed=qtype)
+        assert_close(qgemm(device, qtype, data, n, k, x), orc.matvec(qtype, data, n, k, x), TOL,
+                     "type %d" % qtype)
+
+
+def test_matmul_weights_routing(device, orc):
+    n, k = 96, 512
+    w = synth_weight(nat.Q4_K, n, k)
+    ops = C.ComputeOps(device)
+    wt = C.Tensor.from_quantized(device, w, k, n, C.DataType.Q4_K)
+    for m in (1, 8, 9, 40):
+        x = x_of(m, k, seed=m)
+        a = C.Tensor.from_data(device, x)
+        y = ops.matmul_weights(a, wt)
+        assert y.shape == (m, n)
+        assert_close(y.read(), orc.matvec(nat.Q4_K, w, n, k, x), TOL, "M=%d" % m)
+        a.dispose()
+        y.dispose()
+    wt.dispose()
+
+
+def test_gemm_rows_match_matvec(device):
+    # Both paths round x to fp16; the GEMM also rounds each dequantized weight
+    # to fp16 (the matvec applies the scales in fp32), which alone moves the
+    # result by about 2e-4 normwise.  The two paths agree within that.
+    from gpu_util import qmatvec
+    n, k, m = 256, 4096, 16
+    w = synth_weight(nat.Q6_K, n, k)
+    x = x_of(m, k)
+    yg = qgemm(device, nat.Q6_K, w, n, k, x)
+    ym = np.vstack([qmatvec(device, nat.Q6_K, w, n, k, x[i:i + 1]) for i in range(m)])
+    assert_close(yg, ym, 5e-4)
+
+
+def test_argument_errors(device):
+    L = nat.lib()
+    h = device.handle
+    wb = upload(device, np.zeros(4352 * 4, np.uint8))
+    xb = upload(device, np.zeros(64 * 4096, np.float32))
+    yb = upload(device, np.zeros(64 * 64, np.float32))
+    W, X, Y = wb.get_pointer(), xb.get_pointer(), yb.get_pointer()
+    try:
+        assert L.aih_qgemm(h, nat.Q8_0, W, 4, 4096, X, 16, Y) == nat.AIH_OK
+        assert L.aih_qgemm(h, nat.Q8_0, W, 0, 4096, X, 16, Y) == nat.AIH_OK
+        assert L.aih_qgemm(h, nat.Q8_0, W, 4, 4096, X, 0, Y) == nat.AIH_OK
+        assert L.aih_qgemm(h, nat.Q8_0, W, 4, 100, X, 16, Y) == nat.AIH_E_INVALID
+        assert L.aih_qgemm(h, nat.Q8_0, W, 4, 96, X, 16, Y) == nat.AIH_E_LIMIT
+        assert L.aih_qgemm(h, nat.F32, W, 4, 4096, X, 16, Y) == nat.AIH_E_UNSUPPORTED
+        assert L.aih_qgemm(h, nat.Q8_0, None, 4, 4096, X, 16, Y) == nat.AIH_E_INVALID
+        device.synchronize()
+    finally:
+        for b in (wb, xb, yb):
+            b.dispose()

@@ -78,3 +78,5 @@ int aih_launch_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t
                        const float *X, int64_t ldx, float *Y, int64_t ldy, int batch);
 int aih_launch_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
                      const float *X, int64_t M, float *Y);
+int aih_launch_qmatvec_mfma(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
+                            const float *X, int64_t ldx, float *Y, int64_t ldy, int batch);

@@ -23,150 +23,17 @@
 // than the 1e-3 the path is held to.  Weights are dequantized in fp32 with the
 // reference's formulas (ComputeOps.cs:1629-1678 for Q4_K, :1735-1774 for Q6_K,
 // the GGUF definitions for Q8_0 and Q4_0) before the rounding to fp16.
-#include "aih_internal.h"
+#include "aih_pieces.h"
 
 namespace {
 
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+using namespace aih_pieces;
 typedef float f16v __attribute__((ext_vector_type(16)));
-typedef float f4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 128;          // activation rows per workgroup
 constexpr int BN = 64;           // weight rows per workgroup
 constexpr int BK = 64;           // K per step
 constexpr int LDK = BK + 8;      // LDS row stride in halves (16-byte pad against bank conflicts)
-
-template <class T>
-__device__ __forceinline__ T ldg(const void *p)
-{
-    T v;
-    __builtin_memcpy(&v, p, sizeof(T));
-    return v;
-}
-
-__device__ __forceinline__ float f16_at(const uint8_t *p)
-{
-    return (float)__builtin_bit_cast(_Float16, ldg<uint16_t>(p));
-}
-
-__device__ __forceinline__ uint32_t byte_of(const u4 &v, int j)
-{
-    const uint32_t w0 = v.x, w1 = v.y, w2 = v.z, w3 = v.w;
-    const uint32_t w = (j >> 2) == 0 ? w0 : (j >> 2) == 1 ? w1 : (j >> 2) == 2 ? w2 : w3;
-    return (w >> (8 * (j & 3))) & 0xFFu;
-}
-
-// Each type provides, for 64-element chunk c of a row and 16-element piece
-// s (elements 16s .. 16s+15 of the chunk), a load of the bytes it needs and
-// the 16 fp32 weights in natural element order.
-
-// Q4_K: chunk c is 64-group g = c % 4 of block c / 4; elements 0..31 of the
-// group are the low nibbles of qs[32g .. 32g+31] (sub-block 2g), elements
-// 32..63 the high nibbles (sub-block 2g+1) (ComputeOps.cs:1642-1675).
-struct G4K {
-    struct Raw { u4 hdr, qs; };
-    __device__ static void load(const uint8_t *row, int c, int s, Raw &r)
-    {
-        const uint8_t *b = row + (c >> 2) * 144;
-        r.hdr = ldg<u4>(b);
-        r.qs = ldg<u4>(b + 16 + 32 * (c & 3) + 16 * (s & 1));
-    }
-    __device__ static void piece(const Raw &r, int c, int s, float *y)
-    {
-        const int hi = s >> 1;
-        const int sb = 2 * (c & 3) + hi;   // sub-block 0..7
-        // get_scale_min_k4 (QuantizationFormats.cs:157-165) on scales = hdr bytes 4..15
-        uint32_t sc, mn;
-        if (sb < 4) {
-            sc = byte_of(r.hdr, 4 + sb) & 63u;
-            mn = byte_of(r.hdr, 8 + sb) & 63u;
-        } else {
-            sc = (byte_of(r.hdr, 8 + sb) & 0xFu) | ((byte_of(r.hdr, sb) >> 6) << 4);
-            mn = (byte_of(r.hdr, 8 + sb) >> 4) | ((byte_of(r.hdr, 4 + sb) >> 6) << 4);
-        }
-        const uint32_t h0 = r.hdr.x;
-        const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(h0 & 0xFFFFu));
-        const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(h0 >> 16));
-        const float D = d * (float)sc, Mn = dmin * (float)mn;
-        const uint32_t w[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const uint32_t q = __builtin_amdgcn_ubfe(w[j >> 2], 8 * (j & 3) + 4 * hi, 4);
-            y[j] = D * (float)q - Mn;
-        }
-    }
-};
-
-// Q6_K: chunk c covers half h = (c % 4) / 2 of block c / 4, quarters
-// Q0 = 2 * (c % 2) and Q0 + 1; piece s is quarter Q = Q0 + s / 2, columns
-// 16 * (s % 2) .. +15 (ComputeOps.cs:1748-1771).
-struct G6K {
-    struct Raw { u4 ql, qh; uint32_t sc; float d; };
-    __device__ static void load(const uint8_t *row, int c, int s, Raw &r)
-    {
-        const uint8_t *b = row + (c >> 2) * 210;
-        const int h = (c & 3) >> 1, Q = 2 * (c & 1) + (s >> 1), t = s & 1;
-        r.ql = ldg<u4>(b + 64 * h + 32 * (Q & 1) + 16 * t);
-        r.qh = ldg<u4>(b + 128 + 32 * h + 16 * t);
-        r.sc = b[192 + 8 * h + 2 * Q + t];
-        r.d = f16_at(b + 208);
-    }
-    __device__ static void piece(const Raw &r, int c, int s, float *y)
-    {
-        const int Q = 2 * (c & 1) + (s >> 1);
-        const float ds = r.d * (float)(int)(int8_t)(uint8_t)r.sc;
-        const uint32_t l[4] = {r.ql.x, r.ql.y, r.ql.z, r.ql.w};
-        const uint32_t hb[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const uint32_t lo = __builtin_amdgcn_ubfe(l[j >> 2], 8 * (j & 3) + 4 * (Q >> 1), 4);
-            const uint32_t hi = __builtin_amdgcn_ubfe(hb[j >> 2], 8 * (j & 3) + 2 * Q, 2);
-            y[j] = ds * (float)((int)(lo | (hi << 4)) - 32);
-        }
-    }
-};
-
-// Q8_0: chunk c is blocks 2c and 2c+1; piece s is elements 16 * (s % 2) ..
-// of block 2c + s / 2.  y = d * q.
-struct G80 {
-    struct Raw { u4 qs; float d; };
-    __device__ static void load(const uint8_t *row, int c, int s, Raw &r)
-    {
-        const uint8_t *b = row + 34 * (2 * c + (s >> 1));
-        r.d = f16_at(b);
-        r.qs = ldg<u4>(b + 2 + 16 * (s & 1));
-    }
-    __device__ static void piece(const Raw &r, int, int, float *y)
-    {
-        const uint32_t w[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-            y[j] = r.d * (float)(int)__builtin_amdgcn_sbfe((int)w[j >> 2], 8 * (j & 3), 8);
-    }
-};
-
-// Q4_0: chunk c is blocks 2c and 2c+1; piece s is block 2c + s / 2, low
-// nibbles (elements 0..15) for even s, high nibbles (16..31) for odd s.
-// y = d * (q - 8).
-struct G40 {
-    struct Raw { u4 qs; float d; };
-    __device__ static void load(const uint8_t *row, int c, int s, Raw &r)
-    {
-        const uint8_t *b = row + 18 * (2 * c + (s >> 1));
-        r.d = f16_at(b);
-        r.qs = ldg<u4>(b + 2);
-    }
-    __device__ static void piece(const Raw &r, int, int s, float *y)
-    {
-        const uint32_t w[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const uint32_t q = __builtin_amdgcn_ubfe(w[j >> 2], 8 * (j & 3) + 4 * (s & 1), 4);
-            y[j] = r.d * (float)((int)q - 8);
-        }
-    }
-};
 
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS
 // operations, then for every wave.  __syncthreads() would also wait for the
@@ -176,14 +43,6 @@ struct G40 {
 __device__ __forceinline__ void lds_barrier()
 {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-__device__ __forceinline__ h8 pack8(const float *v)
-{
-    h8 r;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) r[i] = (_Float16)v[i];
-    return r;
 }
 
 // X (fp32, M x K) -> fp16 copy, 8 elements per thread.  Every workgroup of

@@ -656,6 +656,9 @@ int launch_type(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t ro
     return AIH_OK;
 }
 
+// Batches from this size on go to the MFMA kernel (aih_qmatvec_mfma.hip).
+constexpr int kMfmaMinBatch = 3;
+
 }  // namespace
 
 int aih_launch_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
@@ -668,6 +671,8 @@ int aih_launch_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t
     const uintptr_t wa = reinterpret_cast<uintptr_t>(W);
     if (wa % 16 != 0) return AIH_E_INVALID;
     if (reinterpret_cast<uintptr_t>(X) % 16 != 0 || (ldx % 4) != 0) return AIH_E_INVALID;
+    // Three or more columns: the MFMA kernel reads W once for all of them.
+    if (batch >= kMfmaMinBatch) return aih_launch_qmatvec_mfma(ctx, type, W, N, K, X, ldx, Y, ldy, batch);
     const int64_t rb = aih_row_bytes(type, K);
     const uint8_t *w = static_cast<const uint8_t *>(W);
     switch (type) {

@@ -94,17 +94,21 @@ def test_subnormal_and_extreme_scales(device, orc):
                      "type %d" % qtype)
 
 
-def test_linearity_at_full_size(device):
+@pytest.mark.parametrize("batch_path", [2, 3])   # dot2 kernel (1-2 columns), MFMA kernel (3-8)
+def test_linearity_at_full_size(device, batch_path):
     n, k = 14336, 4096
     w = synth_weight(nat.Q4_K, n, k)
     x1, x2 = x_of(k, 1, 1), x_of(k, 1, 2)
-    y1 = qmatvec(device, nat.Q4_K, w, n, k, x1)
-    y2 = qmatvec(device, nat.Q4_K, w, n, k, x2)
-    y12 = qmatvec(device, nat.Q4_K, w, n, k, np.vstack([x1, x2, x1 + x2]))
-    # batch columns are computed independently of each other
-    assert_close(y12[0], y1[0], 1e-6)
-    assert_close(y12[1], y2[0], 1e-6)
-    assert_close(y12[2], y1[0] + y2[0], 1e-3)
+    extra = [x_of(k, 1, 3)] * (batch_path - 2)
+    ya = qmatvec(device, nat.Q4_K, w, n, k, np.vstack([x1, x2] + extra))
+    yb = qmatvec(device, nat.Q4_K, w, n, k, np.vstack([x2, x1] + extra))
+    # columns are computed independently of each other: swapping them swaps
+    # the results bit for bit
+    assert np.array_equal(ya[0], yb[1]) and np.array_equal(ya[1], yb[0])
+    y12 = qmatvec(device, nat.Q4_K, w, n, k, np.vstack([x1 + x2, x1] + extra))
+    assert_close(y12[0], ya[0] + ya[1], 1e-3)       # linearity
+    y1 = qmatvec(device, nat.Q4_K, w, n, k, x1)      # single-column kernel
+    assert_close(ya[0], y1[0], 5e-4)                 # the two kernels agree
 
 
 def test_compute_ops_mirror(device, orc):

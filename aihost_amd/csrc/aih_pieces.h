@@ -13,6 +13,7 @@
 namespace aih_pieces {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
@@ -72,6 +73,45 @@ struct G4K {
         for (int j = 0; j < 16; ++j) {
             const uint32_t q = __builtin_amdgcn_ubfe(w[j >> 2], 8 * (j & 3) + 4 * hi, 4);
             y[j] = D * (float)q - Mn;
+        }
+    }
+    // The same 16 weights as fp16, in about 1.5 instructions per weight: a
+    // nibble OR-ed into the mantissa of 0x6400 is the fp16 value 1024 + q
+    // (1024 + 16q for a high nibble left in place), and one fused fp32
+    // multiply-add with fp16 output gives code * D' - (1024 * D' + Mn), with
+    // D' = D (D / 16 for a high nibble).  Rounding the constant to fp32 moves
+    // a weight by at most 2^-24 * 1024 * D', far below its fp16 rounding.
+    __device__ static void piece_h(const Raw &r, int c, int s, h8 &lo, h8 &hi8)
+    {
+        const int hi = s >> 1;
+        const int sb = 2 * (c & 3) + hi;
+        uint32_t sc, mn;
+        if (sb < 4) {
+            sc = byte_of(r.hdr, 4 + sb) & 63u;
+            mn = byte_of(r.hdr, 8 + sb) & 63u;
+        } else {
+            sc = (byte_of(r.hdr, 8 + sb) & 0xFu) | ((byte_of(r.hdr, sb) >> 6) << 4);
+            mn = (byte_of(r.hdr, 8 + sb) >> 4) | ((byte_of(r.hdr, 4 + sb) >> 6) << 4);
+        }
+        const float D = f16_bits(r.hdr.x) * (float)sc, Mn = f16_bits(r.hdr.x >> 16) * (float)mn;
+        const float Dp = hi ? D * 0.0625f : D;
+        const float C = 1024.f * Dp + Mn;
+        const uint32_t mask = hi ? 0x00F000F0u : 0x000F000Fu;
+        const uint32_t w[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+        _Float16 y[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const h2 a = __builtin_bit_cast(h2, (w[i] & mask) | 0x64006400u);
+            const h2 b = __builtin_bit_cast(h2, ((w[i] >> 8) & mask) | 0x64006400u);
+            y[4 * i + 0] = (_Float16)__builtin_fmaf((float)a.x, Dp, -C);
+            y[4 * i + 2] = (_Float16)__builtin_fmaf((float)a.y, Dp, -C);
+            y[4 * i + 1] = (_Float16)__builtin_fmaf((float)b.x, Dp, -C);
+            y[4 * i + 3] = (_Float16)__builtin_fmaf((float)b.y, Dp, -C);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            lo[j] = y[j];
+            hi8[j] = y[8 + j];
         }
     }
 };
@@ -152,6 +192,31 @@ __device__ __forceinline__ h8 pack8(const float *v)
 #pragma unroll
     for (int i = 0; i < 8; ++i) r[i] = (_Float16)v[i];
     return r;
+}
+
+// fp16 weights of a piece for formats without a dedicated fp16 path.
+template <class T>
+__device__ __forceinline__ void piece_h_of(const typename T::Raw &r, int c, int s, h8 &lo, h8 &hi)
+{
+    float y[16];
+    T::piece(r, c, s, y);
+    lo = pack8(y);
+    hi = pack8(y + 8);
+}
+
+template <class T>
+struct HasPieceH {
+    template <class U> static auto test(int) -> decltype(&U::piece_h, char());
+    template <class U> static int test(...);
+    static constexpr bool value = sizeof(test<T>(0)) == 1;
+};
+
+// The 16 weights of piece s of chunk c as two fp16 vectors.
+template <class T>
+__device__ __forceinline__ void piece16h(const typename T::Raw &r, int c, int s, h8 &lo, h8 &hi)
+{
+    if constexpr (HasPieceH<T>::value) T::piece_h(r, c, s, lo, hi);
+    else piece_h_of<T>(r, c, s, lo, hi);
 }
 
 }  // namespace aih_pieces

@@ -9,13 +9,13 @@
 // dequantizes tiles of W into LDS as fp16 and contracts them on the matrix
 // cores (v_mfma_f32_32x32x16_f16, fp32 accumulation).
 //
-// Tiling.  X is first converted to an fp16 copy in the context's workspace.
-// A workgroup of four waves then owns a 128 (M) x 64 (N) tile of Y and walks
-// K in steps of 64 elements (a Q4_K 64-group, a pair of Q8_0 or Q4_0 blocks,
-// two quarters of a Q6_K half-block).  Per step every thread copies 32 fp16
-// activations and dequantizes 16 weights into LDS; each wave then multiplies
-// its 64 x 32 sub-tile with two MFMAs per 16 k.  LDS is double buffered and
-// the global loads run two steps ahead in registers, one barrier per step.
+// Tiling.  X is first converted to fp16 in the context's workspace, stored in
+// MFMA fragment order.  A workgroup then owns a 128 (M) x 64 (N) tile of Y and
+// walks K in steps of 64 elements (a Q4_K 64-group, a pair of Q8_0 or Q4_0
+// blocks, two quarters of a Q6_K half-block).  Four producer waves dequantize
+// W for the next step into LDS while four consumer waves multiply the current
+// step (two 32x32x16 MFMAs per 16 k per wave), their A fragments loaded
+// straight from the tiled X; one barrier per step.
 //
 // Precision.  Both operands are rounded to fp16 (11-bit significand) and the
 // products accumulate in fp32: normwise error near 3e-4 against the fp32
@@ -45,108 +45,190 @@ __device__ __forceinline__ void lds_barrier()
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// X (fp32, M x K) -> fp16 copy, 8 elements per thread.  Every workgroup of
-// the GEMM re-reads its X rows once per N tile, so converting once here
-// halves that traffic and takes the conversion out of the GEMM's loop.
+// X (fp32, M x K) -> fp16, stored in the order the matrix cores read it.
+// The A operand of v_mfma_f32_32x32x16_f16 for rows 32*mb .. +31 and k
+// 16*kk .. +15 holds, in lane l, the 8 halves X[32*mb + l%32][16*kk +
+// 8*(l/32) .. +7]; here that fragment is the 1 KB block (mb*KC + kk) of Xt
+// (KC = K/16), lane l at 16 bytes * l.  A wave then loads a fragment with one
+// fully coalesced 16-byte load per lane, straight into registers.  Rows past
+// M (up to the next multiple of 32) are zero.  One thread per 8 halves.
 __global__ void __launch_bounds__(256)
-x_to_f16_kernel(const float *__restrict__ X, _Float16 *__restrict__ Xh, int64_t n8)
+x_tile_kernel(const float *__restrict__ X, int64_t M, int64_t K, _Float16 *__restrict__ Xt, int64_t nslots)
 {
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += (int64_t)gridDim.x * 256) {
-        const f4 a = ldg<f4>(X + 8 * i), b = ldg<f4>(X + 8 * i + 4);
-        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-        *reinterpret_cast<h8 *>(Xh + 8 * i) = pack8(v);
+    const int64_t kc = K / 16;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nslots; i += (int64_t)gridDim.x * 256) {
+        const int l = (int)(i & 63);
+        const int64_t frag = i >> 6;
+        const int64_t mb = frag / kc, kk = frag - mb * kc;
+        const int64_t row = 32 * mb + (l & 31);
+        const int64_t k = 16 * kk + 8 * (l >> 5);
+        h8 v = {};
+        if (row < M) {
+            const f4 a = ldg<f4>(X + row * K + k), b = ldg<f4>(X + row * K + k + 4);
+            const float f[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            v = pack8(f);
+        }
+        *reinterpret_cast<h8 *>(Xt + 8 * i) = v;
     }
 }
 
-// Registers of one K step's staging loads: 64 bytes of X (32 halves of one
-// row) and the packed bytes of one weight piece.
+// Eight waves per workgroup in two roles, one of each on every SIMD.
+//   Consumers (waves 0..3) each own a 64 (M) x 32 (N) sub-tile of the
+//   128 x 64 output tile (two 32x32 accumulators).  They load their A
+//   fragments straight from the tiled fp16 copy of X into registers, three
+//   steps ahead in a ring of four register sets, and read the dequantized
+//   weights (B) from LDS.
+//   Producers (waves 4..7) load the packed weights four steps ahead, dequantize
+//   the next step into the other LDS buffer while the consumers multiply the
+//   current one.
+// One LDS barrier per step joins the roles.  Keeping X out of LDS leaves LDS
+// with the weight tile only (8 KB per step written, 16 KB read).
 template <class T>
-struct Stage {
-    u4 x[4];
-    typename T::Raw w;
-};
-
-template <class T>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(512)
 qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
-             const _Float16 *__restrict__ Xh, int64_t M, float *__restrict__ Y)
+             const _Float16 *__restrict__ Xt, int64_t M, float *__restrict__ Y)
 {
-    __shared__ __align__(16) _Float16 xs[2][BM][LDK];
     __shared__ __align__(16) _Float16 wsh[2][BN][LDK];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool producer = wave >= 4;
     const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
-
-    // staging roles: X row xr, halves 32*xh .. +31 of the step; W row wr, piece wp
-    const int xr = tid >> 1, xh = tid & 1;
-    const int64_t xm = m0 + xr < M ? m0 + xr : M - 1;
-    const _Float16 *xrow = Xh + xm * K + 32 * xh;
-    const int wr = tid >> 2, wp = tid & 3;
-    const int64_t wn = n0 + wr < N ? n0 + wr : N - 1;
-    const uint8_t *wrow = W + wn * row_bytes;
-
-    // wave sub-tile: rows wm .. wm+63 of the M tile, columns wc .. wc+31 of the N tile
-    const int wm = (wave >> 1) * 64, wc = (wave & 1) * 32;
-    const int fr = lane & 31, fk = 8 * (lane >> 5);
-
-    f16v acc0 = {}, acc1 = {};
     const int ns = (int)(K / BK);
 
-    // Loads for step kb (clamped to the last step, so that no load sits behind
-    // a branch and the compiler can wait for exactly the set it consumes).
-    auto gload = [&](int kb, Stage<T> &st) {
+    if (producer) {
+        // The four lanes of a quad share weight row t/4 and take its pieces
+        // 0..3, so they read the same header and the same 32 bytes of codes.
+        const int ptid = tid - 256;
+        const int wr = ptid >> 2, wp = ptid & 3;
+        const int64_t wn = n0 + wr < N ? n0 + wr : N - 1;
+        const uint8_t *wrow = W + wn * row_bytes;
+        // loads for step kb, clamped so that no load sits behind a branch
+        auto gload = [&](int kb, typename T::Raw &r) {
+            kb = kb < ns ? kb : ns - 1;
+            T::load(wrow, kb, wp, r);
+        };
+        auto stage = [&](int buf, int kb, const typename T::Raw &r) {
+            // The step index is hidden from the optimiser: in the unrolled
+            // loop it would otherwise know kb % 4, find some loaded dwords
+            // unused (e.g. the scale bytes of the other sub-blocks), reuse
+            // their registers while the load is in flight and so wait for it.
+            asm volatile("" : "+s"(kb));
+            h8 lo, hi;
+            piece16h<T>(r, kb, wp, lo, hi);
+            *reinterpret_cast<h8 *>(&wsh[buf][wr][16 * wp]) = lo;
+            *reinterpret_cast<h8 *>(&wsh[buf][wr][16 * wp + 8]) = hi;
+        };
+        // Four register sets in a ring: the loads for step kb+4 are issued
+        // while step kb+1 is staged.  The loop has a single exit at the bottom
+        // (an exit between a load and the loop head would make the compiler
+        // wait for every load there); the last one to three steps follow it.
+        typename T::Raw s0, s1, s2, s3;
+        gload(0, s0);
+        gload(1, s1);
+        gload(2, s2);
+        gload(3, s3);
+        stage(0, 0, s0);
+        lds_barrier();
+        int kb = 0;
+        for (; kb + 4 < ns; kb += 4) {
+            gload(kb + 4, s0);
+            __builtin_amdgcn_sched_barrier(0);
+            stage(1, kb + 1, s1);
+            lds_barrier();
+            gload(kb + 5, s1);
+            __builtin_amdgcn_sched_barrier(0);
+            stage(0, kb + 2, s2);
+            lds_barrier();
+            gload(kb + 6, s2);
+            __builtin_amdgcn_sched_barrier(0);
+            stage(1, kb + 3, s3);
+            lds_barrier();
+            gload(kb + 7, s3);
+            __builtin_amdgcn_sched_barrier(0);
+            stage(0, kb + 4, s0);
+            lds_barrier();
+        }
+        if (kb + 1 < ns) {
+            stage(1, kb + 1, s1);
+            lds_barrier();
+        }
+        if (kb + 2 < ns) {
+            stage(0, kb + 2, s2);
+            lds_barrier();
+        }
+        if (kb + 3 < ns) {
+            stage(1, kb + 3, s3);
+            lds_barrier();
+        }
+        return;
+    }
+
+    // consumer: rows wm .. wm+63 of the M tile (M blocks mb0, mb0+1), columns
+    // wc .. wc+31 of the N tile
+    const int wm = (wave >> 1) * 64, wc = (wave & 1) * 32;
+    const int fr = lane & 31, fk = 8 * (lane >> 5);
+    const int64_t kc = K / 16, mblocks = (M + 31) / 32;
+    int64_t mb0 = (m0 + wm) / 32, mb1 = mb0 + 1;
+    mb0 = mb0 < mblocks ? mb0 : mblocks - 1;
+    mb1 = mb1 < mblocks ? mb1 : mblocks - 1;
+    const _Float16 *xa0 = Xt + (mb0 * kc * 64 + lane) * 8;
+    const _Float16 *xa1 = Xt + (mb1 * kc * 64 + lane) * 8;
+    struct AF { h8 a0[4], a1[4]; };
+    auto aload = [&](int kb, AF &f) {
         kb = kb < ns ? kb : ns - 1;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) st.x[i] = ldg<u4>(xrow + (int64_t)kb * BK + 8 * i);
-        T::load(wrow, kb, wp, st.w);
-    };
-    auto stage = [&](int buf, int kb, const Stage<T> &st) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) *reinterpret_cast<u4 *>(&xs[buf][xr][32 * xh + 8 * i]) = st.x[i];
-        float y[16];
-        T::piece(st.w, kb, wp, y);
-        *reinterpret_cast<h8 *>(&wsh[buf][wr][16 * wp]) = pack8(y);
-        *reinterpret_cast<h8 *>(&wsh[buf][wr][16 * wp + 8]) = pack8(y + 8);
-    };
-    auto mfma = [&](int buf) {
-#pragma unroll
-        for (int kk = 0; kk < BK; kk += 16) {
-            const h8 a0 = *reinterpret_cast<const h8 *>(&xs[buf][wm + fr][kk + fk]);
-            const h8 a1 = *reinterpret_cast<const h8 *>(&xs[buf][wm + 32 + fr][kk + fk]);
-            const h8 b = *reinterpret_cast<const h8 *>(&wsh[buf][wc + fr][kk + fk]);
-            acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b, acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b, acc1, 0, 0, 0);
+        for (int kk = 0; kk < 4; ++kk) {
+            f.a0[kk] = ldg<h8>(xa0 + ((int64_t)kb * 4 + kk) * 512);
+            f.a1[kk] = ldg<h8>(xa1 + ((int64_t)kb * 4 + kk) * 512);
         }
     };
-
-    // Two register sets: the loads for step kb+2 are issued while step kb is
-    // multiplied and step kb+1 is staged, so every load has about one and a
-    // half steps to arrive.  The loop has a single exit at the bottom (the
-    // last one or two steps follow it): an exit between a load and the loop
-    // head would make the compiler wait for every load at the head.
-    Stage<T> sa, sb;
-    gload(0, sa);
-    gload(1, sb);
-    stage(0, 0, sa);
+    f16v acc0 = {}, acc1 = {};
+    auto mfma = [&](int buf, const AF &f) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const h8 b = *reinterpret_cast<const h8 *>(&wsh[buf][wc + fr][16 * kk + fk]);
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a0[kk], b, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a1[kk], b, acc1, 0, 0, 0);
+        }
+    };
+    // the same barrier sequence as the producers; A loads three steps ahead
+    AF f0, f1, f2, f3;
+    aload(0, f0);
+    aload(1, f1);
+    aload(2, f2);
     lds_barrier();
     int kb = 0;
-    for (; kb + 2 < ns; kb += 2) {
-        gload(kb + 2, sa);
+    for (; kb + 4 < ns; kb += 4) {
+        aload(kb + 3, f3);
         __builtin_amdgcn_sched_barrier(0);
-        mfma(0);
-        stage(1, kb + 1, sb);
+        mfma(0, f0);
         lds_barrier();
-        gload(kb + 3, sb);
+        aload(kb + 4, f0);
         __builtin_amdgcn_sched_barrier(0);
-        mfma(1);
-        stage(0, kb + 2, sa);
+        mfma(1, f1);
+        lds_barrier();
+        aload(kb + 5, f1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma(0, f2);
+        lds_barrier();
+        aload(kb + 6, f2);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma(1, f3);
         lds_barrier();
     }
-    mfma(0);
+    aload(kb + 3, f3);
+    mfma(0, f0);
     if (kb + 1 < ns) {
-        stage(1, kb + 1, sb);
         lds_barrier();
-        mfma(1);
+        mfma(1, f1);
+    }
+    if (kb + 2 < ns) {
+        lds_barrier();
+        mfma(0, f2);
+    }
+    if (kb + 3 < ns) {
+        lds_barrier();
+        mfma(1, f3);
     }
 
     // acc element r of lane l is C[8*(r/4) + 4*(l/32) + r%4][l%32] of its 32x32 block
@@ -168,7 +250,7 @@ int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t row_byt
 {
     const int64_t gx = (N + BN - 1) / BN, gy = (M + BM - 1) / BM;
     if (gy > 65535 || gx > 0x7FFFFFFF) return AIH_E_LIMIT;
-    hipLaunchKernelGGL((qgemm_kernel<T>), dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, ctx->stream,
+    hipLaunchKernelGGL((qgemm_kernel<T>), dim3((unsigned)gx, (unsigned)gy), dim3(512), 0, ctx->stream,
                        W, N, K, row_bytes, Xh, M, Y);
     return aih_launch_status();
 }
@@ -181,14 +263,15 @@ int aih_launch_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K
     // K advances in 64-element steps.
     if (K % BK != 0) return AIH_E_LIMIT;
     if ((reinterpret_cast<uintptr_t>(X) & 15) != 0) return AIH_E_INVALID;
+    const int64_t mpad = (M + 31) / 32 * 32;
     void *work = nullptr;
-    int rc = aih_workspace(ctx, (size_t)M * (size_t)K * sizeof(_Float16), &work);
+    int rc = aih_workspace(ctx, (size_t)mpad * (size_t)K * sizeof(_Float16), &work);
     if (rc) return rc;
     _Float16 *xh = static_cast<_Float16 *>(work);
-    const int64_t n8 = M * K / 8;
-    const int64_t blocks = (n8 + 255) / 256;
-    const unsigned grid = (unsigned)(blocks < 4096 ? blocks : 4096);
-    hipLaunchKernelGGL(x_to_f16_kernel, dim3(grid), dim3(256), 0, ctx->stream, X, xh, n8);
+    const int64_t nslots = mpad * K / 8;
+    const int64_t blocks = (nslots + 255) / 256;
+    const unsigned grid = (unsigned)(blocks < 8192 ? blocks : 8192);
+    hipLaunchKernelGGL(x_tile_kernel, dim3(grid), dim3(256), 0, ctx->stream, X, M, K, xh, nslots);
     rc = aih_launch_status();
     if (rc) return rc;
     const int64_t rb = aih_row_bytes(type, K);

@@ -234,6 +234,21 @@ def main():
                            "us_per_call": round(s * 1e3, 3),
                            "frac_hbm_peak": round(by / (kern * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
             mb.close()
+        # weight upload (host -> HBM through the pinned staging ring), a load-time
+        # rate that crosses PCIe: reported beside the kernels, never as `value`
+        ub = dev.create_buffer(packed.nbytes)
+        src = np.ascontiguousarray(packed)
+        nat.check(nat.lib().aih_upload_tensor(dev.handle, ub.get_pointer(), src.ctypes.data, src.nbytes), "upload")
+        dev.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(5):
+            nat.check(nat.lib().aih_upload_tensor(dev.handle, ub.get_pointer(), src.ctypes.data, src.nbytes),
+                      "upload")
+        dev.synchronize()
+        el = time.perf_counter() - t0
+        extra["upload_q4_k_14336x4096"] = {"GB/s": round(5 * src.nbytes / el / 1e9, 2),
+                                           "ms_per_call": round(el / 5 * 1e3, 3)}
+        ub.dispose()
         # prefill GEMM: Q4_K W 4096x4096, X 512x4096 (MFMA-bound; fp16 operands, fp32 accumulation)
         gb = GemmBench(dev, nat.Q4_K, 4096, 4096, 512)
         ms = gb.time(10)

@@ -116,8 +116,10 @@ struct Q4K {
     }
     __device__ static void load(const uint8_t *row, int u, uint32_t *raw)
     {
-        const uint8_t *b = row + (u >> 2) * 144;
-        u4 h = ldg<u4>(b), qa = ldg<u4>(b + 16 + (u & 3) * 32), qb = ldg<u4>(b + 32 + (u & 3) * 32);
+        // 32-bit unsigned lane offsets: with `row` wave-uniform the loads take
+        // a scalar base plus a vector offset
+        const uint32_t o = (uint32_t)(u >> 2) * 144u, oq = o + 16u + (uint32_t)(u & 3) * 32u;
+        u4 h = ldg<u4>(row + o), qa = ldg<u4>(row + oq), qb = ldg<u4>(row + (oq + 16u));
         raw[0] = h.x; raw[1] = h.y; raw[2] = h.z; raw[3] = h.w;
         raw[4] = qa.x; raw[5] = qa.y; raw[6] = qa.z; raw[7] = qa.w;
         raw[8] = qb.x; raw[9] = qb.y; raw[10] = qb.z; raw[11] = qb.w;
@@ -177,13 +179,13 @@ struct Q80 {
     __device__ static Step step(int u, int s) { return {64 * u + 4 * s, 4 * (s >> 1) + 2 * (s & 1), s >> 3, false}; }
     __device__ static void load(const uint8_t *row, int u, uint32_t *raw)
     {
-        const uint8_t *p = row + 68 * u;
-        u4 v0 = ldg<u4>(p), v1 = ldg<u4>(p + 16), v2 = ldg<u4>(p + 32), v3 = ldg<u4>(p + 48);
+        const uint32_t o = (uint32_t)u * 68u;
+        u4 v0 = ldg<u4>(row + o), v1 = ldg<u4>(row + (o + 16u)), v2 = ldg<u4>(row + (o + 32u)), v3 = ldg<u4>(row + (o + 48u));
         raw[0] = v0.x; raw[1] = v0.y; raw[2] = v0.z; raw[3] = v0.w;
         raw[4] = v1.x; raw[5] = v1.y; raw[6] = v1.z; raw[7] = v1.w;
         raw[8] = v2.x; raw[9] = v2.y; raw[10] = v2.z; raw[11] = v2.w;
         raw[12] = v3.x; raw[13] = v3.y; raw[14] = v3.z; raw[15] = v3.w;
-        raw[16] = ldg<uint32_t>(p + 64);
+        raw[16] = ldg<uint32_t>(row + (o + 64u));
     }
     template <int B, class XA>
     __device__ static void dot(const uint32_t *raw, const XA &xa, int, float *out)
@@ -232,11 +234,11 @@ struct Q40 {
     }
     __device__ static void load(const uint8_t *row, int u, uint32_t *raw)
     {
-        const uint8_t *p = row + 36 * u;
-        u4 v0 = ldg<u4>(p), v1 = ldg<u4>(p + 16);
+        const uint32_t o = (uint32_t)u * 36u;
+        u4 v0 = ldg<u4>(row + o), v1 = ldg<u4>(row + (o + 16u));
         raw[0] = v0.x; raw[1] = v0.y; raw[2] = v0.z; raw[3] = v0.w;
         raw[4] = v1.x; raw[5] = v1.y; raw[6] = v1.z; raw[7] = v1.w;
-        raw[8] = ldg<uint32_t>(p + 32);
+        raw[8] = ldg<uint32_t>(row + (o + 32u));
     }
     template <int B, class XA>
     __device__ static void dot(const uint32_t *raw, const XA &xa, int, float *out)
@@ -291,16 +293,16 @@ struct Q6K {
     }
     __device__ static void load(const uint8_t *row, int u, uint32_t *raw)
     {
-        const uint8_t *b = row + (u >> 2) * 210;
-        const int h = (u >> 1) & 1, t = u & 1;
-        u4 qa = ldg<u4>(b + 64 * h + 16 * t), qb = ldg<u4>(b + 64 * h + 32 + 16 * t);
-        u4 qh = ldg<u4>(b + 128 + 32 * h + 16 * t);
-        uint64_t sc = ldg<uint64_t>(b + 192 + 8 * h);
+        const uint32_t o = (uint32_t)(u >> 2) * 210u, h = (uint32_t)(u >> 1) & 1u, t = (uint32_t)u & 1u;
+        const uint32_t oq = o + 64u * h + 16u * t;
+        u4 qa = ldg<u4>(row + oq), qb = ldg<u4>(row + (oq + 32u));
+        u4 qh = ldg<u4>(row + (o + 128u + 32u * h + 16u * t));
+        uint64_t sc = ldg<uint64_t>(row + (o + 192u + 8u * h));
         raw[0] = qa.x; raw[1] = qa.y; raw[2] = qa.z; raw[3] = qa.w;
         raw[4] = qb.x; raw[5] = qb.y; raw[6] = qb.z; raw[7] = qb.w;
         raw[8] = qh.x; raw[9] = qh.y; raw[10] = qh.z; raw[11] = qh.w;
         raw[12] = (uint32_t)sc; raw[13] = (uint32_t)(sc >> 32);
-        raw[14] = ldg<uint16_t>(b + 208);
+        raw[14] = ldg<uint16_t>(row + (o + 208u));
     }
     template <int B, class XA>
     __device__ static void dot(const uint32_t *raw, const XA &xa, int u, float *out)
@@ -409,16 +411,24 @@ struct Geom {
 // Team t of workgroup w visits the row groups c = w, w + gridDim.x, ... and
 // computes row c*TEAMS + t of each.
 //
-// Software pipeline: before a row is computed, the packed bytes of the
-// team's next row are loaded into the other of two register buffers, so a
-// wave always has one row of loads in flight while it computes.  The loop is
-// unrolled twice so that each buffer keeps fixed registers.
+// Software pipeline: the packed bytes of the team's first row are loaded
+// before the activation conversion and its second row right after; from then
+// on each of the two register buffers is reloaded with the row two ahead as
+// soon as its row is computed, so a wave always has one row of loads in
+// flight while it computes.  The loop is unrolled twice so that each buffer
+// keeps fixed registers.
 //
-// No load sits behind a data-dependent branch (the compiler could then no
-// longer count outstanding loads and would wait for all of them): after the
-// last row group the prefetch re-reads the team's current row, which is
-// still in L2.  Loads complete in issue order, so waiting for the current
-// row leaves the prefetch in flight; the activation loads are issued first.
+// Loads complete in issue order, so waiting for the current row leaves the
+// other buffer's loads in flight; the activation loads are issued first.
+// The compiler can only rely on that where the order is the same on every
+// path into a wait, hence:
+//   - no load sits behind a data-dependent branch inside the loop, and the
+//     loop runs only while both of its reloads are real rows; the last one
+//     to three rows are computed after it in straight-line code;
+//   - the loop has a single exit, at the bottom, on scalar row-group
+//     indices: a loop with two exits is compiled with a flow block whose
+//     (never taken) path back to the head skips half of the body, and the
+//     compiler then waits at the head for loads meant to stay in flight.
 // W is deliberately not __restrict__: that would let the compiler sink the
 // first weight loads below the LDS barrier of the activation exchange.
 template <class T, int B, int TEAMS, bool ONEWAVE, int MAXT>
@@ -433,14 +443,15 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
     const int lane = tid & 63, wave = tid >> 6;
     const int wr = ONEWAVE ? 1 : geo.wr;
     const int team_threads = wr * 64;
+    // (The team index is wave-uniform, but making it a scalar with
+    // readfirstlane measured 0.4 us slower per launch on MI355X.)
     const int team = TEAMS == 1 ? 0 : tid / team_threads;
     const int ut = tid - team * team_threads;   // unit index within the team
     const bool active = ut < geo.units;
     const int u = active ? ut : 0;
     const int64_t ngroups = (N + TEAMS - 1) / TEAMS;
-    const int64_t g = gridDim.x;
-    auto row_of = [&](int64_t c) {
-        const int64_t n = c * TEAMS + team;
+    auto row_of = [&](int c) {
+        const int64_t n = (int64_t)c * TEAMS + team;
         return n < N ? n : N - 1;
     };
 
@@ -452,10 +463,15 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
     for (int b = 0; b < B; ++b)
 #pragma unroll
         for (int k = 0; k < NST; ++k) xv[b][k] = ldg<f4>(X + b * ldx + T::step(u, team * NST + k).src);
-    int64_t c = blockIdx.x;
-    int64_t n_cur = row_of(c);
+    // The team visits row groups blockIdx.x + i*g while below ngroups (the
+    // host launches at most ngroups workgroups and at most 64 row groups per
+    // workgroup, so the indices fit in 32 bits and live in scalar registers).
+    // A load past the end (only rb's first load, for a team of one row)
+    // re-reads `fallback`, a row already loaded.
+    const int ng = (int)ngroups, g = (int)gridDim.x, c0 = (int)blockIdx.x;
+    auto row_ptr = [&](int cc, int fallback) { return W + row_of(cc < ng ? cc : fallback) * row_bytes; };
     uint32_t ra[T::kRaw], rb[T::kRaw];
-    T::load(W + n_cur * row_bytes, u, ra);
+    T::load(row_ptr(c0, c0), u, ra);
     // keep the weight loads here, in flight during the conversion below
     __builtin_amdgcn_sched_barrier(0);
 
@@ -515,7 +531,6 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
     float yb[B];
 #pragma unroll
     for (int b = 0; b < B; ++b) yb[b] = 0.f;
-    const int64_t c_first = c;
     int kept = 0;
 
     // Dot product of one row, reduced over the team into yb.  `par`
@@ -549,37 +564,37 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
         ++kept;
     };
 
-    // The address of each prefetch is computed half an iteration ahead, while
-    // both register buffers are live, so the loop head holds nothing but the
-    // loads (temporaries placed in a just-consumed buffer would make the
-    // compiler wait for that buffer's earlier loads).
-    auto next_ptr = [&](int64_t cc, int64_t n_now) {
-        const int64_t cn = cc + g;
-        return W + (cn < ngroups ? row_of(cn) : n_now) * row_bytes;
-    };
-    int64_t n_next = c + g < ngroups ? row_of(c + g) : n_cur;
-    const uint8_t *p_next = W + n_next * row_bytes;
-    for (;;) {
-        T::load(p_next, u, rb);
-        __builtin_amdgcn_sched_barrier(0);   // prefetch issued before the row is consumed
-        const int64_t cn = c + g;
-        const int64_t n_after = cn < ngroups ? row_of(cn) : n_cur;
-        p_next = next_ptr(cn, n_after);
+    // The loop runs while both reloads are real rows; the last one to three
+    // rows are computed after it with exact loads, so no past-the-end load
+    // is issued after the final row (its latency would then be exposed).
+    // The second row is loaded only now: issued before the conversion as
+    // well, it measured 0.35 us slower on MI355X for teams of 3-4 rows.
+    T::load(row_ptr(c0 + g, c0), u, rb);
+    __builtin_amdgcn_sched_barrier(0);
+    int c = c0;   // ra holds row group c, rb row group c + g
+    while (c + 3 * g < ng) {
         row(ra, 0);
-        if (cn >= ngroups) break;
-        c = cn;
-        n_cur = n_after;
-        T::load(p_next, u, ra);
-        __builtin_amdgcn_sched_barrier(0);
-        const int64_t cn2 = c + g;
-        const int64_t n_after2 = cn2 < ngroups ? row_of(cn2) : n_cur;
-        p_next = next_ptr(cn2, n_after2);
+        T::load(row_ptr(c + 2 * g, c), u, ra);
+        __builtin_amdgcn_sched_barrier(0);   // reload issued before the other row is consumed
         row(rb, 1);
-        if (cn2 >= ngroups) break;
-        c = cn2;
-        n_cur = n_after2;
+        T::load(row_ptr(c + 3 * g, c + g), u, rb);
+        __builtin_amdgcn_sched_barrier(0);
+        c += 2 * g;
     }
-    const int64_t n = (c_first + (int64_t)lane * g) * TEAMS + team;
+    // here c < ng (c0 < ng, and every iteration leaves c + g < ng)
+    if (c + 2 * g < ng) {
+        row(ra, 0);
+        T::load(row_ptr(c + 2 * g, c), u, ra);
+        __builtin_amdgcn_sched_barrier(0);
+        row(rb, 1);
+        row(ra, 0);
+    } else if (c + g < ng) {
+        row(ra, 0);
+        row(rb, 1);
+    } else {
+        row(ra, 0);
+    }
+    const int64_t n = (c0 + (int64_t)lane * g) * TEAMS + team;
     if (leader && lane < kept && n < N) {
 #pragma unroll
         for (int b = 0; b < B; ++b) Y[b * ldy + n] = yb[b];

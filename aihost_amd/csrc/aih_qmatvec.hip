@@ -612,9 +612,10 @@ Geom make_geom(int64_t K)
 
 // One launch of one workgroup per CU: every workgroup pays the activation
 // conversion once, so fewer, longer-lived workgroups win.  On MI355X
-// (14336 x 4096 Q4_K) one workgroup of eight single-wave teams per CU ran
-// 7.9 us, against 8.2 us with two per CU, 9.5 us with one 16-team
-// workgroup per CU and 9.5-11.7 us with 4-7 workgroups per CU.
+// (14336 x 4096 Q4_K, measured with an earlier form of the row loop) one
+// workgroup of eight single-wave teams per CU ran 7.9 us, against 8.2 us
+// with two per CU, 9.5 us with one 16-team workgroup per CU and 9.5-11.7 us
+// with 4-7 workgroups per CU.
 template <class T, int B, int TEAMS, bool ONEWAVE, int MAXT>
 int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
            const float *X, int64_t ldx, float *Y, int64_t ldy)

@@ -86,6 +86,43 @@ __device__ __forceinline__ T ldg(const void *p)
     return v;
 }
 
+// Row addressing for the weight loads, in two forms with the same interface
+// (16/8/4/2-byte loads at a 32-bit byte offset):
+//   PtrRow - a per-lane 64-bit pointer to the row; offsets are added to it.
+//   BufRow - a buffer resource over the launch's slice of W, with the row's
+//            32-bit offset in a scalar register (soffset) and the lane offset
+//            in a vector register (voffset): no 64-bit address arithmetic on
+//            the vector ALUs.  Accesses past num_records read zeros.  Word 3
+//            (0x00020000) is the raw-buffer configuration of the gfx9 family.
+// Single-wave teams use PtrRow and multi-wave teams BufRow: on MI355X the
+// buffer form ran 0.85 us faster on Q6_K 4096 x 14336 (four-wave teams) but
+// 0.2 us slower on the single-wave-team kernel for matrices of 7-14k rows
+// (any form with the row base in a scalar register did).
+struct PtrRow {
+    const uint8_t *p;
+    __device__ __forceinline__ u4 ld16(uint32_t o) const { return ldg<u4>(p + o); }
+    __device__ __forceinline__ uint64_t ld8(uint32_t o) const { return ldg<uint64_t>(p + o); }
+    __device__ __forceinline__ uint32_t ld4(uint32_t o) const { return ldg<uint32_t>(p + o); }
+    __device__ __forceinline__ uint32_t ld2(uint32_t o) const { return ldg<uint16_t>(p + o); }
+};
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+__device__ __forceinline__ Rsrc make_rsrc(const uint8_t *base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), (short)0, (int)bytes, 0x00020000);
+}
+struct BufRow {
+    Rsrc r;
+    uint32_t soff;
+    __device__ __forceinline__ u4 ld16(uint32_t o) const { return __builtin_amdgcn_raw_buffer_load_b128(r, o, soff, 0); }
+    __device__ __forceinline__ uint64_t ld8(uint32_t o) const
+    {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, o, soff, 0);
+        return (uint64_t)v[0] | ((uint64_t)v[1] << 32);
+    }
+    __device__ __forceinline__ uint32_t ld4(uint32_t o) const { return __builtin_amdgcn_raw_buffer_load_b32(r, o, soff, 0); }
+    __device__ __forceinline__ uint32_t ld2(uint32_t o) const { return __builtin_amdgcn_raw_buffer_load_b16(r, o, soff, 0); }
+};
+
 // One prep step turns 4 consecutive activations x[src..src+3] (one 16-byte
 // load) into the fp16 pairs (x0, x2) and (x1, x3), stored at image dwords d0
 // and d0+1, and adds their sum to sum slot `slot`.  Steps with div16 feed
@@ -114,12 +151,12 @@ struct Q4K {
         if (s < 8) return {64 * u + 4 * s, 4 * s, 0, false};
         return {64 * u + 32 + 4 * (s - 8), 4 * (s - 8) + 2, 1, true};
     }
-    __device__ static void load(const uint8_t *row, int u, uint32_t *raw)
+    // The row starts at byte `off` of `w`; lane offsets are added to off.
+    template <class A>
+    __device__ static void load(const A &w, uint32_t off, int u, uint32_t *raw)
     {
-        // 32-bit unsigned lane offsets: with `row` wave-uniform the loads take
-        // a scalar base plus a vector offset
-        const uint32_t o = (uint32_t)(u >> 2) * 144u, oq = o + 16u + (uint32_t)(u & 3) * 32u;
-        u4 h = ldg<u4>(row + o), qa = ldg<u4>(row + oq), qb = ldg<u4>(row + (oq + 16u));
+        const uint32_t o = off + (uint32_t)(u >> 2) * 144u, oq = o + 16u + (uint32_t)(u & 3) * 32u;
+        u4 h = w.ld16(o), qa = w.ld16(oq), qb = w.ld16(oq + 16u);
         raw[0] = h.x; raw[1] = h.y; raw[2] = h.z; raw[3] = h.w;
         raw[4] = qa.x; raw[5] = qa.y; raw[6] = qa.z; raw[7] = qa.w;
         raw[8] = qb.x; raw[9] = qb.y; raw[10] = qb.z; raw[11] = qb.w;
@@ -177,15 +214,16 @@ struct Q80 {
     static constexpr int kRaw = 17;
     static constexpr int kSums = 2;
     __device__ static Step step(int u, int s) { return {64 * u + 4 * s, 4 * (s >> 1) + 2 * (s & 1), s >> 3, false}; }
-    __device__ static void load(const uint8_t *row, int u, uint32_t *raw)
+    template <class A>
+    __device__ static void load(const A &w, uint32_t off, int u, uint32_t *raw)
     {
-        const uint32_t o = (uint32_t)u * 68u;
-        u4 v0 = ldg<u4>(row + o), v1 = ldg<u4>(row + (o + 16u)), v2 = ldg<u4>(row + (o + 32u)), v3 = ldg<u4>(row + (o + 48u));
+        const uint32_t o = off + (uint32_t)u * 68u;
+        u4 v0 = w.ld16(o), v1 = w.ld16(o + 16u), v2 = w.ld16(o + 32u), v3 = w.ld16(o + 48u);
         raw[0] = v0.x; raw[1] = v0.y; raw[2] = v0.z; raw[3] = v0.w;
         raw[4] = v1.x; raw[5] = v1.y; raw[6] = v1.z; raw[7] = v1.w;
         raw[8] = v2.x; raw[9] = v2.y; raw[10] = v2.z; raw[11] = v2.w;
         raw[12] = v3.x; raw[13] = v3.y; raw[14] = v3.z; raw[15] = v3.w;
-        raw[16] = ldg<uint32_t>(row + (o + 64u));
+        raw[16] = w.ld4(o + 64u);
     }
     template <int B, class XA>
     __device__ static void dot(const uint32_t *raw, const XA &xa, int, float *out)
@@ -232,13 +270,14 @@ struct Q40 {
         if (r < 4) return {64 * u + 32 * blk + 4 * r, 4 * (4 * blk + r), blk, false};
         return {64 * u + 32 * blk + 16 + 4 * (r - 4), 4 * (4 * blk + r - 4) + 2, 2 + blk, true};
     }
-    __device__ static void load(const uint8_t *row, int u, uint32_t *raw)
+    template <class A>
+    __device__ static void load(const A &w, uint32_t off, int u, uint32_t *raw)
     {
-        const uint32_t o = (uint32_t)u * 36u;
-        u4 v0 = ldg<u4>(row + o), v1 = ldg<u4>(row + (o + 16u));
+        const uint32_t o = off + (uint32_t)u * 36u;
+        u4 v0 = w.ld16(o), v1 = w.ld16(o + 16u);
         raw[0] = v0.x; raw[1] = v0.y; raw[2] = v0.z; raw[3] = v0.w;
         raw[4] = v1.x; raw[5] = v1.y; raw[6] = v1.z; raw[7] = v1.w;
-        raw[8] = ldg<uint32_t>(row + (o + 32u));
+        raw[8] = w.ld4(o + 32u);
     }
     template <int B, class XA>
     __device__ static void dot(const uint32_t *raw, const XA &xa, int, float *out)
@@ -291,18 +330,19 @@ struct Q6K {
         const int base = (u >> 2) * 256 + 128 * ((u >> 1) & 1) + 16 * (u & 1);
         return {base + 32 * q + 4 * m, 4 * (2 * m + (q >> 1)) + 2 * (q & 1), q, q >= 2};
     }
-    __device__ static void load(const uint8_t *row, int u, uint32_t *raw)
+    template <class A>
+    __device__ static void load(const A &w, uint32_t off, int u, uint32_t *raw)
     {
-        const uint32_t o = (uint32_t)(u >> 2) * 210u, h = (uint32_t)(u >> 1) & 1u, t = (uint32_t)u & 1u;
+        const uint32_t o = off + (uint32_t)(u >> 2) * 210u, h = (uint32_t)(u >> 1) & 1u, t = (uint32_t)u & 1u;
         const uint32_t oq = o + 64u * h + 16u * t;
-        u4 qa = ldg<u4>(row + oq), qb = ldg<u4>(row + (oq + 32u));
-        u4 qh = ldg<u4>(row + (o + 128u + 32u * h + 16u * t));
-        uint64_t sc = ldg<uint64_t>(row + (o + 192u + 8u * h));
+        u4 qa = w.ld16(oq), qb = w.ld16(oq + 32u);
+        u4 qh = w.ld16(o + 128u + 32u * h + 16u * t);
+        const uint64_t sc = w.ld8(o + 192u + 8u * h);
         raw[0] = qa.x; raw[1] = qa.y; raw[2] = qa.z; raw[3] = qa.w;
         raw[4] = qb.x; raw[5] = qb.y; raw[6] = qb.z; raw[7] = qb.w;
         raw[8] = qh.x; raw[9] = qh.y; raw[10] = qh.z; raw[11] = qh.w;
         raw[12] = (uint32_t)sc; raw[13] = (uint32_t)(sc >> 32);
-        raw[14] = ldg<uint16_t>(row + (o + 208u));
+        raw[14] = w.ld2(o + 208u);
     }
     template <int B, class XA>
     __device__ static void dot(const uint32_t *raw, const XA &xa, int u, float *out)
@@ -449,10 +489,19 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
     const int ut = tid - team * team_threads;   // unit index within the team
     const bool active = ut < geo.units;
     const int u = active ? ut : 0;
-    const int64_t ngroups = (N + TEAMS - 1) / TEAMS;
-    auto row_of = [&](int c) {
-        const int64_t n = (int64_t)c * TEAMS + team;
-        return n < N ? n : N - 1;
+    // N is a multiple of TEAMS (the host computes a ragged remainder with
+    // the single-team variant), so every team's row c*TEAMS + team exists.
+    // The host keeps a launch's slice of W below 2^31 bytes.
+    const int64_t ngroups = N / TEAMS;
+    const uint32_t toff = (uint32_t)team * (uint32_t)row_bytes;
+    const Rsrc wres = make_rsrc(W, (uint32_t)(N * row_bytes));
+    const uint32_t gstride = (uint32_t)(TEAMS * row_bytes);   // bytes per row group
+    // loads of the team's row in row group cc (see PtrRow / BufRow)
+    auto load_group = [&](int cc, uint32_t *raw) {
+        if constexpr (ONEWAVE)
+            T::load(PtrRow{W + ((int64_t)cc * TEAMS + team) * row_bytes}, 0u, u, raw);
+        else
+            T::load(BufRow{wres, (uint32_t)cc * gstride}, toff, u, raw);
     };
 
     // The 16 conversion steps of every unit are spread over the teams; a
@@ -467,11 +516,10 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
     // host launches at most ngroups workgroups and at most 64 row groups per
     // workgroup, so the indices fit in 32 bits and live in scalar registers).
     // A load past the end (only rb's first load, for a team of one row)
-    // re-reads `fallback`, a row already loaded.
+    // re-reads the team's first row instead.
     const int ng = (int)ngroups, g = (int)gridDim.x, c0 = (int)blockIdx.x;
-    auto row_ptr = [&](int cc, int fallback) { return W + row_of(cc < ng ? cc : fallback) * row_bytes; };
     uint32_t ra[T::kRaw], rb[T::kRaw];
-    T::load(row_ptr(c0, c0), u, ra);
+    load_group(c0, ra);
     // keep the weight loads here, in flight during the conversion below
     __builtin_amdgcn_sched_barrier(0);
 
@@ -569,22 +617,22 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
     // is issued after the final row (its latency would then be exposed).
     // The second row is loaded only now: issued before the conversion as
     // well, it measured 0.35 us slower on MI355X for teams of 3-4 rows.
-    T::load(row_ptr(c0 + g, c0), u, rb);
+    load_group(c0 + g < ng ? c0 + g : c0, rb);
     __builtin_amdgcn_sched_barrier(0);
     int c = c0;   // ra holds row group c, rb row group c + g
     while (c + 3 * g < ng) {
         row(ra, 0);
-        T::load(row_ptr(c + 2 * g, c), u, ra);
+        load_group(c + 2 * g, ra);
         __builtin_amdgcn_sched_barrier(0);   // reload issued before the other row is consumed
         row(rb, 1);
-        T::load(row_ptr(c + 3 * g, c + g), u, rb);
+        load_group(c + 3 * g, rb);
         __builtin_amdgcn_sched_barrier(0);
         c += 2 * g;
     }
     // here c < ng (c0 < ng, and every iteration leaves c + g < ng)
     if (c + 2 * g < ng) {
         row(ra, 0);
-        T::load(row_ptr(c + 2 * g, c), u, ra);
+        load_group(c + 2 * g, ra);
         __builtin_amdgcn_sched_barrier(0);
         row(rb, 1);
         row(ra, 0);
@@ -625,15 +673,34 @@ int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t row_bytes, Geom ge
     const int64_t cap = ctx->cu_count > 0 ? ctx->cu_count : 256;
     // A workgroup computes at most 64 row groups per launch (its results are
     // held in one register per lane); taller matrices take several launches.
-    const int64_t rows_per_launch = cap * 64 * TEAMS;
-    for (int64_t r0 = 0; r0 < N; r0 += rows_per_launch) {
-        const int64_t nr = N - r0 < rows_per_launch ? N - r0 : rows_per_launch;
-        const int64_t ng = (nr + TEAMS - 1) / TEAMS;
+    // The kernel needs N to be a multiple of TEAMS; the last N % TEAMS rows
+    // go to the single-team variant, one launch per column.
+    const int64_t nmain = N - N % TEAMS;
+    // at most 64 row groups per workgroup, and a slice of W below 2^31 bytes
+    // (the kernel's buffer resource and offsets are 32-bit)
+    int64_t rows_per_launch = cap * 64 * TEAMS;
+    const int64_t by_bytes = (0x7FFFFFFFll / row_bytes) / TEAMS * TEAMS;
+    if (by_bytes < rows_per_launch) rows_per_launch = by_bytes;
+    if (rows_per_launch <= 0) return AIH_E_LIMIT;
+    for (int64_t r0 = 0; r0 < nmain; r0 += rows_per_launch) {
+        const int64_t nr = nmain - r0 < rows_per_launch ? nmain - r0 : rows_per_launch;
+        const int64_t ng = nr / TEAMS;
         const int64_t grid = ng < cap ? ng : cap;
         hipLaunchKernelGGL((qmatvec_kernel<T, B, TEAMS, ONEWAVE, MAXT>), dim3((unsigned)grid), dim3(threads), lds,
                            ctx->stream, W + r0 * row_bytes, nr, row_bytes, geo, X, ldx, Y + r0, ldy);
         const int rc = aih_launch_status();
         if (rc) return rc;
+    }
+    if constexpr (TEAMS > 1) {
+        if (nmain < N) {
+            Geom g1 = geo;
+            g1.teams = 1;
+            for (int b = 0; b < B; ++b) {
+                const int rc = launch<T, 1, 1, false, 1024>(ctx, W + nmain * row_bytes, N - nmain, row_bytes, g1,
+                                                            X + b * ldx, ldx, Y + b * ldy + nmain, ldy);
+                if (rc) return rc;
+            }
+        }
     }
     return AIH_OK;
 }

@@ -62,6 +62,18 @@ SIGNATURES = {
     "aih_qmatvec": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i]),
     "aih_qgemm": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),
     "aih_matmul_weights_q": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),
+    "aih_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _i64, _i64, _f]),
+    "aih_rope_table": (_i, [_vp, _vp, ctypes.c_int32, ctypes.c_int32, _f]),
+    "aih_rope": (_i, [_vp, _vp, _i64, _vp, _i64, _i64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _vp, _vp,
+                      ctypes.c_int32, _i, _i64]),
+    "aih_store_rows": (_i, [_vp, _vp, _i64, _i64, _vp, _i64, ctypes.c_int32, _vp]),
+    "aih_silu_mul": (_i, [_vp, _vp, _vp, _vp, _i64]),
+    "aih_add": (_i, [_vp, _vp, _vp, _vp, _i64]),
+    "aih_attention_scratch_floats": (_i64, [ctypes.c_int32, ctypes.c_int32]),
+    "aih_attention": (_i, [_vp, _vp, _vp, _vp, _vp, _i64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                           ctypes.c_int32, _vp, ctypes.c_int32, _f, _vp, _i64]),
+    "aih_embed_q": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),
+    "aih_argmax": (_i, [_vp, _vp, _i64, _vp, _vp, _vp, _i64, ctypes.c_int32]),
     "aih_sync": (_i, [_vp]),
     "aih_stream": (_vp, [_vp]),
     "aih_capture_begin": (_i, [_vp]),

@@ -28,8 +28,9 @@ HIP_FLAGS = [
     # packed fp32 VALU forms stay off for every kernel in this library
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
-# Per-file extras: the bit-exact dequantizer must not contract a*b-c into FMA.
-EXTRA = {"aih_dequant.hip": ["-ffp-contract=off"]}
+# Per-file extras: the bit-exact dequantizer must not contract a*b-c into FMA;
+# the decoder operators round their element-wise formulas like the reference.
+EXTRA = {"aih_dequant.hip": ["-ffp-contract=off"], "aih_decoder.hip": ["-ffp-contract=off"]}
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-pthread"]
 
 

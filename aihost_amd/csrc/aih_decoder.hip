@@ -1,0 +1,519 @@
+// aih_decoder.hip -- the non-matmul operators of a Llama decoder layer, so
+// that a whole decode step (and prefill) runs on the device around the fused
+// quantized matmuls:
+//
+//   RMSNorm            ComputeOps.LayerNorm (ComputeOps.cs:517-542),
+//                      shader ComputeShaders.cs:247-278
+//   RoPE (interleaved) ComputeOps.ApplyRoPEFull (ComputeOps.cs:959-979),
+//                      shader ComputeShaders.cs:517-543
+//   causal GQA attention   ComputeOps.MultiHeadAttention (ComputeOps.cs:1055-1102)
+//                      and FusedMHAGenerate (ComputeOps.cs:1015-1043, shader
+//                      ComputeShaders.cs:656-733)
+//   SiLU(gate) * up, residual add   ComputeOps.FeedForward / Add
+//                      (ComputeOps.cs:1218-1241, 389-...), shaders
+//                      ComputeShaders.cs:280-320
+//   KV cache append    KVCache.Add (InferenceEngine.cs:598-622), here an
+//                      in-place row store instead of an O(L^2) concat
+//   greedy argmax      the sampling step of InferenceEngine for a greedy
+//                      configuration
+//
+// Positions.  Every position-dependent operator takes `start` and an
+// optional device pointer `pos`: the position of row r is start + r, plus
+// *pos when pos is not null.  A decode step captured into a HIP graph reads
+// its position from device memory, and the argmax operator advances it, so
+// the graph can be replayed token after token without the host.
+//
+// This file is compiled without FMA contraction, so that the element-wise
+// formulas round like the reference's (x / rms * w, x1*c - x2*s, ...);
+// attention contracts its dot products with explicit fmaf.
+#include "aih_internal.h"
+
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int32_t dev_pos(int32_t start, const int32_t *pos)
+{
+    return pos ? start + *pos : start;
+}
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// Sum over a workgroup of `NT` threads (multiple of 64); every thread gets it.
+template <int NT>
+__device__ __forceinline__ float block_sum(float v, float *red)
+{
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < NT / 64; ++i) t += red[i];
+    return t;
+}
+
+// ---------------------------------------------------------------- RMSNorm
+// One workgroup per row: rms = sqrt(sum(x^2)/cols + eps); y = (x / rms) * w.
+// Y may alias X.
+template <bool VEC>
+__global__ void __launch_bounds__(256)
+rmsnorm_kernel(const float *X, const float *__restrict__ Wt, float *Y, int64_t cols, float eps)
+{
+    __shared__ float red[4];
+    const float *x = X + (int64_t)blockIdx.x * cols;
+    float *y = Y + (int64_t)blockIdx.x * cols;
+    float ss = 0.f;
+    if (VEC) {
+        const f4 *x4 = reinterpret_cast<const f4 *>(x);
+        for (int64_t i = threadIdx.x; i < cols / 4; i += 256) {
+            const f4 v = x4[i];
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+    } else {
+        for (int64_t i = threadIdx.x; i < cols; i += 256) ss += x[i] * x[i];
+    }
+    ss = block_sum<256>(ss, red);
+    const float rms = sqrtf(ss / (float)cols + eps);
+    if (VEC) {
+        const f4 *x4 = reinterpret_cast<const f4 *>(x);
+        const f4 *w4 = reinterpret_cast<const f4 *>(Wt);
+        f4 *y4 = reinterpret_cast<f4 *>(y);
+        for (int64_t i = threadIdx.x; i < cols / 4; i += 256) {
+            const f4 v = x4[i], w = w4[i];
+            f4 o;
+            o.x = (v.x / rms) * w.x;
+            o.y = (v.y / rms) * w.y;
+            o.z = (v.z / rms) * w.z;
+            o.w = (v.w / rms) * w.w;
+            y4[i] = o;
+        }
+    } else {
+        for (int64_t i = threadIdx.x; i < cols; i += 256) y[i] = (x[i] / rms) * Wt[i];
+    }
+}
+
+// ---------------------------------------------------------------- RoPE
+// Table of (cos, sin) per (position, pair): angle = (float)pos * freq with
+// freq = 1 / theta^((2i)/d) -- the reference's fp32 formula -- where the
+// power, cosine and sine are evaluated in double and rounded to float.
+__global__ void __launch_bounds__(256)
+rope_table_kernel(float *table, int32_t max_pos, int32_t head_dim, float theta)
+{
+    const int half = head_dim / 2;
+    const int64_t total = (int64_t)max_pos * half;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+        const int32_t pos = (int32_t)(t / half), i = (int32_t)(t % half);
+        const float e = (float)(2 * i) / (float)head_dim;
+        const float pw = (float)pow((double)theta, (double)e);
+        const float freq = 1.0f / pw;
+        const float ang = (float)pos * freq;
+        table[2 * t] = (float)cos((double)ang);
+        table[2 * t + 1] = (float)sin((double)ang);
+    }
+}
+
+// Pair (2i, 2i+1) of head h of row r at position p:
+//   y0 = x0*c - x1*s,  y1 = x0*s + x1*c.
+// The output row is r, or the position p itself when y_at_pos (the row of a
+// KV cache); rows at or past y_rows are not written.
+__global__ void __launch_bounds__(256)
+rope_kernel(const float *X, int64_t ldx, float *Y, int64_t ldy, int64_t rows, int32_t n_heads, int32_t head_dim,
+            int32_t start, const int32_t *pos, const float *__restrict__ table, int32_t table_rows, int y_at_pos,
+            int64_t y_rows)
+{
+    const int half = head_dim / 2;
+    const int64_t per_row = (int64_t)n_heads * half;
+    const int64_t total = rows * per_row;
+    const int32_t p0 = dev_pos(start, pos);
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = t / per_row, rem = t % per_row;
+        const int h = (int)(rem / half), i = (int)(rem % half);
+        const int64_t p = p0 + r;
+        if (p < 0 || p >= table_rows) continue;
+        const int64_t yr = y_at_pos ? p : r;
+        if (yr >= y_rows) continue;
+        const float c = table[2 * (p * half + i)], s = table[2 * (p * half + i) + 1];
+        const float *x = X + r * ldx + (int64_t)h * head_dim + 2 * i;
+        float *y = Y + yr * ldy + (int64_t)h * head_dim + 2 * i;
+        const float x0 = x[0], x1 = x[1];
+        y[0] = x0 * c - x1 * s;
+        y[1] = x0 * s + x1 * c;
+    }
+}
+
+// ---------------------------------------------------------------- row store
+// Y[(p + r) * cols + c] = X[r * cols + c] for rows whose position p + r is
+// below y_rows (a KV cache append).
+__global__ void __launch_bounds__(256)
+store_rows_kernel(const float *__restrict__ X, int64_t rows, int64_t cols, float *__restrict__ Y, int64_t y_rows,
+                  int32_t start, const int32_t *pos)
+{
+    const int64_t p0 = dev_pos(start, pos);
+    const int64_t total = rows * cols;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = t / cols;
+        if (p0 + r >= 0 && p0 + r < y_rows) Y[(p0 + r) * cols + t % cols] = X[t];
+    }
+}
+
+// ---------------------------------------------------------------- SiLU * up, add
+__global__ void __launch_bounds__(256)
+silu_mul_kernel(const float *G, const float *U, float *Y, int64_t n)
+{
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const float g = G[i];
+        const float sig = 1.0f / (1.0f + expf(-g));
+        Y[i] = (g * sig) * U[i];
+    }
+}
+
+__global__ void __launch_bounds__(256)
+add_kernel(const float *A, const float *B, float *Y, int64_t n)
+{
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        Y[i] = A[i] + B[i];
+}
+
+// ---------------------------------------------------------------- attention
+// Query row i (position p_i = p0 + i) of head h attends to cache rows
+// 0..p_i of KV head h / (n_heads / n_kv_heads):
+//   o = sum_j softmax_j(scale * q.k_j) v_j.
+// Q/O rows hold n_heads*head_dim floats, K/V cache rows n_kv_heads*head_dim.
+
+constexpr int kHD = 128;      // head_dim supported by the attention kernels
+constexpr int kChunk = 64;    // keys per decode split (upper bound)
+constexpr int kQTile = 64;    // queries per prefill workgroup
+
+// Decode, split over keys: workgroup (h, s) of 256 threads handles the keys of
+// split s (ceil(L / n_split) of them, at most kChunk) and writes its partial
+// (max, sum, unnormalised output) to scratch.  Thread t: key t/4, dims
+// 32*(t%4) .. +31.
+__global__ void __launch_bounds__(256)
+attn_decode_partial(const float *__restrict__ Q, const float *__restrict__ Kc, const float *__restrict__ Vc,
+                    float *__restrict__ part, int32_t n_heads, int32_t n_kv_heads, int32_t start,
+                    const int32_t *pos, int32_t max_len, float scale, int32_t n_split)
+{
+    __shared__ float qs[kHD];
+    __shared__ float ps[kChunk];
+    __shared__ float red[4];
+    __shared__ float accs[2][kHD];
+    const int h = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
+    const int kvh = h / (n_heads / n_kv_heads);
+    const int64_t kv_stride = (int64_t)n_kv_heads * kHD;
+    const int32_t L = min(dev_pos(start, pos) + 1, max_len);   // keys 0..p, within the cache
+    const int32_t chunk = (L + n_split - 1) / n_split;
+    const int32_t j0 = s * chunk, j1 = min(L, j0 + chunk);
+    float *out = part + ((int64_t)h * n_split + s) * (kHD + 2);
+    if (t < kHD) qs[t] = Q[(int64_t)h * kHD + t];
+    __syncthreads();
+    // scores
+    const int kk = t >> 2, part4 = t & 3;
+    float sc = -INFINITY;
+    if (kk < j1 - j0) {
+        const f4 *k4 = reinterpret_cast<const f4 *>(Kc + (int64_t)(j0 + kk) * kv_stride + kvh * kHD + part4 * 32);
+        float a = 0.f;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            const f4 k = k4[d];
+            a = fmaf(qs[part4 * 32 + 4 * d], k.x, a);
+            a = fmaf(qs[part4 * 32 + 4 * d + 1], k.y, a);
+            a = fmaf(qs[part4 * 32 + 4 * d + 2], k.z, a);
+            a = fmaf(qs[part4 * 32 + 4 * d + 3], k.w, a);
+        }
+        a += __shfl_xor(a, 1);
+        a += __shfl_xor(a, 2);
+        sc = a * scale;
+    }
+    // max over the split
+    float m = sc;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((t & 63) == 0) red[t >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    const float e = (kk < j1 - j0) ? expf(sc - m) : 0.f;
+    if (part4 == 0 && kk < kChunk) ps[kk] = e;
+    const float l = block_sum<256>(part4 == 0 ? e : 0.f, red);   // barrier inside also publishes ps
+    // unnormalised output: thread t -> dim t % 128, keys of parity t / 128
+    const int d = t & (kHD - 1), par = t >> 7;
+    float acc = 0.f;
+    for (int j = par; j < j1 - j0; j += 2) acc = fmaf(ps[j], Vc[(int64_t)(j0 + j) * kv_stride + kvh * kHD + d], acc);
+    accs[par][d] = acc;
+    __syncthreads();
+    if (t < kHD) out[2 + t] = accs[0][t] + accs[1][t];
+    if (t == 0) {
+        out[0] = j1 > j0 ? m : -INFINITY;
+        out[1] = j1 > j0 ? l : 0.f;
+    }
+}
+
+// Combine the splits of head h: o = sum_s acc_s * e^(m_s - M) / sum_s l_s * e^(m_s - M).
+__global__ void __launch_bounds__(kHD)
+attn_decode_combine(const float *__restrict__ part, float *__restrict__ O, int32_t n_split)
+{
+    const int h = blockIdx.x, d = threadIdx.x;
+    const float *p = part + (int64_t)h * n_split * (kHD + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < n_split; ++s) M = fmaxf(M, p[s * (kHD + 2)]);
+    float l = 0.f, a = 0.f;
+    for (int s = 0; s < n_split; ++s) {
+        const float ms = p[s * (kHD + 2)];
+        if (ms == -INFINITY) continue;
+        const float f = expf(ms - M);
+        l += p[s * (kHD + 2) + 1] * f;
+        a += p[s * (kHD + 2) + 2 + d] * f;
+    }
+    O[(int64_t)h * kHD + d] = l > 0.f ? a / l : 0.f;
+}
+
+// Prefill: workgroup (h, tile) of 256 threads handles kQTile query rows;
+// thread t: query t/4, dims 32*(t%4) .. +31, with an online softmax over key
+// tiles of 64 rows staged in LDS.
+__global__ void __launch_bounds__(256)
+attn_prefill_kernel(const float *__restrict__ Q, const float *__restrict__ Kc, const float *__restrict__ Vc,
+                    float *__restrict__ O, int64_t n_q, int32_t n_heads, int32_t n_kv_heads, int32_t start,
+                    const int32_t *pos, int32_t max_len, float scale)
+{
+    __shared__ f4 ks[64][kHD / 4];
+    __shared__ f4 vs[64][kHD / 4];
+    const int h = blockIdx.x, t = threadIdx.x;
+    const int kvh = h / (n_heads / n_kv_heads);
+    const int64_t kv_stride = (int64_t)n_kv_heads * kHD, q_stride = (int64_t)n_heads * kHD;
+    const int32_t p0 = dev_pos(start, pos);
+    const int64_t i0 = (int64_t)blockIdx.y * kQTile;
+    const int qi = t >> 2, part4 = t & 3;
+    const int64_t i = i0 + qi;
+    const bool valid = i < n_q;
+    const int64_t p_i = p0 + (valid ? i : n_q - 1);            // last key of this query
+    // keys beyond the cache (a position past max_len) are never read
+    const int64_t p_last = min<int64_t>(p0 + min<int64_t>(i0 + kQTile, n_q) - 1, (int64_t)max_len - 1);
+
+    f4 q[8], acc[8];
+    const f4 *q4 = reinterpret_cast<const f4 *>(Q + (valid ? i : 0) * q_stride + (int64_t)h * kHD + part4 * 32);
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+        q[d] = q4[d];
+        acc[d] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+    float m = -INFINITY, l = 0.f;
+    for (int64_t j0 = 0; j0 <= p_last; j0 += 64) {
+        __syncthreads();   // previous tile consumed
+        for (int e = t; e < 64 * (kHD / 4); e += 256) {
+            const int r = e / (kHD / 4), c = e % (kHD / 4);
+            const int64_t j = j0 + r;
+            const bool in = j <= p_last;
+            ks[r][c] = in ? reinterpret_cast<const f4 *>(Kc + j * kv_stride + kvh * kHD)[c] : f4{0.f, 0.f, 0.f, 0.f};
+            vs[r][c] = in ? reinterpret_cast<const f4 *>(Vc + j * kv_stride + kvh * kHD)[c] : f4{0.f, 0.f, 0.f, 0.f};
+        }
+        __syncthreads();
+        const int64_t jn = min<int64_t>(64, p_last - j0 + 1);
+        for (int jj = 0; jj < jn; ++jj) {
+            float a = 0.f;
+#pragma unroll
+            for (int d = 0; d < 8; ++d) {
+                const f4 k = ks[jj][part4 * 8 + d];
+                a = fmaf(q[d].x, k.x, a);
+                a = fmaf(q[d].y, k.y, a);
+                a = fmaf(q[d].z, k.z, a);
+                a = fmaf(q[d].w, k.w, a);
+            }
+            a += __shfl_xor(a, 1);
+            a += __shfl_xor(a, 2);
+            if (j0 + jj > p_i) continue;            // causal: key after the query
+            const float s = a * scale;
+            const float mn = fmaxf(m, s);
+            const float corr = expf(m - mn), pj = expf(s - mn);
+            l = l * corr + pj;
+#pragma unroll
+            for (int d = 0; d < 8; ++d) {
+                const f4 v = vs[jj][part4 * 8 + d];
+                acc[d].x = fmaf(pj, v.x, acc[d].x * corr);
+                acc[d].y = fmaf(pj, v.y, acc[d].y * corr);
+                acc[d].z = fmaf(pj, v.z, acc[d].z * corr);
+                acc[d].w = fmaf(pj, v.w, acc[d].w * corr);
+            }
+            m = mn;
+        }
+    }
+    if (valid) {
+        f4 *o4 = reinterpret_cast<f4 *>(O + i * q_stride + (int64_t)h * kHD + part4 * 32);
+#pragma unroll
+        for (int d = 0; d < 8; ++d) o4[d] = acc[d] / l;
+    }
+}
+
+// ---------------------------------------------------------------- argmax
+// First index of the maximum of X[0..n) (NaN never wins).  Writes it to
+// *token; when pos is given, also stores it in history[*pos - hist_offset]
+// (when inside [0, hist_len)) and advances *pos by one.
+__global__ void __launch_bounds__(1024)
+argmax_kernel(const float *__restrict__ X, int64_t n, int32_t *token, int32_t *pos, int32_t *history,
+              int64_t hist_len, int32_t hist_offset)
+{
+    __shared__ float bv[16];
+    __shared__ int64_t bi[16];
+    float v = -INFINITY;
+    int64_t idx = INT64_MAX;
+    for (int64_t i = threadIdx.x; i < n; i += 1024) {
+        const float x = X[i];
+        if (x > v || (idx == INT64_MAX && x == v)) { v = x; idx = i; }
+    }
+    // (value desc, index asc) reduction
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(v, o);
+        const int64_t oi = __shfl_xor(idx, o);
+        if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
+    }
+    if ((threadIdx.x & 63) == 0) { bv[threadIdx.x >> 6] = v; bi[threadIdx.x >> 6] = idx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 16; ++w)
+            if (bv[w] > v || (bv[w] == v && bi[w] < idx)) { v = bv[w]; idx = bi[w]; }
+        const int32_t tok = idx == INT64_MAX ? 0 : (int32_t)idx;
+        *token = tok;
+        if (pos) {
+            const int64_t k = (int64_t)*pos - hist_offset;
+            if (history && k >= 0 && k < hist_len) history[k] = tok;
+            *pos = *pos + 1;
+        }
+    }
+}
+
+unsigned grid_for(aih_ctx *ctx, int64_t work, int per_block = 256)
+{
+    const int64_t want = (work + per_block - 1) / per_block;
+    const int64_t cap = (int64_t)(ctx->cu_count > 0 ? ctx->cu_count : 256) * 8;
+    return (unsigned)(want < 1 ? 1 : want < cap ? want : cap);
+}
+
+bool aligned16(const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int aih_rmsnorm(aih_ctx *ctx, const float *X, const float *W, float *Y, int64_t rows, int64_t cols, float eps)
+{
+    if (!ctx || !X || !W || !Y || rows < 0 || cols <= 0) return AIH_E_INVALID;
+    if (rows == 0) return AIH_OK;
+    if (rows > 0x7FFFFFFF) return AIH_E_LIMIT;
+    const bool vec = cols % 4 == 0 && aligned16(X) && aligned16(W) && aligned16(Y);
+    if (vec)
+        hipLaunchKernelGGL((rmsnorm_kernel<true>), dim3((unsigned)rows), dim3(256), 0, ctx->stream, X, W, Y, cols, eps);
+    else
+        hipLaunchKernelGGL((rmsnorm_kernel<false>), dim3((unsigned)rows), dim3(256), 0, ctx->stream, X, W, Y, cols, eps);
+    return aih_launch_status();
+}
+
+int aih_rope_table(aih_ctx *ctx, float *table, int32_t max_pos, int32_t head_dim, float theta)
+{
+    if (!ctx || !table || max_pos <= 0 || head_dim <= 0 || head_dim % 2) return AIH_E_INVALID;
+    hipLaunchKernelGGL(rope_table_kernel, dim3(grid_for(ctx, (int64_t)max_pos * head_dim / 2)), dim3(256), 0,
+                       ctx->stream, table, max_pos, head_dim, theta);
+    return aih_launch_status();
+}
+
+int aih_rope(aih_ctx *ctx, const float *X, int64_t ldx, float *Y, int64_t ldy, int64_t rows, int32_t n_heads,
+             int32_t head_dim, int32_t start, const int32_t *pos, const float *table, int32_t table_rows,
+             int y_at_pos, int64_t y_rows)
+{
+    if (!ctx || !X || !Y || !table || rows < 0 || n_heads <= 0 || head_dim <= 0 || head_dim % 2) return AIH_E_INVALID;
+    if (ldx < (int64_t)n_heads * head_dim || ldy < (int64_t)n_heads * head_dim) return AIH_E_INVALID;
+    if (rows == 0) return AIH_OK;
+    if (!pos && (start < 0 || start + rows > table_rows || (y_at_pos && start + rows > y_rows))) return AIH_E_LIMIT;
+    hipLaunchKernelGGL(rope_kernel, dim3(grid_for(ctx, rows * n_heads * (head_dim / 2))), dim3(256), 0, ctx->stream,
+                       X, ldx, Y, ldy, rows, n_heads, head_dim, start, pos, table, table_rows, y_at_pos, y_rows);
+    return aih_launch_status();
+}
+
+int aih_store_rows(aih_ctx *ctx, const float *X, int64_t rows, int64_t cols, float *Y, int64_t y_rows, int32_t start,
+                   const int32_t *pos)
+{
+    if (!ctx || !X || !Y || rows < 0 || cols <= 0) return AIH_E_INVALID;
+    if (rows == 0) return AIH_OK;
+    if (!pos && (start < 0 || start + rows > y_rows)) return AIH_E_LIMIT;
+    hipLaunchKernelGGL(store_rows_kernel, dim3(grid_for(ctx, rows * cols)), dim3(256), 0, ctx->stream, X, rows, cols,
+                       Y, y_rows, start, pos);
+    return aih_launch_status();
+}
+
+int aih_silu_mul(aih_ctx *ctx, const float *G, const float *U, float *Y, int64_t n)
+{
+    if (!ctx || !G || !U || !Y || n < 0) return AIH_E_INVALID;
+    if (n == 0) return AIH_OK;
+    hipLaunchKernelGGL(silu_mul_kernel, dim3(grid_for(ctx, n)), dim3(256), 0, ctx->stream, G, U, Y, n);
+    return aih_launch_status();
+}
+
+int aih_add(aih_ctx *ctx, const float *A, const float *B, float *Y, int64_t n)
+{
+    if (!ctx || !A || !B || !Y || n < 0) return AIH_E_INVALID;
+    if (n == 0) return AIH_OK;
+    hipLaunchKernelGGL(add_kernel, dim3(grid_for(ctx, n)), dim3(256), 0, ctx->stream, A, B, Y, n);
+    return aih_launch_status();
+}
+
+int64_t aih_attention_scratch_floats(int32_t n_heads, int32_t max_len)
+{
+    if (n_heads <= 0 || max_len <= 0) return AIH_E_INVALID;
+    const int64_t n_split = (max_len + kChunk - 1) / kChunk;
+    return (int64_t)n_heads * n_split * (kHD + 2);
+}
+
+int aih_attention(aih_ctx *ctx, const float *Q, const float *Kc, const float *Vc, float *O, int64_t n_q,
+                  int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t start, const int32_t *pos,
+                  int32_t max_len, float scale, float *scratch, int64_t scratch_floats)
+{
+    if (!ctx || !Q || !Kc || !Vc || !O || n_q < 0 || n_heads <= 0 || n_kv_heads <= 0 || max_len <= 0)
+        return AIH_E_INVALID;
+    if (n_heads % n_kv_heads) return AIH_E_INVALID;
+    if (head_dim != kHD) return AIH_E_UNSUPPORTED;
+    if (!aligned16(Q) || !aligned16(Kc) || !aligned16(Vc) || !aligned16(O)) return AIH_E_INVALID;
+    if (n_q == 0) return AIH_OK;
+    if (!pos && (start < 0 || start + n_q > max_len)) return AIH_E_LIMIT;
+    if (n_q == 1) {
+        const int32_t n_split = (max_len + kChunk - 1) / kChunk;
+        if (!scratch || scratch_floats < (int64_t)n_heads * n_split * (kHD + 2)) return AIH_E_INVALID;
+        hipLaunchKernelGGL(attn_decode_partial, dim3(n_heads, n_split), dim3(256), 0, ctx->stream, Q, Kc, Vc, scratch,
+                           n_heads, n_kv_heads, start, pos, max_len, scale, n_split);
+        int rc = aih_launch_status();
+        if (rc) return rc;
+        hipLaunchKernelGGL(attn_decode_combine, dim3(n_heads), dim3(kHD), 0, ctx->stream, scratch, O, n_split);
+        return aih_launch_status();
+    }
+    const int64_t tiles = (n_q + kQTile - 1) / kQTile;
+    if (tiles > 65535) return AIH_E_LIMIT;
+    hipLaunchKernelGGL(attn_prefill_kernel, dim3(n_heads, (unsigned)tiles), dim3(256), 0, ctx->stream, Q, Kc, Vc, O,
+                       n_q, n_heads, n_kv_heads, start, pos, max_len, scale);
+    return aih_launch_status();
+}
+
+int aih_embed_q(aih_ctx *ctx, int type, const void *table, int64_t vocab, int64_t dim, const int32_t *ids, int64_t n,
+                float *Y)
+{
+    if (!ctx || !table || !ids || !Y || vocab <= 0 || dim <= 0 || n < 0) return AIH_E_INVALID;
+    const aih_block_geom g = aih_geom(type);
+    if (!aih_is_quant(type)) return AIH_E_UNSUPPORTED;
+    if (dim % g.elems) return AIH_E_INVALID;
+    return aih_launch_embed(ctx, type, table, vocab, dim, ids, n, Y);
+}
+
+int aih_argmax(aih_ctx *ctx, const float *X, int64_t n, int32_t *token, int32_t *pos, int32_t *history,
+               int64_t hist_len, int32_t hist_offset)
+{
+    if (!ctx || !X || !token || n <= 0) return AIH_E_INVALID;
+    if (n > 0x7FFFFFFF) return AIH_E_LIMIT;
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, ctx->stream, X, n, token, pos, history, hist_len,
+                       hist_offset);
+    return aih_launch_status();
+}
+
+}  // extern "C"

@@ -179,6 +179,52 @@ dequant_kernel(const uint8_t *__restrict__ q, f4 *__restrict__ out, uint64_t n_b
     }
 }
 
+// Row gather: out[i, :] = dequantized row ids[i] of a [vocab, dim] table,
+// with the same per-lane decoders as dequant_kernel (bit-exact to it).  An
+// id outside [0, vocab) yields a row of zeros.
+template <int TYPE>
+__global__ void __launch_bounds__(256)
+embed_kernel(const uint8_t *__restrict__ table, int64_t vocab, int64_t row_bytes, int64_t blocks_per_row,
+             const int32_t *__restrict__ ids, int64_t n, f4 *__restrict__ out)
+{
+    constexpr int QK = (TYPE == AIH_TYPE_Q4_K || TYPE == AIH_TYPE_Q6_K) ? 256 : 32;
+    constexpr int BB = TYPE == AIH_TYPE_Q4_K ? 144 : TYPE == AIH_TYPE_Q6_K ? 210 : TYPE == AIH_TYPE_Q8_0 ? 34 : 18;
+    constexpr int LPB = QK / 4;
+    const uint64_t per_row = (uint64_t)blocks_per_row * LPB;
+    const uint64_t total = (uint64_t)n * per_row;
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += stride) {
+        const uint64_t i = t / per_row, r = t % per_row;
+        const int64_t id = ids[i];
+        f4 v = {0.f, 0.f, 0.f, 0.f};
+        if (id >= 0 && id < vocab) {
+            const uint8_t *b = table + id * row_bytes + (r / LPB) * BB;
+            const int lane = (int)(r % LPB);
+            if (TYPE == AIH_TYPE_Q4_K) v = deq4_q4_k<AIH_F16_IEEE>(b, lane);
+            else if (TYPE == AIH_TYPE_Q6_K) v = deq4_q6_k<AIH_F16_IEEE>(b, lane);
+            else if (TYPE == AIH_TYPE_Q8_0) v = deq4_q8_0<AIH_F16_IEEE>(b, lane);
+            else v = deq4_q4_0<AIH_F16_IEEE>(b, lane);
+        }
+        out[t] = v;
+    }
+}
+
+template <int TYPE>
+int launch_embed(aih_ctx *ctx, const void *table, int64_t vocab, int64_t dim, const int32_t *ids, int64_t n,
+                 float *out)
+{
+    constexpr int QK = (TYPE == AIH_TYPE_Q4_K || TYPE == AIH_TYPE_Q6_K) ? 256 : 32;
+    constexpr int BB = TYPE == AIH_TYPE_Q4_K ? 144 : TYPE == AIH_TYPE_Q6_K ? 210 : TYPE == AIH_TYPE_Q8_0 ? 34 : 18;
+    const int64_t bpr = dim / QK;
+    const uint64_t threads = (uint64_t)n * bpr * (QK / 4);
+    const uint64_t want = (threads + 255) / 256;
+    const uint64_t cap = (uint64_t)(ctx->cu_count > 0 ? ctx->cu_count : 256) * 16;
+    const unsigned grid = (unsigned)(want < cap ? want : cap);
+    hipLaunchKernelGGL((embed_kernel<TYPE>), dim3(grid), dim3(256), 0, ctx->stream,
+                       static_cast<const uint8_t *>(table), vocab, bpr * BB, bpr, ids, n, reinterpret_cast<f4 *>(out));
+    return aih_launch_status();
+}
+
 template <int TYPE>
 int launch_type(aih_ctx *ctx, const void *q, float *out, uint64_t n_blocks, int mode)
 {
@@ -197,6 +243,20 @@ int launch_type(aih_ctx *ctx, const void *q, float *out, uint64_t n_blocks, int 
 }
 
 }  // namespace
+
+int aih_launch_embed(aih_ctx *ctx, int type, const void *table, int64_t vocab, int64_t dim,
+                     const int32_t *ids, int64_t n, float *out)
+{
+    if (n == 0) return AIH_OK;
+    if (reinterpret_cast<uintptr_t>(out) % 16 != 0) return AIH_E_INVALID;
+    switch (type) {
+    case AIH_TYPE_Q4_K: return launch_embed<AIH_TYPE_Q4_K>(ctx, table, vocab, dim, ids, n, out);
+    case AIH_TYPE_Q6_K: return launch_embed<AIH_TYPE_Q6_K>(ctx, table, vocab, dim, ids, n, out);
+    case AIH_TYPE_Q8_0: return launch_embed<AIH_TYPE_Q8_0>(ctx, table, vocab, dim, ids, n, out);
+    case AIH_TYPE_Q4_0: return launch_embed<AIH_TYPE_Q4_0>(ctx, table, vocab, dim, ids, n, out);
+    default: return AIH_E_UNSUPPORTED;
+    }
+}
 
 int aih_launch_dequant(aih_ctx *ctx, int type, const void *q, float *out,
                        uint64_t n_blocks, int f16_mode)

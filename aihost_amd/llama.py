@@ -1,0 +1,306 @@
+"""Llama-family decoder on the HIP library: prefill and greedy decode with
+every weight matmul on the fused quantized kernels.
+
+Mirrors the reference's layer and head (paths relative to the reference
+repository):
+  LlamaDecoder.layer     LlamaFormat.ApplyLayer (AIHost/AIHost/Compute/Formats/
+                         LlamaFormat.cs:24-87) -> ComputeOps.TransformerLayer
+                         (AIHost/AIHost/Compute/ComputeOps.cs:1250-1356):
+                         x -> RMSNorm -> Q/K/V -> RoPE(Q, K) -> KV cache ->
+                         GQA attention -> W_o -> +x -> RMSNorm -> SiLU(gate)*up
+                         -> down -> +x
+  LlamaDecoder.head      TransformerBase.ForwardHead (TransformerBase.cs:168-191):
+                         output norm, then the vocabulary projection
+  LlamaDecoder.prefill / decode
+                         InferenceEngine.RunGenerationLoop (AIHost/AIHost/Inference/
+                         InferenceEngine.cs:213-334) with greedy sampling
+
+Routing seam.  The reference dequantizes every weight to F32 per use
+(TransformerBase.TempF32, TransformerBase.cs:254-271) before MatMulWeights;
+here quantized weights go straight to aih_matmul_weights_q (the fused matvec
+for M <= 8, the fused GEMM above), and the KV cache is preallocated and
+appended in place instead of concatenated (InferenceEngine.cs:598-622).
+
+Differences of scope, on purpose: prefill computes logits for the last row
+only (the greedy choice reads nothing else); a decode step is captured once
+into a HIP graph -- its position and input token live in device memory and
+the argmax step advances them -- and replayed per token.
+"""
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _native as nat
+from .compute import HipComputeDevice, fill_normal, quantize, row_bytes  # noqa: F401
+
+Q4_K, Q6_K, F32 = nat.Q4_K, nat.Q6_K, nat.F32
+
+
+@dataclass(frozen=True)
+class LlamaConfig:
+    n_layers: int
+    dim: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    ffn: int
+    vocab: int
+    eps: float = 1e-5
+    theta: float = 10000.0
+
+    @property
+    def kv_dim(self):
+        return self.n_kv_heads * self.head_dim
+
+
+# 32 layers, hidden 4096, 32/8 heads of 128, SwiGLU 14336, vocab 32000.
+LLAMA_8B_SHAPE = LlamaConfig(n_layers=32, dim=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=14336, vocab=32000)
+
+
+def layer_tensors(cfg):
+    """(suffix, qtype, rows, cols) of the weights of one layer; rows are
+    output features (GGUF dims [cols, rows])."""
+    d, kv, f = cfg.dim, cfg.kv_dim, cfg.ffn
+    qd = cfg.n_heads * cfg.head_dim
+    return [("attn_norm", F32, 1, d), ("attn_q", Q4_K, qd, d), ("attn_k", Q4_K, kv, d), ("attn_v", Q4_K, kv, d),
+            ("attn_output", Q4_K, d, qd), ("ffn_norm", F32, 1, d), ("ffn_gate", Q4_K, f, d), ("ffn_up", Q4_K, f, d),
+            ("ffn_down", Q4_K, d, f)]
+
+
+def synth_weights(cfg, seed=42, distinct_layers=None, head_type=Q6_K):
+    """Host weights of a random-init decoder: matrices N(0, 0.02) quantized to
+    Q4_K (the head to `head_type`), norm weights 1 + N(0, 0.02) in fp32.
+
+    Returns {name: (qtype, array, rows, cols)} with GGUF tensor names.  With
+    distinct_layers = m, only m layer sets are generated and layer l reuses set
+    l % m (the device still holds a separate copy per layer)."""
+    m = cfg.n_layers if distinct_layers is None else max(1, min(distinct_layers, cfg.n_layers))
+    out = {}
+    s = seed
+
+    def make(qtype, rows, cols):
+        nonlocal s
+        s += 1
+        if qtype == F32:
+            return 1.0 + fill_normal(s, rows * cols, 0.0, 0.02)
+        return quantize(qtype, fill_normal(s, rows * cols, 0.0, 0.02), rows, cols)
+
+    out["token_embd"] = (Q4_K, make(Q4_K, cfg.vocab, cfg.dim), cfg.vocab, cfg.dim)
+    sets = []
+    for _ in range(m):
+        sets.append({suf: (qt, make(qt, r, c), r, c) for suf, qt, r, c in layer_tensors(cfg)})
+    for l in range(cfg.n_layers):
+        for suf, t in sets[l % m].items():
+            out["blk.%d.%s" % (l, suf)] = t
+    out["output_norm"] = (F32, make(F32, 1, cfg.dim), 1, cfg.dim)
+    out["output"] = (head_type, make(head_type, cfg.vocab, cfg.dim), cfg.vocab, cfg.dim)
+    return out
+
+
+class DeviceWeights:
+    """Every tensor of a weight dict in its own device buffer (packed blocks
+    verbatim, as aih_upload_tensor would place them from a GGUF file)."""
+
+    def __init__(self, device, weights):
+        self.device = device
+        self.t = {}
+        try:
+            for name, (qt, arr, r, c) in weights.items():
+                a = np.ascontiguousarray(arr)
+                buf = device.create_buffer(max(16, a.nbytes))
+                nat.check(nat.lib().aih_upload_tensor(device.handle, buf.get_pointer(), a.ctypes.data, a.nbytes),
+                          "aih_upload_tensor(%s)" % name)
+                self.t[name] = (qt, buf, r, c)
+        except Exception:
+            self.dispose()
+            raise
+
+    def __getitem__(self, name):
+        return self.t[name]
+
+    def ptr(self, name):
+        return self.t[name][1].get_pointer()
+
+    def nbytes(self):
+        return sum(b.size for _, b, _, _ in self.t.values())
+
+    def dispose(self):
+        for _, b, _, _ in self.t.values():
+            b.dispose()
+        self.t = {}
+
+
+class LlamaDecoder:
+    """Prefill + greedy decode of one sequence of up to max_len positions."""
+
+    def __init__(self, device, cfg, weights, max_len, max_prefill):
+        if cfg.head_dim != 128:
+            raise ValueError("the attention kernels need head_dim 128")
+        if max_prefill > max_len:
+            raise ValueError("max_prefill > max_len")
+        self.dev, self.cfg, self.w = device, cfg, weights
+        self.max_len, self.max_prefill = int(max_len), int(max_prefill)
+        self.L = nat.lib()
+        self.h = device.handle
+        self._bufs = []
+        c, P = cfg, self.max_prefill
+
+        def buf(nbytes):
+            b = device.create_buffer(max(16, int(nbytes)))
+            self._bufs.append(b)
+            return b.get_pointer()
+
+        qd = c.n_heads * c.head_dim
+        self.x, self.xn = buf(P * c.dim * 4), buf(P * c.dim * 4)
+        self.q, self.att, self.tmp = buf(P * qd * 4), buf(P * qd * 4), buf(P * c.dim * 4)
+        self.k, self.v = buf(P * c.kv_dim * 4), buf(P * c.kv_dim * 4)
+        self.gate, self.up = buf(P * c.ffn * 4), buf(P * c.ffn * 4)
+        self.logits = buf(c.vocab * 4)
+        self.kc = [buf(self.max_len * c.kv_dim * 4) for _ in range(c.n_layers)]
+        self.vc = [buf(self.max_len * c.kv_dim * 4) for _ in range(c.n_layers)]
+        self.scratch_floats = int(self.L.aih_attention_scratch_floats(c.n_heads, self.max_len))
+        nat.check(self.scratch_floats if self.scratch_floats < 0 else 0, "aih_attention_scratch_floats")
+        self.scratch = buf(self.scratch_floats * 4)
+        self.table = buf(self.max_len * c.head_dim * 4)
+        self.ids = buf(P * 4)
+        self.token = buf(4)
+        self.pos = buf(4)
+        self.history_len = self.max_len
+        self.history = buf(self.history_len * 4)
+        self.scale = float(np.float32(1.0) / np.sqrt(np.float32(c.head_dim)))
+        nat.check(self.L.aih_rope_table(self.h, self.table, self.max_len, c.head_dim, c.theta), "aih_rope_table")
+        self.n_prompt = 0
+        self.graph = None
+
+    # -- operators (thin checked wrappers)
+    def _mm(self, name, X, M, Y):
+        qt, b, n, k = self.w[name]
+        nat.check(self.L.aih_matmul_weights_q(self.h, qt, b.get_pointer(), n, k, X, M, Y), "matmul %s" % name)
+
+    def _norm(self, name, X, Y, rows):
+        nat.check(self.L.aih_rmsnorm(self.h, X, self.w.ptr(name), Y, rows, self.cfg.dim, self.cfg.eps),
+                  "rmsnorm %s" % name)
+
+    def layer(self, l, rows, start, pos):
+        """One decoder layer over `rows` activation rows at positions start..
+        (+*pos when pos is a device pointer)."""
+        c, L, h, p = self.cfg, self.L, self.h, "blk.%d." % l
+        qd = c.n_heads * c.head_dim
+        self._norm(p + "attn_norm", self.x, self.xn, rows)
+        self._mm(p + "attn_q", self.xn, rows, self.q)
+        self._mm(p + "attn_k", self.xn, rows, self.k)
+        self._mm(p + "attn_v", self.xn, rows, self.v)
+        nat.check(L.aih_rope(h, self.q, qd, self.q, qd, rows, c.n_heads, c.head_dim, start, pos, self.table,
+                             self.max_len, 0, rows), "rope q")
+        nat.check(L.aih_rope(h, self.k, c.kv_dim, self.kc[l], c.kv_dim, rows, c.n_kv_heads, c.head_dim, start, pos,
+                             self.table, self.max_len, 1, self.max_len), "rope k -> cache")
+        nat.check(L.aih_store_rows(h, self.v, rows, c.kv_dim, self.vc[l], self.max_len, start, pos), "v -> cache")
+        nat.check(L.aih_attention(h, self.q, self.kc[l], self.vc[l], self.att, rows, c.n_heads, c.n_kv_heads,
+                                  c.head_dim, start, pos, self.max_len, self.scale, self.scratch,
+                                  self.scratch_floats), "attention")
+        self._mm(p + "attn_output", self.att, rows, self.tmp)
+        nat.check(L.aih_add(h, self.x, self.tmp, self.x, rows * c.dim), "residual")
+        self._norm(p + "ffn_norm", self.x, self.xn, rows)
+        self._mm(p + "ffn_gate", self.xn, rows, self.gate)
+        self._mm(p + "ffn_up", self.xn, rows, self.up)
+        nat.check(L.aih_silu_mul(h, self.gate, self.up, self.gate, rows * c.ffn), "silu*up")
+        self._mm(p + "ffn_down", self.gate, rows, self.tmp)
+        nat.check(L.aih_add(h, self.x, self.tmp, self.x, rows * c.dim), "residual")
+
+    def head(self, row_ptr, pos, hist_offset):
+        """Output norm + vocabulary projection of one row, then the greedy
+        token (and history / position update when pos is given)."""
+        c = self.cfg
+        self._norm("output_norm", row_ptr, self.xn, 1)
+        self._mm("output", self.xn, 1, self.logits)
+        nat.check(self.L.aih_argmax(self.h, self.logits, c.vocab, self.token, pos, self.history, self.history_len,
+                                    hist_offset), "argmax")
+
+    def prefill(self, ids):
+        """Run the prompt; return the first generated token (host int)."""
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        n = len(ids)
+        if not 0 < n <= self.max_prefill:
+            raise ValueError("prompt of %d tokens (max %d)" % (n, self.max_prefill))
+        c = self.cfg
+        if self.graph is not None:          # recorded for another prompt length
+            self.L.aih_graph_destroy(self.graph)
+            self.graph = None
+        nat.check(self.L.aih_memcpy_h2d(self.h, self.ids, ids.ctypes.data, ids.nbytes), "ids")
+        qt, tb, vocab, dim = self.w["token_embd"]
+        nat.check(self.L.aih_embed_q(self.h, qt, tb.get_pointer(), vocab, dim, self.ids, n, self.x), "embed")
+        for l in range(c.n_layers):
+            self.layer(l, n, 0, None)
+        # decode bookkeeping: the first token is history[0]; position becomes n
+        p = np.array([n - 1], dtype=np.int32)
+        nat.check(self.L.aih_memcpy_h2d(self.h, self.pos, p.ctypes.data, 4), "pos")
+        self.n_prompt = n
+        self.head(self.x + (n - 1) * c.dim * 4, self.pos, n - 1)
+        return self.read_token()
+
+    def decode_step(self):
+        """One greedy decode step reading its token and position from device
+        memory (capturable into a graph)."""
+        c = self.cfg
+        qt, tb, vocab, dim = self.w["token_embd"]
+        nat.check(self.L.aih_embed_q(self.h, qt, tb.get_pointer(), vocab, dim, self.token, 1, self.x), "embed")
+        for l in range(c.n_layers):
+            self.layer(l, 1, 0, self.pos)
+        self.head(self.x, self.pos, self.n_prompt - 1)
+
+    def capture(self):
+        """Record decode_step into a HIP graph (after prefill)."""
+        if self.graph is not None:
+            return self.graph
+        g = ctypes.c_void_p()
+        nat.check(self.L.aih_capture_begin(self.h), "aih_capture_begin")
+        try:
+            self.decode_step()
+        finally:
+            st = self.L.aih_capture_end(self.h, ctypes.byref(g))
+        nat.check(st, "aih_capture_end")
+        self.graph = g.value
+        return self.graph
+
+    def decode(self, steps, use_graph=True):
+        """Run `steps` greedy decode steps on the device; returns nothing (the
+        tokens accumulate in the device history, see tokens())."""
+        if self.n_prompt + steps > self.max_len:
+            raise ValueError("decode past max_len")
+        if use_graph:
+            g = self.capture()
+            for _ in range(steps):
+                nat.check(self.L.aih_graph_launch(self.h, g), "aih_graph_launch")
+        else:
+            for _ in range(steps):
+                self.decode_step()
+
+    def read_token(self):
+        t = np.empty(1, dtype=np.int32)
+        nat.check(self.L.aih_memcpy_d2h(self.h, t.ctypes.data, self.token, 4), "token")
+        return int(t[0])
+
+    def tokens(self, count):
+        """history[0..count): the first generated token and the decoded ones."""
+        t = np.empty(count, dtype=np.int32)
+        nat.check(self.L.aih_memcpy_d2h(self.h, t.ctypes.data, self.history, 4 * count), "history")
+        return t
+
+    def read_logits(self):
+        out = np.empty(self.cfg.vocab, dtype=np.float32)
+        nat.check(self.L.aih_memcpy_d2h(self.h, out.ctypes.data, self.logits, out.nbytes), "logits")
+        return out
+
+    def read(self, ptr, count):
+        out = np.empty(count, dtype=np.float32)
+        nat.check(self.L.aih_memcpy_d2h(self.h, out.ctypes.data, ptr, out.nbytes), "read")
+        return out
+
+    def dispose(self):
+        if self.graph is not None:
+            self.L.aih_graph_destroy(self.graph)
+            self.graph = None
+        for b in self._bufs:
+            b.dispose()
+        self._bufs = []

@@ -166,6 +166,84 @@ int aih_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
 int aih_matmul_weights_q(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
                          const float *X, int64_t M, float *Y);
 
+/* ---- decoder operators (the rest of a Llama layer around the matmuls) --
+ *
+ * All tensors are fp32 device arrays, row-major.  Position-dependent
+ * operators take `start` and an optional device pointer `pos`: row r is at
+ * position start + r, plus *pos when pos is not NULL (a decode step captured
+ * into a graph reads its position from device memory; aih_argmax advances
+ * it).  Bounds that depend on *pos are enforced on the device by skipping
+ * rows past the cache; with pos == NULL they are checked here (AIH_E_LIMIT). */
+
+/* Row-wise RMSNorm: Y[r,:] = (X[r,:] / sqrt(mean(X[r,:]^2) + eps)) * W.
+ * Y may alias X.  Replaces ComputeOps.LayerNorm (ComputeOps.cs:517-542,
+ * shader ComputeShaders.cs:247-278). */
+int aih_rmsnorm(aih_ctx *ctx, const float *X, const float *W, float *Y, int64_t rows, int64_t cols, float eps);
+
+/* RoPE table: table[(p*head_dim/2 + i)*2 + {0,1}] = {cos, sin}(p * freq_i),
+ * freq_i = 1 / theta^(2i/head_dim), for p < max_pos (the reference's fp32
+ * angle; power, cos and sin in double, rounded to float).  Computed once per
+ * context length and shared by every layer and head. */
+int aih_rope_table(aih_ctx *ctx, float *table, int32_t max_pos, int32_t head_dim, float theta);
+
+/* Interleaved-pair RoPE of n_heads heads of each row: pair (2i, 2i+1) of a
+ * head at position p is rotated by the table's angle for (p, i).  Output row
+ * r, or row p itself when y_at_pos != 0 (writing rotated keys straight into a
+ * KV cache of y_rows rows).  Y may alias X when !y_at_pos.  Replaces
+ * ComputeOps.ApplyRoPEFull (ComputeOps.cs:959-979, shader
+ * ComputeShaders.cs:517-543). */
+int aih_rope(aih_ctx *ctx, const float *X, int64_t ldx, float *Y, int64_t ldy, int64_t rows, int32_t n_heads,
+             int32_t head_dim, int32_t start, const int32_t *pos, const float *table, int32_t table_rows,
+             int y_at_pos, int64_t y_rows);
+
+/* KV cache append: Y[(p + r)*cols + c] = X[r*cols + c] for positions below
+ * y_rows.  Replaces KVCache.Add's O(L^2) concat (InferenceEngine.cs:598-622). */
+int aih_store_rows(aih_ctx *ctx, const float *X, int64_t rows, int64_t cols, float *Y, int64_t y_rows, int32_t start,
+                   const int32_t *pos);
+
+/* Y = SiLU(G) * U = (G * (1 / (1 + exp(-G)))) * U, element-wise (Y may alias
+ * G or U).  Replaces the SiLU + Multiply steps of ComputeOps.FeedForward
+ * (ComputeOps.cs:1218-1241). */
+int aih_silu_mul(aih_ctx *ctx, const float *G, const float *U, float *Y, int64_t n);
+
+/* Y = A + B, element-wise (Y may alias A or B).  Replaces ComputeOps.Add
+ * (ComputeOps.cs:389). */
+int aih_add(aih_ctx *ctx, const float *A, const float *B, float *Y, int64_t n);
+
+/* Floats of scratch aih_attention needs for single-query rows with a cache of
+ * max_len rows, or a negative status. */
+int64_t aih_attention_scratch_floats(int32_t n_heads, int32_t max_len);
+
+/* Causal grouped-query attention over a KV cache.  Query row i (position
+ * p_i) of head h attends to cache rows 0..p_i of KV head
+ * h / (n_heads / n_kv_heads):  O = softmax(scale * q K^T) V.  Q and O rows
+ * hold n_heads*head_dim floats, cache rows n_kv_heads*head_dim; the rows for
+ * the query positions must already be in the cache.  head_dim must be 128.
+ * One query row uses a split-over-keys kernel with `scratch`
+ * (aih_attention_scratch_floats) and a combine step; more rows use a tiled
+ * kernel.  Replaces ComputeOps.MultiHeadAttention and FusedMHAGenerate
+ * (ComputeOps.cs:1015-1102, shaders ComputeShaders.cs:656-733), without the
+ * latter's 4096-key limit. */
+int aih_attention(aih_ctx *ctx, const float *Q, const float *Kc, const float *Vc, float *O, int64_t n_q,
+                  int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t start, const int32_t *pos,
+                  int32_t max_len, float scale, float *scratch, int64_t scratch_floats);
+
+/* Quantized embedding gather: Y[i,:] = dequantized row ids[i] of a [vocab,
+ * dim] table of `type` blocks (ids from device memory; an id outside
+ * [0, vocab) gives zeros).  Bit-exact to aih_dequantize (IEEE fp16 scales).
+ * Replaces ComputeOps.EmbeddingLookupFromQuantized (ComputeOps.cs:1399-1454),
+ * which dequantizes the whole table below 512 MiB. */
+int aih_embed_q(aih_ctx *ctx, int type, const void *table, int64_t vocab, int64_t dim, const int32_t *ids, int64_t n,
+                float *Y);
+
+/* Greedy sampling step: *token = first index of the maximum of X[0..n) (NaN
+ * never wins).  When pos is not NULL, also history[*pos - hist_offset] = token
+ * (if inside [0, hist_len)) and *pos += 1.  Replaces the sampling of
+ * InferenceEngine.RunGenerationLoop (InferenceEngine.cs:213-390) for a
+ * greedy configuration. */
+int aih_argmax(aih_ctx *ctx, const float *X, int64_t n, int32_t *token, int32_t *pos, int32_t *history,
+               int64_t hist_len, int32_t hist_offset);
+
 /* ---- queue (IComputeCommandQueue, IComputeCommandQueue.cs:6-33) -------- */
 
 /* Wait for all work on the context stream.  Replaces Flush

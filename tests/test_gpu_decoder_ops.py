@@ -1,0 +1,225 @@
+"""Decoder operators (aih_rmsnorm, aih_rope_table, aih_rope, aih_store_rows,
+aih_silu_mul, aih_add, aih_attention, aih_embed_q, aih_argmax) vs the oracle
+(oracle/llama.py) through the C ABI.
+
+Bars: bit-exact for the row store, add, embedding gather and RoPE applied
+from the same table (the same fp32 formula, no contraction); RoPE table
+entries within 1 ulp (double pow/cos/sin on both sides, then rounded);
+RMSNorm and SiLU*up within 2e-6 relative (fp32 tree sums and expf against
+exact sums and numpy's exp); attention within 1e-5 normwise against a
+float64 evaluation.  Shapes are the decoder's (32 query / 8 KV heads of
+128, hidden 4096, FFN 14336) plus edge cases: one key, split boundaries of
+the decode kernel (63/64/65/640 keys), positions from device memory, rows
+past the cache, ids out of range, argmax ties and NaN.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from aihost_amd import _native as nat
+from aihost_amd import compute as C
+from gpu_util import upload
+from oracle import llama as ol
+
+pytestmark = pytest.mark.gpu
+L = None
+
+
+@pytest.fixture(autouse=True)
+def _lib():
+    global L
+    L = nat.lib()
+
+
+class Bufs:
+    def __init__(self, device):
+        self.device, self.b = device, []
+
+    def up(self, arr):
+        b = upload(self.device, arr)
+        self.b.append(b)
+        return b.get_pointer()
+
+    def empty(self, nbytes, fill=0xFF):
+        b = self.device.create_buffer(max(16, nbytes))
+        self.b.append(b)
+        nat.check(L.aih_memset(self.device.handle, b.get_pointer(), fill, max(16, nbytes)), "memset")
+        return b.get_pointer()
+
+    def read(self, ptr, count, dtype=np.float32):
+        out = np.empty(count, dtype=dtype)
+        nat.check(L.aih_memcpy_d2h(self.device.handle, out.ctypes.data, ptr, out.nbytes), "d2h")
+        return out
+
+    def close(self):
+        for b in self.b:
+            b.dispose()
+
+
+@pytest.fixture
+def bufs(device):
+    b = Bufs(device)
+    yield b
+    b.close()
+
+
+def rnd(seed, *shape, scale=1.0):
+    return (np.random.default_rng(seed).standard_normal(shape) * scale).astype(np.float32)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 4096), (512, 4096), (3, 1000), (2, 14336)])
+def test_rmsnorm(device, bufs, rows, cols):
+    x, w = rnd(rows, rows, cols), 1.0 + rnd(cols, cols, scale=0.02)
+    X, W, Y = bufs.up(x), bufs.up(w), bufs.empty(rows * cols * 4)
+    nat.check(L.aih_rmsnorm(device.handle, X, W, Y, rows, cols, 1e-5), "rmsnorm")
+    y = bufs.read(Y, rows * cols).reshape(rows, cols)
+    ref = ol.rmsnorm(x, w, 1e-5)
+    assert np.max(np.abs(y - ref) / (np.abs(ref) + 1e-30)) < 2e-6
+    nat.check(L.aih_rmsnorm(device.handle, X, W, X, rows, cols, 1e-5), "rmsnorm in place")
+    assert np.array_equal(bufs.read(X, rows * cols).reshape(rows, cols), y)
+
+
+def test_rope_table_matches_oracle(device, bufs):
+    T = bufs.empty(640 * 128 * 4)
+    nat.check(L.aih_rope_table(device.handle, T, 640, 128, 10000.0), "rope_table")
+    t = bufs.read(T, 640 * 128).reshape(640, 64, 2)
+    ref = ol.rope_table(640, 128, 10000.0)
+    ulps = np.abs(t.view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
+    assert ulps.max() <= 1, ulps.max()
+
+
+def _table(device, bufs, max_pos=700):
+    T = bufs.empty(max_pos * 128 * 4)
+    nat.check(L.aih_rope_table(device.handle, T, max_pos, 128, 10000.0), "rope_table")
+    return T, bufs.read(T, max_pos * 128).reshape(max_pos, 64, 2)
+
+
+@pytest.mark.parametrize("rows,heads,start", [(512, 32, 0), (1, 8, 577), (7, 32, 100)])
+def test_rope_exact_from_the_same_table(device, bufs, rows, heads, start):
+    T, t = _table(device, bufs)
+    x = rnd(rows + heads, rows, heads * 128)
+    X, Y = bufs.up(x), bufs.empty(x.nbytes)
+    nat.check(L.aih_rope(device.handle, X, heads * 128, Y, heads * 128, rows, heads, 128, start, None, T, 700, 0,
+                         rows), "rope")
+    ref = ol.rope(x, list(range(start, start + rows)), heads, 128, t)
+    assert np.array_equal(bufs.read(Y, x.size).reshape(x.shape), ref)
+
+
+def test_rope_into_cache_at_device_position(device, bufs):
+    T, t = _table(device, bufs)
+    rows, heads, max_len, p = 3, 8, 64, 60          # positions 60, 61, 62, 63 -> the 4th is past the cache
+    x = rnd(5, rows + 1, heads * 128)
+    X, C_ = bufs.up(x), bufs.empty(max_len * heads * 128 * 4, fill=0)
+    P = bufs.up(np.array([p], np.int32))
+    nat.check(L.aih_rope(device.handle, X, heads * 128, C_, heads * 128, rows + 1, heads, 128, 1, P, T, 700, 1,
+                         max_len), "rope -> cache")
+    c = bufs.read(C_, max_len * heads * 128).reshape(max_len, heads * 128)
+    ref = ol.rope(x[:3], [61, 62, 63], heads, 128, t)
+    assert np.array_equal(c[61:64], ref) and not c[:61].any()     # row 3 (position 64) skipped
+    with pytest.raises(nat.AihError):                               # host-known position past the cache
+        nat.check(L.aih_rope(device.handle, X, heads * 128, C_, heads * 128, 2, heads, 128, 63, None, T, 700, 1,
+                             max_len), "rope")
+
+
+def test_store_rows_and_add_exact(device, bufs):
+    x = rnd(6, 4, 1024)
+    X, Y = bufs.up(x), bufs.empty(10 * 1024 * 4, fill=0)
+    P = bufs.up(np.array([5], np.int32))
+    nat.check(L.aih_store_rows(device.handle, X, 4, 1024, Y, 10, 2, P), "store_rows")   # rows 7, 8, 9 (+10 skipped)
+    y = bufs.read(Y, 10 * 1024).reshape(10, 1024)
+    assert np.array_equal(y[7:10], x[:3]) and not y[:7].any()
+    a, b = rnd(7, 4096 * 3), rnd(8, 4096 * 3)
+    A, B, S = bufs.up(a), bufs.up(b), bufs.empty(a.nbytes)
+    nat.check(L.aih_add(device.handle, A, B, S, a.size), "add")
+    assert np.array_equal(bufs.read(S, a.size), a + b)
+
+
+def test_silu_mul(device, bufs):
+    g = np.concatenate([rnd(9, 14336 * 2, scale=3.0), np.array([0.0, 88.0, -88.0, -200.0, 20.0], np.float32)])
+    u = rnd(10, g.size)
+    G, U = bufs.up(g), bufs.up(u)
+    nat.check(L.aih_silu_mul(device.handle, G, U, G, g.size), "silu_mul in place")
+    y = bufs.read(G, g.size)
+    ref = ol.silu_mul(g, u)
+    assert np.max(np.abs(y - ref) / (np.abs(ref) + 1e-30)) < 2e-6
+
+
+def _attn(device, bufs, n_q, start, L_cache, nh=32, nkv=8, pos_dev=None, seed=11):
+    kvd = nkv * 128
+    q = rnd(seed, n_q, nh * 128)
+    K, V = rnd(seed + 1, L_cache, kvd), rnd(seed + 2, L_cache, kvd)
+    Q, KC, VC = bufs.up(q), bufs.up(K), bufs.up(V)
+    O = bufs.empty(q.nbytes)
+    nsc = int(L.aih_attention_scratch_floats(nh, L_cache))
+    S = bufs.empty(nsc * 4)
+    scale = float(np.float32(1) / np.sqrt(np.float32(128)))
+    P = None
+    if pos_dev is not None:
+        P = bufs.up(np.array([pos_dev], np.int32))
+    nat.check(L.aih_attention(device.handle, Q, KC, VC, O, n_q, nh, nkv, 128, start, P, L_cache, scale, S, nsc),
+              "attention")
+    o = bufs.read(O, q.size).reshape(q.shape)
+    p0 = start + (pos_dev or 0)
+    ref = ol.attention(q, K, V, list(range(p0, p0 + n_q)), nh, nkv, 128)
+    err = np.linalg.norm(o - ref) / np.linalg.norm(ref)
+    assert err < 1e-5, err
+    return o
+
+
+@pytest.mark.parametrize("keys", [1, 2, 63, 64, 65, 200, 640])
+def test_attention_decode_split_boundaries(device, bufs, keys):
+    _attn(device, bufs, 1, keys - 1, 640)
+
+
+def test_attention_decode_position_from_device(device, bufs):
+    _attn(device, bufs, 1, 0, 640, pos_dev=517)
+
+
+@pytest.mark.parametrize("n_q,start", [(512, 0), (100, 0), (65, 40), (2, 7)])
+def test_attention_prefill(device, bufs, n_q, start):
+    _attn(device, bufs, n_q, start, 640)
+
+
+def test_attention_gqa_small(device, bufs):
+    _attn(device, bufs, 40, 0, 64, nh=4, nkv=2)
+    _attn(device, bufs, 1, 39, 64, nh=4, nkv=2)
+
+
+def test_attention_argument_errors(device, bufs):
+    X = bufs.empty(4096 * 4)
+    h = device.handle
+    assert L.aih_attention(h, X, X, X, X, 1, 32, 8, 64, 0, None, 8, 1.0, X, 4096) == nat.AIH_E_UNSUPPORTED
+    assert L.aih_attention(h, X, X, X, X, 1, 32, 5, 128, 0, None, 8, 1.0, X, 4096) == nat.AIH_E_INVALID
+    assert L.aih_attention(h, X, X, X, X, 4, 32, 8, 128, 6, None, 8, 1.0, X, 4096) == nat.AIH_E_LIMIT
+    assert L.aih_attention(h, X, X, X, X, 1, 32, 8, 128, 0, None, 8, 1.0, None, 0) == nat.AIH_E_INVALID
+    device.synchronize()
+
+
+@pytest.mark.parametrize("qtype,dim", [(nat.Q4_K, 4096), (nat.Q6_K, 512), (nat.Q8_0, 96), (nat.Q4_0, 64)])
+def test_embed_bit_exact(device, bufs, qtype, dim):
+    vocab = 300
+    tab = C.quantize(qtype, C.fill_normal(12, vocab * dim, 0.0, 0.02), vocab, dim)
+    ids = np.array([5, 0, 299, 5, 300, -3, 17], np.int32)
+    T, I = bufs.up(tab), bufs.up(ids)
+    Y = bufs.empty(len(ids) * dim * 4)
+    nat.check(L.aih_embed_q(device.handle, qtype, T, vocab, dim, I, len(ids), Y), "embed")
+    y = bufs.read(Y, len(ids) * dim).reshape(len(ids), dim)
+    assert np.array_equal(y, ol.embed(qtype, tab, vocab, dim, ids))
+
+
+def test_argmax_ties_nan_and_history(device, bufs):
+    x = rnd(13, 32000)
+    x[[100, 2000, 31999]] = 50.0                  # ties: the first index wins
+    x[7] = np.nan
+    X, T = bufs.up(x), bufs.empty(16)
+    H, P = bufs.empty(64, fill=0), bufs.up(np.array([10], np.int32))
+    nat.check(L.aih_argmax(device.handle, X, x.size, T, P, H, 8, 9), "argmax")
+    assert bufs.read(T, 1, np.int32)[0] == 100 == ol.argmax(x)
+    assert bufs.read(P, 1, np.int32)[0] == 11
+    h = bufs.read(H, 8, np.int32)
+    assert h[1] == 100 and not np.delete(h, 1).any()         # history[10 - 9]
+    y = np.full(5, -np.inf, np.float32)
+    Y = bufs.up(y)
+    nat.check(L.aih_argmax(device.handle, Y, 5, T, None, None, 0, 0), "argmax")
+    assert bufs.read(T, 1, np.int32)[0] == 0

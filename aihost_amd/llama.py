@@ -217,14 +217,15 @@ class LlamaDecoder:
         nat.check(self.L.aih_argmax(self.h, self.logits, c.vocab, self.token, pos, self.history, self.history_len,
                                     hist_offset), "argmax")
 
-    def prefill(self, ids):
-        """Run the prompt; return the first generated token (host int)."""
+    def prefill(self, ids, read=True):
+        """Run the prompt; return the first generated token (host int), or
+        None with read=False (nothing waits for the device then)."""
         ids = np.ascontiguousarray(ids, dtype=np.int32)
         n = len(ids)
         if not 0 < n <= self.max_prefill:
             raise ValueError("prompt of %d tokens (max %d)" % (n, self.max_prefill))
         c = self.cfg
-        if self.graph is not None:          # recorded for another prompt length
+        if self.graph is not None and n != self.n_prompt:   # recorded for another prompt length
             self.L.aih_graph_destroy(self.graph)
             self.graph = None
         nat.check(self.L.aih_memcpy_h2d(self.h, self.ids, ids.ctypes.data, ids.nbytes), "ids")
@@ -237,7 +238,7 @@ class LlamaDecoder:
         nat.check(self.L.aih_memcpy_h2d(self.h, self.pos, p.ctypes.data, 4), "pos")
         self.n_prompt = n
         self.head(self.x + (n - 1) * c.dim * 4, self.pos, n - 1)
-        return self.read_token()
+        return self.read_token() if read else None
 
     def decode_step(self):
         """One greedy decode step reading its token and position from device

@@ -185,6 +185,89 @@ def cpu_baseline(packed, x, n, k, seconds, threads=1):
     return reps, el
 
 
+def decoder_bench(dev, distinct_layers, prompt=512, gen=128, cpu=True):
+    """Full Llama decoder of the 8B shape (32 layers, hidden 4096, 32/8 heads
+    of 128, FFN 14336, vocab 32000), Q4_K weights with a Q6_K head: prefill of
+    a `prompt`-token random prompt, then `gen` greedy decode steps replayed
+    from one captured HIP graph.  Weights are random-init; `distinct_layers`
+    layer sets are generated on the host and every layer gets its own copy in
+    HBM, so each decode step streams all 32 layers' weights."""
+    from aihost_amd import _native as nat
+    from aihost_amd import llama
+    cfg = llama.LLAMA_8B_SHAPE
+    L, h = nat.lib(), dev.handle
+    t0 = time.perf_counter()
+    w = llama.synth_weights(cfg, seed=42, distinct_layers=distinct_layers)
+    t_synth = time.perf_counter() - t0
+    dw = llama.DeviceWeights(dev, w)
+    dec = llama.LlamaDecoder(dev, cfg, dw, max_len=prompt + gen, max_prefill=prompt)
+    ids = np.random.default_rng(43).integers(0, cfg.vocab, prompt).astype(np.int32)
+    try:
+        first = dec.prefill(ids)          # warm-up (GEMM workspace, code paths)
+        dec.decode(4)                     # captures the decode graph
+        dev.synchronize()
+        nat.check(L.aih_event_record(h, 2), "event")
+        dec.prefill(ids, read=False)
+        nat.check(L.aih_event_record(h, 3), "event")
+        dec.decode(gen)
+        nat.check(L.aih_event_record(h, 4), "event")
+        dev.synchronize()
+        ms = ctypes.c_float()
+        nat.check(L.aih_event_elapsed(h, 2, 3, ctypes.byref(ms)), "event")
+        t_pre = ms.value * 1e-3
+        nat.check(L.aih_event_elapsed(h, 3, 4, ctypes.byref(ms)), "event")
+        t_dec = ms.value * 1e-3
+        toks = dec.tokens(gen + 1)
+    finally:
+        dec.dispose()
+    wbytes = dw.nbytes() - w["token_embd"][1].nbytes + cfg.dim * 4 * 2   # one embedding row read per token
+    dw.dispose()
+    # KV cache reads per decode step (fp32 K and V rows 0..p of every layer), averaged over the steps
+    avg_keys = prompt + (gen + 1) / 2.0
+    kv_bytes = 2 * cfg.n_layers * avg_keys * cfg.kv_dim * 4
+    per_tok = t_dec / gen
+    flops_pre = 2.0 * prompt * sum(r * c for n_, (qt, a, r, c) in w.items()
+                                   if n_.startswith("blk.") and qt != llama.F32)
+    out = {
+        "model": "Llama 8B shape, random init: 32 layers, hidden 4096, 32/8 heads x 128, FFN 14336, vocab 32000; "
+                 "Q4_K weights, Q6_K head (%d distinct layer sets, one HBM copy per layer)" % distinct_layers,
+        "prefill_tokens": prompt, "prefill_ms": round(t_pre * 1e3, 2),
+        "prefill_tokens_per_s": round(prompt / t_pre, 1),
+        "prefill_layer_matmul_TFLOP/s": round(flops_pre / t_pre / 1e12, 1),
+        "decode_tokens": gen, "decode_ms_per_token": round(per_tok * 1e3, 4),
+        "decode_tokens_per_s": round(gen / t_dec, 1),
+        "decode_GB/s": round((wbytes + kv_bytes) / per_tok / 1e9, 1),
+        "decode_frac_hbm_peak": round((wbytes + kv_bytes) / per_tok / 1e9 / HBM_PEAK_GBS, 4),
+        "decode_bytes_per_token": int(wbytes + kv_bytes),
+        "first_tokens": [int(t) for t in toks[:8]], "first_token_check": int(first) == int(toks[0]),
+        "host_weight_synthesis_s": round(t_synth, 1),
+    }
+    if cpu:
+        # the oracle's single-thread matvec (the reference's scalar CPU path) on
+        # one layer's seven matrices and the head, extrapolated to 32 layers
+        from oracle import oracle as orc
+        orc.lib()
+        t_layer = 0.0
+        x = np.random.default_rng(1).standard_normal((1, cfg.ffn)).astype(np.float32)
+        for suf, qt, r, c in llama.layer_tensors(cfg):
+            if qt == llama.F32:
+                continue
+            t1 = time.perf_counter()
+            orc.matvec(qt, w["blk.0." + suf][1], r, c, x[:, :c], nthreads=1)
+            t_layer += time.perf_counter() - t1
+        qt, a, r, c = w["output"]
+        t1 = time.perf_counter()
+        orc.matvec(qt, a, r, c, x[:, :c], nthreads=1)
+        t_head = time.perf_counter() - t1
+        t_tok = cfg.n_layers * t_layer + t_head
+        out["cpu_baseline_decode"] = {
+            "value": round(1.0 / t_tok, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": "one layer's 7 Q4_K matvecs (%.2f s) and the Q6_K head (%.2f s) through the oracle's "
+                      "single-thread row dequant + fp32 dot, extrapolated to 32 layers; attention and norms "
+                      "not counted" % (t_layer, t_head)}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -193,6 +276,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary workloads")
+    ap.add_argument("--no-decoder", action="store_true", help="skip the full-decoder prefill/decode leg")
+    ap.add_argument("--decoder-distinct-layers", type=int, default=2)
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -258,6 +343,10 @@ def main():
                                              "frac_mfma_peak": round(flops / (ms * 1e-3) / MFMA_F16_PEAK, 4)}
         gb.close()
 
+    decode = None
+    if not args.no_decoder:
+        decode = decoder_bench(dev, args.decoder_distinct_layers, cpu=not args.no_cpu_baseline)
+
     cpu = None
     if not args.no_cpu_baseline:
         reps, el = cpu_baseline(packed, x_host.reshape(1, k), n, k, args.cpu_seconds, threads=1)
@@ -287,6 +376,7 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel_us": round(ms_kernel * 1e3, 3), "bytes_per_launch": nbytes},
         "cpu_baseline": cpu,
+        "decode": decode,
         "also": extra,
         "y_checksum": float(np.sum(y_check.astype(np.float64))),
     }

@@ -66,6 +66,8 @@ SIGNATURES = {
     "aih_rope_table": (_i, [_vp, _vp, ctypes.c_int32, ctypes.c_int32, _f]),
     "aih_rope": (_i, [_vp, _vp, _i64, _vp, _i64, _i64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _vp, _vp,
                       ctypes.c_int32, _i, _i64]),
+    "aih_rope_qkv": (_i, [_vp, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, ctypes.c_int32, ctypes.c_int32,
+                          ctypes.c_int32, ctypes.c_int32, _vp, _vp, ctypes.c_int32, _i64]),
     "aih_store_rows": (_i, [_vp, _vp, _i64, _i64, _vp, _i64, ctypes.c_int32, _vp]),
     "aih_silu_mul": (_i, [_vp, _vp, _vp, _vp, _i64]),
     "aih_add": (_i, [_vp, _vp, _vp, _vp, _i64]),

@@ -147,6 +147,50 @@ rope_kernel(const float *X, int64_t ldx, float *Y, int64_t ldy, int64_t rows, in
     }
 }
 
+// Q/K/V of one layer after the projections, in one launch: RoPE of the
+// query heads in place, RoPE of the key heads into the K cache at their
+// positions, the value rows into the V cache.  Q, K and V rows have strides
+// ldq / ldk / ldv (the three may be parts of one fused projection output).
+__global__ void __launch_bounds__(256)
+rope_qkv_kernel(float *Q, int64_t ldq, const float *K, int64_t ldk, const float *V, int64_t ldv, float *Kc,
+                float *Vc, int64_t rows, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t start,
+                const int32_t *pos, const float *__restrict__ table, int32_t table_rows, int64_t cache_rows)
+{
+    const int half = head_dim / 2;
+    const int64_t nq = (int64_t)n_heads * half, nk = (int64_t)n_kv_heads * half, nv = (int64_t)n_kv_heads * half;
+    const int64_t per_row = nq + nk + nv;           // pairs per row: q, k, v (v "pairs" are plain copies)
+    const int64_t kv_dim = (int64_t)n_kv_heads * head_dim;
+    const int32_t p0 = dev_pos(start, pos);
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < rows * per_row;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = t / per_row, e = t % per_row;
+        const int64_t p = p0 + r;
+        if (p < 0 || p >= table_rows) continue;
+        if (e < nq + nk) {
+            const bool is_q = e < nq;
+            const int64_t pe = is_q ? e : e - nq;
+            const int hh = (int)(pe / half), i = (int)(pe % half);
+            const float c = table[2 * (p * half + i)], sn = table[2 * (p * half + i) + 1];
+            const float *x = (is_q ? Q + r * ldq : K + r * ldk) + (int64_t)hh * head_dim + 2 * i;
+            const float x0 = x[0], x1 = x[1];
+            float *y;
+            if (is_q) {
+                y = Q + r * ldq + (int64_t)hh * head_dim + 2 * i;
+            } else {
+                if (p >= cache_rows) continue;
+                y = Kc + p * kv_dim + (int64_t)hh * head_dim + 2 * i;
+            }
+            y[0] = x0 * c - x1 * sn;
+            y[1] = x0 * sn + x1 * c;
+        } else {
+            if (p >= cache_rows) continue;
+            const int64_t c2 = 2 * (e - nq - nk);
+            Vc[p * kv_dim + c2] = V[r * ldv + c2];
+            Vc[p * kv_dim + c2 + 1] = V[r * ldv + c2 + 1];
+        }
+    }
+}
+
 // ---------------------------------------------------------------- row store
 // Y[(p + r) * cols + c] = X[r * cols + c] for rows whose position p + r is
 // below y_rows (a KV cache append).
@@ -187,90 +231,150 @@ add_kernel(const float *A, const float *B, float *Y, int64_t n)
 // Q/O rows hold n_heads*head_dim floats, K/V cache rows n_kv_heads*head_dim.
 
 constexpr int kHD = 128;      // head_dim supported by the attention kernels
-constexpr int kChunk = 64;    // keys per decode split (upper bound)
+constexpr int kSub = 64;      // keys per decode sub-chunk (one pass of the score step)
+constexpr int kMaxSplit = 64; // decode splits per head (upper bound)
 constexpr int kQTile = 64;    // queries per prefill workgroup
 
-// Decode, split over keys: workgroup (h, s) of 256 threads handles the keys of
-// split s (ceil(L / n_split) of them, at most kChunk) and writes its partial
-// (max, sum, unnormalised output) to scratch.  Thread t: key t/4, dims
-// 32*(t%4) .. +31.
+int32_t decode_splits(int32_t max_len)
+{
+    const int32_t n = (max_len + kSub - 1) / kSub;
+    return n < kMaxSplit ? n : kMaxSplit;
+}
+
+// Decode (one query row), split over keys.  Workgroup (h, s) of 256 threads
+// walks the keys of split s in sub-chunks of kSub with an online softmax and
+// writes its partial (max, sum, unnormalised output) to `part`;
+// attn_decode_combine then merges the splits of each head.  (A single kernel
+// whose last workgroup per head combines, found through a device counter,
+// measured slower on MI355X: the agent-scope fences it needs write back the
+// XCD's L2.)
+//   scores: thread t -> key t/4 of the sub-chunk, dims 32*(t%4) .. +31
+//   values: thread t -> dims 4*(t%32) .. +3 of keys t/32, t/32 + 8, ...
 __global__ void __launch_bounds__(256)
 attn_decode_partial(const float *__restrict__ Q, const float *__restrict__ Kc, const float *__restrict__ Vc,
                     float *__restrict__ part, int32_t n_heads, int32_t n_kv_heads, int32_t start,
                     const int32_t *pos, int32_t max_len, float scale, int32_t n_split)
 {
     __shared__ float qs[kHD];
-    __shared__ float ps[kChunk];
+    __shared__ float ps[kSub];
     __shared__ float red[4];
-    __shared__ float accs[2][kHD];
+    __shared__ f4 accs[8][kHD / 4];
     const int h = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
     const int kvh = h / (n_heads / n_kv_heads);
     const int64_t kv_stride = (int64_t)n_kv_heads * kHD;
     const int32_t L = min(dev_pos(start, pos) + 1, max_len);   // keys 0..p, within the cache
     const int32_t chunk = (L + n_split - 1) / n_split;
-    const int32_t j0 = s * chunk, j1 = min(L, j0 + chunk);
-    float *out = part + ((int64_t)h * n_split + s) * (kHD + 2);
+    const int32_t j0 = min(s * chunk, L), j1 = min(L, j0 + chunk);
     if (t < kHD) qs[t] = Q[(int64_t)h * kHD + t];
     __syncthreads();
-    // scores
     const int kk = t >> 2, part4 = t & 3;
-    float sc = -INFINITY;
-    if (kk < j1 - j0) {
-        const f4 *k4 = reinterpret_cast<const f4 *>(Kc + (int64_t)(j0 + kk) * kv_stride + kvh * kHD + part4 * 32);
-        float a = 0.f;
+    const int vc = t & 31, vr = t >> 5;
+    float m = -INFINITY, l = 0.f;
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int32_t c0 = j0; c0 < j1; c0 += kSub) {
+        const int n = min(kSub, j1 - c0);
+        // V rows of this sub-chunk are loaded together with the K rows (their
+        // addresses do not depend on the scores): one memory round trip
+        f4 vv[kSub / 8];
 #pragma unroll
-        for (int d = 0; d < 8; ++d) {
-            const f4 k = k4[d];
-            a = fmaf(qs[part4 * 32 + 4 * d], k.x, a);
-            a = fmaf(qs[part4 * 32 + 4 * d + 1], k.y, a);
-            a = fmaf(qs[part4 * 32 + 4 * d + 2], k.z, a);
-            a = fmaf(qs[part4 * 32 + 4 * d + 3], k.w, a);
+        for (int u = 0; u < kSub / 8; ++u) {
+            const int j = vr + 8 * u;
+            vv[u] = j < n ? reinterpret_cast<const f4 *>(Vc + (int64_t)(c0 + j) * kv_stride + kvh * kHD)[vc]
+                          : f4{0.f, 0.f, 0.f, 0.f};
         }
-        a += __shfl_xor(a, 1);
-        a += __shfl_xor(a, 2);
-        sc = a * scale;
-    }
-    // max over the split
-    float m = sc;
+        float sc = -INFINITY;
+        if (kk < n) {
+            const f4 *k4 = reinterpret_cast<const f4 *>(Kc + (int64_t)(c0 + kk) * kv_stride + kvh * kHD + part4 * 32);
+            float a = 0.f;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    if ((t & 63) == 0) red[t >> 6] = m;
+            for (int d = 0; d < 8; ++d) {
+                const f4 k = k4[d];
+                a = fmaf(qs[part4 * 32 + 4 * d], k.x, a);
+                a = fmaf(qs[part4 * 32 + 4 * d + 1], k.y, a);
+                a = fmaf(qs[part4 * 32 + 4 * d + 2], k.z, a);
+                a = fmaf(qs[part4 * 32 + 4 * d + 3], k.w, a);
+            }
+            a += __shfl_xor(a, 1);
+            a += __shfl_xor(a, 2);
+            sc = a * scale;
+        }
+        float mc = sc;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) mc = fmaxf(mc, __shfl_xor(mc, o));
+        if ((t & 63) == 0) red[t >> 6] = mc;
+        __syncthreads();
+        const float mn = fmaxf(m, fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+        __syncthreads();
+        const float e = kk < n ? expf(sc - mn) : 0.f;
+        if (part4 == 0) ps[kk] = e;
+        const float lc = block_sum<256>(part4 == 0 ? e : 0.f, red);   // its barrier publishes ps
+        const float corr = expf(m - mn);                              // 0 on the first sub-chunk
+        l = l * corr + lc;
+        f4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < kSub / 8; ++u) {
+            const int j = vr + 8 * u;
+            const float pj = j < n ? ps[j] : 0.f;
+            a.x = fmaf(pj, vv[u].x, a.x);
+            a.y = fmaf(pj, vv[u].y, a.y);
+            a.z = fmaf(pj, vv[u].z, a.z);
+            a.w = fmaf(pj, vv[u].w, a.w);
+        }
+        acc = acc * corr + a;
+        m = mn;
+        __syncthreads();   // ps and red reused by the next sub-chunk
+    }
+    // partial of this split: sum the eight key groups
+    accs[vr][vc] = acc;
     __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
-    const float e = (kk < j1 - j0) ? expf(sc - m) : 0.f;
-    if (part4 == 0 && kk < kChunk) ps[kk] = e;
-    const float l = block_sum<256>(part4 == 0 ? e : 0.f, red);   // barrier inside also publishes ps
-    // unnormalised output: thread t -> dim t % 128, keys of parity t / 128
-    const int d = t & (kHD - 1), par = t >> 7;
-    float acc = 0.f;
-    for (int j = par; j < j1 - j0; j += 2) acc = fmaf(ps[j], Vc[(int64_t)(j0 + j) * kv_stride + kvh * kHD + d], acc);
-    accs[par][d] = acc;
-    __syncthreads();
-    if (t < kHD) out[2 + t] = accs[0][t] + accs[1][t];
+    float *mine = part + ((int64_t)h * n_split + s) * (kHD + 2);
+    if (t < kHD) {
+        const float *af = reinterpret_cast<const float *>(&accs[0][0]);
+        float v = 0.f;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) v += af[r * kHD + t];
+        mine[2 + t] = v;
+    }
     if (t == 0) {
-        out[0] = j1 > j0 ? m : -INFINITY;
-        out[1] = j1 > j0 ? l : 0.f;
+        mine[0] = j1 > j0 ? m : -INFINITY;
+        mine[1] = j1 > j0 ? l : 0.f;
     }
 }
 
-// Combine the splits of head h: o = sum_s acc_s * e^(m_s - M) / sum_s l_s * e^(m_s - M).
+// Combine the splits of head h: o = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M).
+// Every split's (m, l) is loaded in one round, the weights go through LDS,
+// and the accumulators are read eight splits at a time.
 __global__ void __launch_bounds__(kHD)
 attn_decode_combine(const float *__restrict__ part, float *__restrict__ O, int32_t n_split)
 {
-    const int h = blockIdx.x, d = threadIdx.x;
-    const float *p = part + (int64_t)h * n_split * (kHD + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < n_split; ++s) M = fmaxf(M, p[s * (kHD + 2)]);
-    float l = 0.f, a = 0.f;
-    for (int s = 0; s < n_split; ++s) {
-        const float ms = p[s * (kHD + 2)];
-        if (ms == -INFINITY) continue;
-        const float f = expf(ms - M);
-        l += p[s * (kHD + 2) + 1] * f;
-        a += p[s * (kHD + 2) + 2 + d] * f;
+    __shared__ float ws[kMaxSplit];
+    __shared__ float red[2];
+    const int h = blockIdx.x, t = threadIdx.x;
+    const float *ph = part + (int64_t)h * n_split * (kHD + 2);
+    const float mt = t < n_split ? ph[t * (kHD + 2)] : -INFINITY;
+    const float lt = t < n_split ? ph[t * (kHD + 2) + 1] : 0.f;
+    float M = mt;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+    if ((t & 63) == 0) red[t >> 6] = M;
+    __syncthreads();
+    M = fmaxf(red[0], red[1]);
+    const float w = mt == -INFINITY ? 0.f : expf(mt - M);
+    if (t < n_split) ws[t] = w;
+    float lw = wave_sum(lt * w);
+    __syncthreads();
+    if ((t & 63) == 0) red[t >> 6] = lw;
+    __syncthreads();
+    const float lsum = red[0] + red[1];
+    float a = 0.f;
+    for (int i0 = 0; i0 < n_split; i0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = i0 + u < n_split ? ph[(i0 + u) * (kHD + 2) + 2 + t] : 0.f;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) a = fmaf(v[u], i0 + u < n_split ? ws[i0 + u] : 0.f, a);
     }
-    O[(int64_t)h * kHD + d] = l > 0.f ? a / l : 0.f;
+    O[(int64_t)h * kHD + t] = lsum > 0.f ? a / lsum : 0.f;
 }
 
 // Prefill: workgroup (h, tile) of 256 threads handles kQTile query rows;
@@ -434,6 +538,24 @@ int aih_rope(aih_ctx *ctx, const float *X, int64_t ldx, float *Y, int64_t ldy, i
     return aih_launch_status();
 }
 
+int aih_rope_qkv(aih_ctx *ctx, float *Q, int64_t ldq, const float *K, int64_t ldk, const float *V, int64_t ldv,
+                 float *Kc, float *Vc, int64_t rows, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                 int32_t start, const int32_t *pos, const float *table, int32_t table_rows, int64_t cache_rows)
+{
+    if (!ctx || !Q || !K || !V || !Kc || !Vc || !table || rows < 0 || n_heads <= 0 || n_kv_heads <= 0 ||
+        head_dim <= 0 || head_dim % 2)
+        return AIH_E_INVALID;
+    if (ldq < (int64_t)n_heads * head_dim || ldk < (int64_t)n_kv_heads * head_dim ||
+        ldv < (int64_t)n_kv_heads * head_dim)
+        return AIH_E_INVALID;
+    if (rows == 0) return AIH_OK;
+    if (!pos && (start < 0 || start + rows > table_rows || start + rows > cache_rows)) return AIH_E_LIMIT;
+    const int64_t work = rows * (int64_t)(n_heads + 2 * n_kv_heads) * (head_dim / 2);
+    hipLaunchKernelGGL(rope_qkv_kernel, dim3(grid_for(ctx, work)), dim3(256), 0, ctx->stream, Q, ldq, K, ldk, V, ldv,
+                       Kc, Vc, rows, n_heads, n_kv_heads, head_dim, start, pos, table, table_rows, cache_rows);
+    return aih_launch_status();
+}
+
 int aih_store_rows(aih_ctx *ctx, const float *X, int64_t rows, int64_t cols, float *Y, int64_t y_rows, int32_t start,
                    const int32_t *pos)
 {
@@ -464,8 +586,8 @@ int aih_add(aih_ctx *ctx, const float *A, const float *B, float *Y, int64_t n)
 int64_t aih_attention_scratch_floats(int32_t n_heads, int32_t max_len)
 {
     if (n_heads <= 0 || max_len <= 0) return AIH_E_INVALID;
-    const int64_t n_split = (max_len + kChunk - 1) / kChunk;
-    return (int64_t)n_heads * n_split * (kHD + 2);
+    // partials of every (head, split)
+    return (int64_t)n_heads * decode_splits(max_len) * (kHD + 2);
 }
 
 int aih_attention(aih_ctx *ctx, const float *Q, const float *Kc, const float *Vc, float *O, int64_t n_q,
@@ -480,11 +602,12 @@ int aih_attention(aih_ctx *ctx, const float *Q, const float *Kc, const float *Vc
     if (n_q == 0) return AIH_OK;
     if (!pos && (start < 0 || start + n_q > max_len)) return AIH_E_LIMIT;
     if (n_q == 1) {
-        const int32_t n_split = (max_len + kChunk - 1) / kChunk;
-        if (!scratch || scratch_floats < (int64_t)n_heads * n_split * (kHD + 2)) return AIH_E_INVALID;
+        const int32_t n_split = decode_splits(max_len);
+        const int64_t n_part = (int64_t)n_heads * n_split * (kHD + 2);
+        if (!scratch || scratch_floats < n_part) return AIH_E_INVALID;
         hipLaunchKernelGGL(attn_decode_partial, dim3(n_heads, n_split), dim3(256), 0, ctx->stream, Q, Kc, Vc, scratch,
                            n_heads, n_kv_heads, start, pos, max_len, scale, n_split);
-        int rc = aih_launch_status();
+        const int rc = aih_launch_status();
         if (rc) return rc;
         hipLaunchKernelGGL(attn_decode_combine, dim3(n_heads), dim3(kHD), 0, ctx->stream, scratch, O, n_split);
         return aih_launch_status();

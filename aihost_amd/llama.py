@@ -98,36 +98,84 @@ def synth_weights(cfg, seed=42, distinct_layers=None, head_type=Q6_K):
     return out
 
 
+# Weights stored back to back in one device buffer, so that a decode step
+# runs one matvec over all of them (their outputs land back to back too):
+# Q|K|V share the input x, gate|up share the normed x.
+FUSED_GROUPS = (("attn_qkv", ("attn_q", "attn_k", "attn_v")), ("ffn_gate_up", ("ffn_gate", "ffn_up")))
+
+
 class DeviceWeights:
-    """Every tensor of a weight dict in its own device buffer (packed blocks
-    verbatim, as aih_upload_tensor would place them from a GGUF file)."""
+    """Every tensor of a weight dict in device memory, packed blocks verbatim
+    (as aih_upload_tensor places them from a GGUF file).  The matrices of each
+    FUSED_GROUPS group of a layer are placed back to back in one buffer and
+    are also reachable under the group name ("blk.<l>.attn_qkv", ...).
+    Entries are (qtype, device pointer, rows, cols)."""
 
     def __init__(self, device, weights):
         self.device = device
         self.t = {}
+        self._owned = []
+        grouped = {}
+        for name in weights:
+            if name.startswith("blk."):
+                pre, suf = name.rsplit(".", 1)[0], name.rsplit(".", 1)[1]
+                for gname, members in FUSED_GROUPS:
+                    if suf in members:
+                        grouped.setdefault(pre + "." + gname, []).append(name)
         try:
+            done = set()
+            for gname, names in grouped.items():
+                names = sorted(names, key=lambda n: [m for g, ms in FUSED_GROUPS for m in ms].index(n.rsplit(".", 1)[1]))
+                qts = {weights[n][0] for n in names}
+                cols = {weights[n][3] for n in names}
+                if len(qts) != 1 or len(cols) != 1:
+                    continue                    # mixed formats or widths: stored separately
+                sizes = [np.ascontiguousarray(weights[n][1]).nbytes for n in names]
+                buf = self._alloc(sum(sizes))
+                off = 0
+                for n, sz in zip(names, sizes):
+                    qt, arr, r, c = weights[n]
+                    self._upload(buf.get_pointer() + off, arr, n)
+                    self.t[n] = (qt, buf.get_pointer() + off, r, c)
+                    off += sz
+                    done.add(n)
+                self.t[gname] = (qts.pop(), buf.get_pointer(), sum(weights[n][2] for n in names), cols.pop())
             for name, (qt, arr, r, c) in weights.items():
-                a = np.ascontiguousarray(arr)
-                buf = device.create_buffer(max(16, a.nbytes))
-                nat.check(nat.lib().aih_upload_tensor(device.handle, buf.get_pointer(), a.ctypes.data, a.nbytes),
-                          "aih_upload_tensor(%s)" % name)
-                self.t[name] = (qt, buf, r, c)
+                if name in done:
+                    continue
+                buf = self._alloc(np.ascontiguousarray(arr).nbytes)
+                self._upload(buf.get_pointer(), arr, name)
+                self.t[name] = (qt, buf.get_pointer(), r, c)
         except Exception:
             self.dispose()
             raise
 
+    def _alloc(self, nbytes):
+        b = self.device.create_buffer(max(16, nbytes))
+        self._owned.append(b)
+        return b
+
+    def _upload(self, ptr, arr, name):
+        a = np.ascontiguousarray(arr)
+        nat.check(nat.lib().aih_upload_tensor(self.device.handle, ptr, a.ctypes.data, a.nbytes),
+                  "aih_upload_tensor(%s)" % name)
+
     def __getitem__(self, name):
         return self.t[name]
 
+    def __contains__(self, name):
+        return name in self.t
+
     def ptr(self, name):
-        return self.t[name][1].get_pointer()
+        return self.t[name][1]
 
     def nbytes(self):
-        return sum(b.size for _, b, _, _ in self.t.values())
+        return sum(b.size for b in self._owned)
 
     def dispose(self):
-        for _, b, _, _ in self.t.values():
+        for b in self._owned:
             b.dispose()
+        self._owned = []
         self.t = {}
 
 
@@ -156,6 +204,9 @@ class LlamaDecoder:
         self.q, self.att, self.tmp = buf(P * qd * 4), buf(P * qd * 4), buf(P * c.dim * 4)
         self.k, self.v = buf(P * c.kv_dim * 4), buf(P * c.kv_dim * 4)
         self.gate, self.up = buf(P * c.ffn * 4), buf(P * c.ffn * 4)
+        # decode: outputs of the fused Q|K|V and gate|up matvecs
+        self.qkv = buf((qd + 2 * c.kv_dim) * 4)
+        self.gu = buf(2 * c.ffn * 4)
         self.logits = buf(c.vocab * 4)
         self.kc = [buf(self.max_len * c.kv_dim * 4) for _ in range(c.n_layers)]
         self.vc = [buf(self.max_len * c.kv_dim * 4) for _ in range(c.n_layers)]
@@ -175,8 +226,8 @@ class LlamaDecoder:
 
     # -- operators (thin checked wrappers)
     def _mm(self, name, X, M, Y):
-        qt, b, n, k = self.w[name]
-        nat.check(self.L.aih_matmul_weights_q(self.h, qt, b.get_pointer(), n, k, X, M, Y), "matmul %s" % name)
+        qt, ptr, n, k = self.w[name]
+        nat.check(self.L.aih_matmul_weights_q(self.h, qt, ptr, n, k, X, M, Y), "matmul %s" % name)
 
     def _norm(self, name, X, Y, rows):
         nat.check(self.L.aih_rmsnorm(self.h, X, self.w.ptr(name), Y, rows, self.cfg.dim, self.cfg.eps),
@@ -184,28 +235,37 @@ class LlamaDecoder:
 
     def layer(self, l, rows, start, pos):
         """One decoder layer over `rows` activation rows at positions start..
-        (+*pos when pos is a device pointer)."""
+        (+*pos when pos is a device pointer).  A single row (decode) uses the
+        fused Q|K|V and gate|up matvecs when the weights have them."""
         c, L, h, p = self.cfg, self.L, self.h, "blk.%d." % l
         qd = c.n_heads * c.head_dim
         self._norm(p + "attn_norm", self.x, self.xn, rows)
-        self._mm(p + "attn_q", self.xn, rows, self.q)
-        self._mm(p + "attn_k", self.xn, rows, self.k)
-        self._mm(p + "attn_v", self.xn, rows, self.v)
-        nat.check(L.aih_rope(h, self.q, qd, self.q, qd, rows, c.n_heads, c.head_dim, start, pos, self.table,
-                             self.max_len, 0, rows), "rope q")
-        nat.check(L.aih_rope(h, self.k, c.kv_dim, self.kc[l], c.kv_dim, rows, c.n_kv_heads, c.head_dim, start, pos,
-                             self.table, self.max_len, 1, self.max_len), "rope k -> cache")
-        nat.check(L.aih_store_rows(h, self.v, rows, c.kv_dim, self.vc[l], self.max_len, start, pos), "v -> cache")
-        nat.check(L.aih_attention(h, self.q, self.kc[l], self.vc[l], self.att, rows, c.n_heads, c.n_kv_heads,
+        if rows == 1 and p + "attn_qkv" in self.w:
+            self._mm(p + "attn_qkv", self.xn, 1, self.qkv)
+            q, k, v = self.qkv, self.qkv + qd * 4, self.qkv + (qd + c.kv_dim) * 4
+        else:
+            self._mm(p + "attn_q", self.xn, rows, self.q)
+            self._mm(p + "attn_k", self.xn, rows, self.k)
+            self._mm(p + "attn_v", self.xn, rows, self.v)
+            q, k, v = self.q, self.k, self.v
+        nat.check(L.aih_rope_qkv(h, q, qd, k, c.kv_dim, v, c.kv_dim, self.kc[l], self.vc[l], rows, c.n_heads,
+                                 c.n_kv_heads, c.head_dim, start, pos, self.table, self.max_len, self.max_len),
+                  "rope q, k -> cache, v -> cache")
+        nat.check(L.aih_attention(h, q, self.kc[l], self.vc[l], self.att, rows, c.n_heads, c.n_kv_heads,
                                   c.head_dim, start, pos, self.max_len, self.scale, self.scratch,
                                   self.scratch_floats), "attention")
         self._mm(p + "attn_output", self.att, rows, self.tmp)
         nat.check(L.aih_add(h, self.x, self.tmp, self.x, rows * c.dim), "residual")
         self._norm(p + "ffn_norm", self.x, self.xn, rows)
-        self._mm(p + "ffn_gate", self.xn, rows, self.gate)
-        self._mm(p + "ffn_up", self.xn, rows, self.up)
-        nat.check(L.aih_silu_mul(h, self.gate, self.up, self.gate, rows * c.ffn), "silu*up")
-        self._mm(p + "ffn_down", self.gate, rows, self.tmp)
+        if rows == 1 and p + "ffn_gate_up" in self.w:
+            self._mm(p + "ffn_gate_up", self.xn, 1, self.gu)
+            gate, up = self.gu, self.gu + c.ffn * 4
+        else:
+            self._mm(p + "ffn_gate", self.xn, rows, self.gate)
+            self._mm(p + "ffn_up", self.xn, rows, self.up)
+            gate, up = self.gate, self.up
+        nat.check(L.aih_silu_mul(h, gate, up, gate, rows * c.ffn), "silu*up")
+        self._mm(p + "ffn_down", gate, rows, self.tmp)
         nat.check(L.aih_add(h, self.x, self.tmp, self.x, rows * c.dim), "residual")
 
     def head(self, row_ptr, pos, hist_offset):
@@ -230,7 +290,7 @@ class LlamaDecoder:
             self.graph = None
         nat.check(self.L.aih_memcpy_h2d(self.h, self.ids, ids.ctypes.data, ids.nbytes), "ids")
         qt, tb, vocab, dim = self.w["token_embd"]
-        nat.check(self.L.aih_embed_q(self.h, qt, tb.get_pointer(), vocab, dim, self.ids, n, self.x), "embed")
+        nat.check(self.L.aih_embed_q(self.h, qt, tb, vocab, dim, self.ids, n, self.x), "embed")
         for l in range(c.n_layers):
             self.layer(l, n, 0, None)
         # decode bookkeeping: the first token is history[0]; position becomes n
@@ -245,7 +305,7 @@ class LlamaDecoder:
         memory (capturable into a graph)."""
         c = self.cfg
         qt, tb, vocab, dim = self.w["token_embd"]
-        nat.check(self.L.aih_embed_q(self.h, qt, tb.get_pointer(), vocab, dim, self.token, 1, self.x), "embed")
+        nat.check(self.L.aih_embed_q(self.h, qt, tb, vocab, dim, self.token, 1, self.x), "embed")
         for l in range(c.n_layers):
             self.layer(l, 1, 0, self.pos)
         self.head(self.x, self.pos, self.n_prompt - 1)

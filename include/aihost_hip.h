@@ -196,6 +196,16 @@ int aih_rope(aih_ctx *ctx, const float *X, int64_t ldx, float *Y, int64_t ldy, i
              int32_t head_dim, int32_t start, const int32_t *pos, const float *table, int32_t table_rows,
              int y_at_pos, int64_t y_rows);
 
+/* The three position steps of a layer in one launch: RoPE of the query heads
+ * of Q in place, RoPE of the key heads of K into the K cache at their
+ * positions, V rows into the V cache (cache rows n_kv_heads*head_dim floats;
+ * positions at or past cache_rows are skipped).  Q/K/V row strides ldq/ldk/ldv
+ * let them be parts of one fused projection output.  Same results as
+ * aih_rope (Q), aih_rope with y_at_pos (K) and aih_store_rows (V). */
+int aih_rope_qkv(aih_ctx *ctx, float *Q, int64_t ldq, const float *K, int64_t ldk, const float *V, int64_t ldv,
+                 float *Kc, float *Vc, int64_t rows, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                 int32_t start, const int32_t *pos, const float *table, int32_t table_rows, int64_t cache_rows);
+
 /* KV cache append: Y[(p + r)*cols + c] = X[r*cols + c] for positions below
  * y_rows.  Replaces KVCache.Add's O(L^2) concat (InferenceEngine.cs:598-622). */
 int aih_store_rows(aih_ctx *ctx, const float *X, int64_t rows, int64_t cols, float *Y, int64_t y_rows, int32_t start,
@@ -211,7 +221,7 @@ int aih_silu_mul(aih_ctx *ctx, const float *G, const float *U, float *Y, int64_t
 int aih_add(aih_ctx *ctx, const float *A, const float *B, float *Y, int64_t n);
 
 /* Floats of scratch aih_attention needs for single-query rows with a cache of
- * max_len rows, or a negative status. */
+ * max_len rows (per-split partial results), or a negative status. */
 int64_t aih_attention_scratch_floats(int32_t n_heads, int32_t max_len);
 
 /* Causal grouped-query attention over a KV cache.  Query row i (position
@@ -219,9 +229,9 @@ int64_t aih_attention_scratch_floats(int32_t n_heads, int32_t max_len);
  * h / (n_heads / n_kv_heads):  O = softmax(scale * q K^T) V.  Q and O rows
  * hold n_heads*head_dim floats, cache rows n_kv_heads*head_dim; the rows for
  * the query positions must already be in the cache.  head_dim must be 128.
- * One query row uses a split-over-keys kernel with `scratch`
- * (aih_attention_scratch_floats) and a combine step; more rows use a tiled
- * kernel.  Replaces ComputeOps.MultiHeadAttention and FusedMHAGenerate
+ * One query row uses a split-over-keys kernel and a combine kernel, with
+ * `scratch` (aih_attention_scratch_floats floats); more rows use a tiled
+ * kernel with an online softmax.  Calls sharing a scratch must not overlap.  Replaces ComputeOps.MultiHeadAttention and FusedMHAGenerate
  * (ComputeOps.cs:1015-1102, shaders ComputeShaders.cs:656-733), without the
  * latter's 4096-key limit. */
 int aih_attention(aih_ctx *ctx, const float *Q, const float *Kc, const float *Vc, float *O, int64_t n_q,

@@ -172,8 +172,27 @@ def test_attention_decode_split_boundaries(device, bufs, keys):
     _attn(device, bufs, 1, keys - 1, 640)
 
 
-def test_attention_decode_position_from_device(device, bufs):
-    _attn(device, bufs, 1, 0, 640, pos_dev=517)
+@pytest.mark.parametrize("keys", [4096, 5000, 9000])
+def test_attention_decode_long_context(device, bufs, keys):
+    # more keys than 64 splits of 64: each split walks several sub-chunks
+    _attn(device, bufs, 1, keys - 1, 9000, nh=8, nkv=2)
+
+
+def test_attention_decode_scratch_reused(device, bufs):
+    # one scratch serves consecutive calls at different positions
+    kvd = 8 * 128
+    K, V = rnd(21, 640, kvd), rnd(22, 640, kvd)
+    KC, VC = bufs.up(K), bufs.up(V)
+    nsc = int(L.aih_attention_scratch_floats(32, 640))
+    S = bufs.empty(nsc * 4)
+    scale = float(np.float32(1) / np.sqrt(np.float32(128)))
+    for i, p in enumerate((100, 639, 7, 300)):
+        q = rnd(30 + i, 1, 32 * 128)
+        Q, O = bufs.up(q), bufs.empty(q.nbytes)
+        nat.check(L.aih_attention(device.handle, Q, KC, VC, O, 1, 32, 8, 128, p, None, 640, scale, S, nsc), "attn")
+        ref = ol.attention(q, K, V, [p], 32, 8, 128)
+        o = bufs.read(O, q.size).reshape(q.shape)
+        assert np.linalg.norm(o - ref) / np.linalg.norm(ref) < 1e-5
 
 
 @pytest.mark.parametrize("n_q,start", [(512, 0), (100, 0), (65, 40), (2, 7)])
@@ -223,3 +242,28 @@ def test_argmax_ties_nan_and_history(device, bufs):
     Y = bufs.up(y)
     nat.check(L.aih_argmax(device.handle, Y, 5, T, None, None, 0, 0), "argmax")
     assert bufs.read(T, 1, np.int32)[0] == 0
+
+
+@pytest.mark.parametrize("rows,start,pos_dev", [(1, 0, 517), (40, 0, None), (3, 61, None)])
+def test_rope_qkv_equals_separate_ops(device, bufs, rows, start, pos_dev):
+    nh, nkv, hd, max_len = 32, 8, 128, 640
+    qd, kvd = nh * hd, nkv * hd
+    T, t = _table(device, bufs, 640)
+    fused = rnd(40 + rows, rows, qd + 2 * kvd)               # one fused projection output per row
+    q, k, v = fused[:, :qd], fused[:, qd:qd + kvd], fused[:, qd + kvd:]
+    F = bufs.up(fused)
+    KC, VC = bufs.empty(max_len * kvd * 4, fill=0), bufs.empty(max_len * kvd * 4, fill=0)
+    P = bufs.up(np.array([pos_dev], np.int32)) if pos_dev is not None else None
+    ld = qd + 2 * kvd
+    nat.check(L.aih_rope_qkv(device.handle, F, ld, F + qd * 4, ld, F + (qd + kvd) * 4, ld, KC, VC, rows, nh, nkv, hd,
+                             start, P, T, 640, max_len), "rope_qkv")
+    p0 = start + (pos_dev or 0)
+    pos = list(range(p0, p0 + rows))
+    out = bufs.read(F, fused.size).reshape(fused.shape)
+    kc = bufs.read(KC, max_len * kvd).reshape(max_len, kvd)
+    vc = bufs.read(VC, max_len * kvd).reshape(max_len, kvd)
+    assert np.array_equal(out[:, :qd], ol.rope(q, pos, nh, hd, t))
+    assert np.array_equal(out[:, qd:], fused[:, qd:])                     # K and V inputs untouched
+    assert np.array_equal(kc[p0:p0 + rows], ol.rope(k, pos, nkv, hd, t))
+    assert np.array_equal(vc[p0:p0 + rows], v)
+    assert not kc[:p0].any() and not vc[p0 + rows:].any()

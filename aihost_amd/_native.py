@@ -22,6 +22,7 @@ HIP_ERROR_OUT_OF_MEMORY = 2
 
 F32, Q4_0, Q8_0, Q4_K, Q6_K = 0, 2, 8, 12, 14
 F16_IEEE, F16_REFCPU = 0, 1
+PRE_NONE, PRE_RMSNORM, PRE_SILU_MUL = 0, 1, 2
 
 
 class DeviceInfo(ctypes.Structure):
@@ -60,6 +61,7 @@ SIGNATURES = {
     "aih_row_bytes": (_i64, [_i, _i64]),
     "aih_dequantize": (_i, [_vp, _i, _vp, _vp, _u64, _i]),
     "aih_qmatvec": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i]),
+    "aih_qmatvec_fused": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _vp, _f, _i, _i, _vp]),
     "aih_qgemm": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),
     "aih_matmul_weights_q": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),
     "aih_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _i64, _i64, _f]),

@@ -447,6 +447,25 @@ struct Geom {
     int teams;     // row teams per workgroup (1, 2, 4 or 8)
 };
 
+// Work fused around the product (decode steps of a Llama layer):
+//   pre = kPreNone:    x as given
+//   pre = kPreRmsNorm: x <- (x / sqrt(mean(x^2) + eps)) * x2   (x2 = norm weights;
+//                      every workgroup loads all of x anyway, so it reduces the
+//                      sum of squares itself)
+//   pre = kPreSiluMul: x <- SiLU(x) * x2   (x2 = the up projection, same layout as x)
+//   acc:               Y += W x instead of Y = W x (the residual add)
+// The formulas and their rounding are those of aih_rmsnorm, aih_silu_mul and
+// aih_add; everything happens outside the row loop.
+enum { kPreNone = 0, kPreRmsNorm = 1, kPreSiluMul = 2 };
+struct Fuse {
+    const float *x2;
+    float eps;
+    int pre;
+    int acc;
+};
+
+__device__ __forceinline__ float silu_f(float g) { return g * (1.0f / (1.0f + expf(-g))); }
+
 // A workgroup is TEAMS row teams of geo.wr waves (ONEWAVE: geo.wr == 1).
 // Team t of workgroup w visits the row groups c = w, w + gridDim.x, ... and
 // computes row c*TEAMS + t of each.
@@ -471,10 +490,10 @@ struct Geom {
 //     compiler then waits at the head for loads meant to stay in flight.
 // W is deliberately not __restrict__: that would let the compiler sink the
 // first weight loads below the LDS barrier of the activation exchange.
-template <class T, int B, int TEAMS, bool ONEWAVE, int MAXT>
+template <class T, int B, int TEAMS, bool ONEWAVE, int MAXT, bool FUSED>
 __global__ void __launch_bounds__(MAXT)
 qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
-               const float *__restrict__ X, int64_t ldx, float *__restrict__ Y, int64_t ldy)
+               const float *__restrict__ X, int64_t ldx, float *__restrict__ Y, int64_t ldy, Fuse fz)
 {
     extern __shared__ __align__(16) uint32_t xs[];
     __shared__ float red[2][MAXT / 64][B];
@@ -512,6 +531,21 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
     for (int b = 0; b < B; ++b)
 #pragma unroll
         for (int k = 0; k < NST; ++k) xv[b][k] = ldg<f4>(X + b * ldx + T::step(u, team * NST + k).src);
+    // The second operand of a fused prologue: with several teams (a few
+    // steps per thread) it is loaded with x, before the weights, so waiting
+    // for it never waits for a weight row; a single team (16 steps per thread,
+    // 128 registers) loads it where it is used.
+    constexpr bool X2_EARLY = TEAMS > 1;
+    f4 x2v[B][X2_EARLY ? NST : 1];
+    auto x2_at = [&](int b, int k) {
+        return ldg<f4>(fz.x2 + (fz.pre == kPreSiluMul ? b * ldx : 0) + T::step(u, team * NST + k).src);
+    };
+    if (FUSED && X2_EARLY && fz.pre != kPreNone) {
+#pragma unroll
+        for (int b = 0; b < B; ++b)
+#pragma unroll
+            for (int k = 0; k < NST; ++k) x2v[b][X2_EARLY ? k : 0] = x2_at(b, k);
+    }
     // The team visits row groups blockIdx.x + i*g while below ngroups (the
     // host launches at most ngroups workgroups and at most 64 row groups per
     // workgroup, so the indices fit in 32 bits and live in scalar registers).
@@ -522,6 +556,62 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
     load_group(c0, ra);
     // keep the weight loads here, in flight during the conversion below
     __builtin_amdgcn_sched_barrier(0);
+
+    auto x2_of = [&](int b, int k) { return X2_EARLY ? x2v[b][X2_EARLY ? k : 0] : x2_at(b, k); };
+    if (!FUSED) {
+        // plain product: x as given
+    } else if (fz.pre == kPreSiluMul) {
+#pragma unroll
+        for (int b = 0; b < B; ++b)
+#pragma unroll
+            for (int k = 0; k < NST; ++k) {
+                f4 &v = xv[b][k];
+                const f4 up = x2_of(b, k);
+                v.x = silu_f(v.x) * up.x;
+                v.y = silu_f(v.y) * up.y;
+                v.z = silu_f(v.z) * up.z;
+                v.w = silu_f(v.w) * up.w;
+            }
+    } else if (fz.pre == kPreRmsNorm) {
+        // The workgroup's threads hold every element of x exactly once
+        // (inactive lanes re-read unit 0 and are left out).
+        float ss[B];
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            ss[b] = 0.f;
+#pragma unroll
+            for (int k = 0; k < NST; ++k) {
+                const f4 v = xv[b][k];
+                ss[b] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            }
+            float t = active ? ss[b] : 0.f;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o);
+            if (lane == 0) red[0][wave][b] = t;
+        }
+        __syncthreads();
+        const int nw = (int)(blockDim.x >> 6);
+        float rms[B];
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            float t = 0.f;
+            for (int w = 0; w < nw; ++w) t += red[0][w][b];
+            rms[b] = sqrtf(t / (float)(geo.units * 64) + fz.eps);
+        }
+        __syncthreads();   // red is reused by the row reductions
+#pragma unroll
+        for (int k = 0; k < NST; ++k) {
+            const f4 w = x2_of(0, k);
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                f4 &v = xv[b][k];
+                v.x = (v.x / rms[b]) * w.x;
+                v.y = (v.y / rms[b]) * w.y;
+                v.z = (v.z / rms[b]) * w.z;
+                v.w = (v.w / rms[b]) * w.w;
+            }
+        }
+    }
 
     typedef typename std::conditional<TEAMS == 1, XRegs<B, T::kSums>, XLds<B, T::kSums>>::type XA;
     XA xa;
@@ -645,7 +735,7 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
     const int64_t n = (c0 + (int64_t)lane * g) * TEAMS + team;
     if (leader && lane < kept && n < N) {
 #pragma unroll
-        for (int b = 0; b < B; ++b) Y[b * ldy + n] = yb[b];
+        for (int b = 0; b < B; ++b) Y[b * ldy + n] = FUSED && fz.acc ? Y[b * ldy + n] + yb[b] : yb[b];
     }
 }
 
@@ -666,8 +756,11 @@ Geom make_geom(int64_t K)
 // with 4-7 workgroups per CU.
 template <class T, int B, int TEAMS, bool ONEWAVE, int MAXT>
 int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
-           const float *X, int64_t ldx, float *Y, int64_t ldy)
+           const float *X, int64_t ldx, float *Y, int64_t ldy, Fuse fz)
 {
+    // fused prologue / epilogue kernels exist for one column only
+    const bool fused = fz.pre != kPreNone || fz.acc;
+    if (fused && B != 1) return AIH_E_INVALID;
     const int threads = TEAMS * geo.wr * 64;
     const size_t lds = TEAMS > 1 ? (size_t)B * kLdsBytesPerUnit * geo.wr * 64 : 0;
     const int64_t cap = ctx->cu_count > 0 ? ctx->cu_count : 256;
@@ -686,8 +779,14 @@ int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t row_bytes, Geom ge
         const int64_t nr = nmain - r0 < rows_per_launch ? nmain - r0 : rows_per_launch;
         const int64_t ng = nr / TEAMS;
         const int64_t grid = ng < cap ? ng : cap;
-        hipLaunchKernelGGL((qmatvec_kernel<T, B, TEAMS, ONEWAVE, MAXT>), dim3((unsigned)grid), dim3(threads), lds,
-                           ctx->stream, W + r0 * row_bytes, nr, row_bytes, geo, X, ldx, Y + r0, ldy);
+        if (fused)
+            hipLaunchKernelGGL((qmatvec_kernel<T, B, TEAMS, ONEWAVE, MAXT, B == 1>), dim3((unsigned)grid),
+                               dim3(threads), lds, ctx->stream, W + r0 * row_bytes, nr, row_bytes, geo, X, ldx,
+                               Y + r0, ldy, fz);
+        else
+            hipLaunchKernelGGL((qmatvec_kernel<T, B, TEAMS, ONEWAVE, MAXT, false>), dim3((unsigned)grid),
+                               dim3(threads), lds, ctx->stream, W + r0 * row_bytes, nr, row_bytes, geo, X, ldx,
+                               Y + r0, ldy, fz);
         const int rc = aih_launch_status();
         if (rc) return rc;
     }
@@ -696,8 +795,10 @@ int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t row_bytes, Geom ge
             Geom g1 = geo;
             g1.teams = 1;
             for (int b = 0; b < B; ++b) {
+                Fuse f1 = fz;
+                if (f1.pre == kPreSiluMul) f1.x2 += b * ldx;
                 const int rc = launch<T, 1, 1, false, 1024>(ctx, W + nmain * row_bytes, N - nmain, row_bytes, g1,
-                                                            X + b * ldx, ldx, Y + b * ldy + nmain, ldy);
+                                                            X + b * ldx, ldx, Y + b * ldy + nmain, ldy, f1);
                 if (rc) return rc;
             }
         }
@@ -708,18 +809,22 @@ int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t row_bytes, Geom ge
 // One pass over W for `two` ? 2 : 1 activation columns.
 template <class T>
 int launch_pass(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
-                const float *X, int64_t ldx, float *Y, int64_t ldy, bool two)
+                const float *X, int64_t ldx, float *Y, int64_t ldy, bool two, Fuse fz)
 {
     switch (geo.teams) {
-    case 8: return two ? launch<T, 2, 8, true, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy)
-                       : launch<T, 1, 8, true, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy);
-    case 4: return two ? launch<T, 2, 4, false, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy)
-                       : launch<T, 1, 4, false, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy);
-    case 2: return two ? launch<T, 2, 2, false, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy)
-                       : launch<T, 1, 2, false, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy);
+    case 8: return two ? launch<T, 2, 8, true, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, fz)
+                       : launch<T, 1, 8, true, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, fz);
+    case 4: return two ? launch<T, 2, 4, false, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, fz)
+                       : launch<T, 1, 4, false, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, fz);
+    case 2: return two ? launch<T, 2, 2, false, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, fz)
+                       : launch<T, 1, 2, false, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, fz);
     default: {  // one team of up to 16 waves: one column per pass within 128 VGPRs
-        int rc = launch<T, 1, 1, false, 1024>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy);
-        if (!rc && two) rc = launch<T, 1, 1, false, 1024>(ctx, W, N, row_bytes, geo, X + ldx, ldx, Y + ldy, ldy);
+        int rc = launch<T, 1, 1, false, 1024>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, fz);
+        if (!rc && two) {
+            Fuse f1 = fz;
+            if (f1.pre == kPreSiluMul) f1.x2 += ldx;
+            rc = launch<T, 1, 1, false, 1024>(ctx, W, N, row_bytes, geo, X + ldx, ldx, Y + ldy, ldy, f1);
+        }
         return rc;
     }
     }
@@ -727,13 +832,15 @@ int launch_pass(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t row_bytes, Ge
 
 template <class T>
 int launch_type(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
-                const float *X, int64_t ldx, float *Y, int64_t ldy, int batch)
+                const float *X, int64_t ldx, float *Y, int64_t ldy, int batch, Fuse fz)
 {
     const Geom geo = make_geom(K);
     // Columns are processed in passes of at most two; each pass re-reads W.
     for (int b0 = 0; b0 < batch; b0 += 2) {
+        Fuse fb = fz;
+        if (fb.pre == kPreSiluMul) fb.x2 += b0 * ldx;
         const int rc = launch_pass<T>(ctx, W, N, row_bytes, geo, X + b0 * ldx, ldx, Y + b0 * ldy, ldy,
-                                      batch - b0 >= 2);
+                                      batch - b0 >= 2, fb);
         if (rc) return rc;
     }
     return AIH_OK;
@@ -744,25 +851,51 @@ constexpr int kMfmaMinBatch = 3;
 
 }  // namespace
 
-int aih_launch_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
-                       const float *X, int64_t ldx, float *Y, int64_t ldy, int batch)
+namespace {
+
+int dispatch(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *X, int64_t ldx, float *Y,
+             int64_t ldy, int batch, Fuse fz)
+{
+    const int64_t rb = aih_row_bytes(type, K);
+    const uint8_t *w = static_cast<const uint8_t *>(W);
+    switch (type) {
+    case AIH_TYPE_Q4_K: return launch_type<Q4K>(ctx, w, N, K, rb, X, ldx, Y, ldy, batch, fz);
+    case AIH_TYPE_Q6_K: return launch_type<Q6K>(ctx, w, N, K, rb, X, ldx, Y, ldy, batch, fz);
+    case AIH_TYPE_Q8_0: return launch_type<Q80>(ctx, w, N, K, rb, X, ldx, Y, ldy, batch, fz);
+    case AIH_TYPE_Q4_0: return launch_type<Q40>(ctx, w, N, K, rb, X, ldx, Y, ldy, batch, fz);
+    default: return AIH_E_UNSUPPORTED;
+    }
+}
+
+// Shape and pointer checks shared by both entry points.
+int check_args(int64_t K, const void *W, const float *X, int64_t ldx)
 {
     // Every kernel reads 64-element units: K must be a multiple of 64, and a
     // row team (one lane per unit) holds at most 1024 lanes.
     if (K % 64 != 0) return AIH_E_LIMIT;
     if (K / 64 > 1024) return AIH_E_LIMIT;
-    const uintptr_t wa = reinterpret_cast<uintptr_t>(W);
-    if (wa % 16 != 0) return AIH_E_INVALID;
+    if (reinterpret_cast<uintptr_t>(W) % 16 != 0) return AIH_E_INVALID;
     if (reinterpret_cast<uintptr_t>(X) % 16 != 0 || (ldx % 4) != 0) return AIH_E_INVALID;
+    return AIH_OK;
+}
+
+}  // namespace
+
+int aih_launch_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
+                       const float *X, int64_t ldx, float *Y, int64_t ldy, int batch)
+{
+    const int rc = check_args(K, W, X, ldx);
+    if (rc) return rc;
     // Three or more columns: the MFMA kernel reads W once for all of them.
     if (batch >= kMfmaMinBatch) return aih_launch_qmatvec_mfma(ctx, type, W, N, K, X, ldx, Y, ldy, batch);
-    const int64_t rb = aih_row_bytes(type, K);
-    const uint8_t *w = static_cast<const uint8_t *>(W);
-    switch (type) {
-    case AIH_TYPE_Q4_K: return launch_type<Q4K>(ctx, w, N, K, rb, X, ldx, Y, ldy, batch);
-    case AIH_TYPE_Q6_K: return launch_type<Q6K>(ctx, w, N, K, rb, X, ldx, Y, ldy, batch);
-    case AIH_TYPE_Q8_0: return launch_type<Q80>(ctx, w, N, K, rb, X, ldx, Y, ldy, batch);
-    case AIH_TYPE_Q4_0: return launch_type<Q40>(ctx, w, N, K, rb, X, ldx, Y, ldy, batch);
-    default: return AIH_E_UNSUPPORTED;
-    }
+    return dispatch(ctx, type, W, N, K, X, ldx, Y, ldy, batch, Fuse{nullptr, 0.f, kPreNone, 0});
+}
+
+int aih_launch_qmatvec_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *X,
+                             const float *X2, float eps, int pre, int accumulate, float *Y)
+{
+    const int rc = check_args(K, W, X, K);
+    if (rc) return rc;
+    if (pre != kPreNone && reinterpret_cast<uintptr_t>(X2) % 16 != 0) return AIH_E_INVALID;
+    return dispatch(ctx, type, W, N, K, X, K, Y, N, 1, Fuse{X2, eps, pre, accumulate ? 1 : 0});
 }

@@ -233,17 +233,29 @@ class LlamaDecoder:
         nat.check(self.L.aih_rmsnorm(self.h, X, self.w.ptr(name), Y, rows, self.cfg.dim, self.cfg.eps),
                   "rmsnorm %s" % name)
 
+    def _mmf(self, name, X, X2, pre, acc, Y):
+        """Decode matvec with a fused prologue (RMSNorm or SiLU*up) and/or the
+        residual add (aih_qmatvec_fused)."""
+        qt, ptr, n, k = self.w[name]
+        nat.check(self.L.aih_qmatvec_fused(self.h, qt, ptr, n, k, X, X2, self.cfg.eps, pre, acc, Y),
+                  "fused matvec %s" % name)
+
     def layer(self, l, rows, start, pos):
         """One decoder layer over `rows` activation rows at positions start..
-        (+*pos when pos is a device pointer).  A single row (decode) uses the
-        fused Q|K|V and gate|up matvecs when the weights have them."""
+        (+*pos when pos is a device pointer).  A single row (decode) runs as
+        seven kernels: Q|K|V matvec with the attention RMSNorm fused in,
+        RoPE + KV cache, attention (two), W_o matvec adding into x, gate|up
+        matvec with the FFN RMSNorm fused in, down matvec with SiLU*up fused
+        in and adding into x.  Several rows (prefill) use the GEMM and the
+        separate operators."""
         c, L, h, p = self.cfg, self.L, self.h, "blk.%d." % l
         qd = c.n_heads * c.head_dim
-        self._norm(p + "attn_norm", self.x, self.xn, rows)
-        if rows == 1 and p + "attn_qkv" in self.w:
-            self._mm(p + "attn_qkv", self.xn, 1, self.qkv)
+        decode = rows == 1 and p + "attn_qkv" in self.w and p + "ffn_gate_up" in self.w
+        if decode:
+            self._mmf(p + "attn_qkv", self.x, self.w.ptr(p + "attn_norm"), nat.PRE_RMSNORM, 0, self.qkv)
             q, k, v = self.qkv, self.qkv + qd * 4, self.qkv + (qd + c.kv_dim) * 4
         else:
+            self._norm(p + "attn_norm", self.x, self.xn, rows)
             self._mm(p + "attn_q", self.xn, rows, self.q)
             self._mm(p + "attn_k", self.xn, rows, self.k)
             self._mm(p + "attn_v", self.xn, rows, self.v)
@@ -254,26 +266,25 @@ class LlamaDecoder:
         nat.check(L.aih_attention(h, q, self.kc[l], self.vc[l], self.att, rows, c.n_heads, c.n_kv_heads,
                                   c.head_dim, start, pos, self.max_len, self.scale, self.scratch,
                                   self.scratch_floats), "attention")
+        if decode:
+            self._mmf(p + "attn_output", self.att, None, nat.PRE_NONE, 1, self.x)
+            self._mmf(p + "ffn_gate_up", self.x, self.w.ptr(p + "ffn_norm"), nat.PRE_RMSNORM, 0, self.gu)
+            self._mmf(p + "ffn_down", self.gu, self.gu + c.ffn * 4, nat.PRE_SILU_MUL, 1, self.x)
+            return
         self._mm(p + "attn_output", self.att, rows, self.tmp)
         nat.check(L.aih_add(h, self.x, self.tmp, self.x, rows * c.dim), "residual")
         self._norm(p + "ffn_norm", self.x, self.xn, rows)
-        if rows == 1 and p + "ffn_gate_up" in self.w:
-            self._mm(p + "ffn_gate_up", self.xn, 1, self.gu)
-            gate, up = self.gu, self.gu + c.ffn * 4
-        else:
-            self._mm(p + "ffn_gate", self.xn, rows, self.gate)
-            self._mm(p + "ffn_up", self.xn, rows, self.up)
-            gate, up = self.gate, self.up
-        nat.check(L.aih_silu_mul(h, gate, up, gate, rows * c.ffn), "silu*up")
-        self._mm(p + "ffn_down", gate, rows, self.tmp)
+        self._mm(p + "ffn_gate", self.xn, rows, self.gate)
+        self._mm(p + "ffn_up", self.xn, rows, self.up)
+        nat.check(L.aih_silu_mul(h, self.gate, self.up, self.gate, rows * c.ffn), "silu*up")
+        self._mm(p + "ffn_down", self.gate, rows, self.tmp)
         nat.check(L.aih_add(h, self.x, self.tmp, self.x, rows * c.dim), "residual")
 
     def head(self, row_ptr, pos, hist_offset):
         """Output norm + vocabulary projection of one row, then the greedy
         token (and history / position update when pos is given)."""
         c = self.cfg
-        self._norm("output_norm", row_ptr, self.xn, 1)
-        self._mm("output", self.xn, 1, self.logits)
+        self._mmf("output", row_ptr, self.w.ptr("output_norm"), nat.PRE_RMSNORM, 0, self.logits)
         nat.check(self.L.aih_argmax(self.h, self.logits, c.vocab, self.token, pos, self.history, self.history_len,
                                     hist_offset), "argmax")
 

@@ -151,6 +151,24 @@ int aih_dequantize(aih_ctx *ctx, int type, const void *q, float *out,
 int aih_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
                 const float *X, int64_t ldx, float *Y, int64_t ldy, int batch);
 
+/* Decode matvec (one column) with the neighbouring element-wise steps of a
+ * Llama layer fused in, so that a decode step needs no separate kernels for
+ * them:
+ *   pre = AIH_PRE_NONE       x = X
+ *   pre = AIH_PRE_RMSNORM    x = (X / sqrt(mean(X^2) + eps)) * X2   (X2: norm weights)
+ *   pre = AIH_PRE_SILU_MUL   x = SiLU(X) * X2                        (X2: the up projection)
+ *   accumulate != 0          Y[n] += sum_k x[k] W[n, k]  (the residual add), else Y[n] = ...
+ * with the formulas of aih_rmsnorm, aih_silu_mul and aih_add.  X, X2 16-byte
+ * aligned; Y must not alias X or X2.  Replaces, for a decode step, the
+ * LayerNorm / SiLU+Multiply / Add around MatMulWeights in
+ * ComputeOps.TransformerLayer (ComputeOps.cs:1250-1356) and FeedForward
+ * (ComputeOps.cs:1218-1241). */
+#define AIH_PRE_NONE     0
+#define AIH_PRE_RMSNORM  1
+#define AIH_PRE_SILU_MUL 2
+int aih_qmatvec_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *X,
+                      const float *X2, float eps, int pre, int accumulate, float *Y);
+
 /* Prefill GEMM, dequantization fused:  Y[m*N + n] = sum_k X[m*K + k] * W[n, k].
  * X is converted once to fp16 in a context workspace (M*K*2 bytes, grown on
  * demand and kept until aih_destroy); tiles of W are dequantized into LDS as

@@ -23,6 +23,7 @@ HIP_ERROR_OUT_OF_MEMORY = 2
 F32, Q4_0, Q8_0, Q4_K, Q6_K = 0, 2, 8, 12, 14
 F16_IEEE, F16_REFCPU = 0, 1
 PRE_NONE, PRE_RMSNORM, PRE_SILU_MUL = 0, 1, 2
+POST_STORE, POST_ACCUMULATE, POST_SILU_PAIRS = 0, 1, 2
 
 
 class DeviceInfo(ctypes.Structure):
@@ -72,10 +73,13 @@ SIGNATURES = {
                           ctypes.c_int32, ctypes.c_int32, _vp, _vp, ctypes.c_int32, _i64]),
     "aih_store_rows": (_i, [_vp, _vp, _i64, _i64, _vp, _i64, ctypes.c_int32, _vp]),
     "aih_silu_mul": (_i, [_vp, _vp, _vp, _vp, _i64]),
+    "aih_silu_mul_pairs": (_i, [_vp, _vp, _vp, _i64, _i64]),
     "aih_add": (_i, [_vp, _vp, _vp, _vp, _i64]),
     "aih_attention_scratch_floats": (_i64, [ctypes.c_int32, ctypes.c_int32]),
     "aih_attention": (_i, [_vp, _vp, _vp, _vp, _vp, _i64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                            ctypes.c_int32, _vp, ctypes.c_int32, _f, _vp, _i64]),
+    "aih_attention_decode_qkv": (_i, [_vp, _vp, _vp, _vp, _vp, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                      ctypes.c_int32, _vp, _vp, ctypes.c_int32, ctypes.c_int32, _f, _vp, _i64]),
     "aih_embed_q": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),
     "aih_argmax": (_i, [_vp, _vp, _i64, _vp, _vp, _vp, _i64, ctypes.c_int32]),
     "aih_sync": (_i, [_vp]),

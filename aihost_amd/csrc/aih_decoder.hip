@@ -218,6 +218,18 @@ silu_mul_kernel(const float *G, const float *U, float *Y, int64_t n)
 }
 
 __global__ void __launch_bounds__(256)
+silu_mul_pairs_kernel(const float *__restrict__ X, float *__restrict__ Y, int64_t rows, int64_t n)
+{
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < rows * n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / n, c = i % n;
+        const float g = X[r * 2 * n + 2 * c];
+        const float sig = 1.0f / (1.0f + expf(-g));
+        Y[i] = (g * sig) * X[r * 2 * n + 2 * c + 1];
+    }
+}
+
+__global__ void __launch_bounds__(256)
 add_kernel(const float *A, const float *B, float *Y, int64_t n)
 {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
@@ -262,7 +274,7 @@ attn_decode_partial(const float *__restrict__ Q, const float *__restrict__ Kc, c
     const int h = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
     const int kvh = h / (n_heads / n_kv_heads);
     const int64_t kv_stride = (int64_t)n_kv_heads * kHD;
-    const int32_t L = min(dev_pos(start, pos) + 1, max_len);   // keys 0..p, within the cache
+    const int32_t L = max(0, min(dev_pos(start, pos) + 1, max_len));   // keys 0..p, within the cache
     const int32_t chunk = (L + n_split - 1) / n_split;
     const int32_t j0 = min(s * chunk, L), j1 = min(L, j0 + chunk);
     if (t < kHD) qs[t] = Q[(int64_t)h * kHD + t];
@@ -341,16 +353,224 @@ attn_decode_partial(const float *__restrict__ Q, const float *__restrict__ Kc, c
     }
 }
 
+// Decode attention of one query row fused with the position steps before it.
+// Workgroup (kvh, s) serves the G = n_heads / n_kv_heads query heads of KV
+// head kvh over split s of the keys 0..L-1 (L = min(p + 1, cache_rows), p =
+// start + *pos), so each cached K/V row is read once for the G heads.  It
+// applies RoPE to the G query heads of the projection output QKV (q | k | v
+// of one row) itself, and the workgroup whose split holds key p ropes that
+// key, stores the key and value rows into the caches at row p and uses them
+// from LDS (no other workgroup reads row p).  Per head, the arithmetic and its
+// order are those of rope_qkv_kernel followed by attn_decode_partial, so the
+// partials are the same bits.
+template <int G>
+__global__ void __launch_bounds__(256)
+attn_decode_qkv_partial(const float *__restrict__ QKV, float *Kc, float *Vc, float *__restrict__ part,
+                        int32_t n_heads, int32_t n_kv_heads, int32_t start, const int32_t *pos,
+                        const float *__restrict__ table, int32_t table_rows, int32_t cache_rows, float scale,
+                        int32_t n_split)
+{
+    __shared__ f4 qs[G][kHD / 4];
+    __shared__ f4 kn[kHD / 4], vn[kHD / 4];
+    __shared__ float ps[G][kSub];
+    __shared__ float red[4][G];
+    __shared__ f4 accs[8][G][kHD / 4];
+    const int kvh = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
+    constexpr int half = kHD / 2;
+    const int64_t kv_stride = (int64_t)n_kv_heads * kHD;
+    const int32_t p = dev_pos(start, pos);
+    const int32_t L = max(0, min(p + 1, cache_rows));
+    const int32_t chunk = (L + n_split - 1) / n_split;
+    const int32_t j0 = min(s * chunk, L), j1 = min(L, j0 + chunk);
+    const bool own = j0 <= p && p < j1;   // this split holds the new key
+    const bool rot = p >= 0 && p < table_rows;
+    const float *tp = table + 2 * (int64_t)(rot ? p : 0) * half;
+    // Thread t scores key t/4 of a sub-chunk over dims 32*(t%4).. and
+    // accumulates V dims 4*(t%32).. for keys t/32 + 8u.  The K and V rows of
+    // the first sub-chunk are loaded before the query phase (their addresses
+    // depend on p only); row p itself, when this split holds it, is taken
+    // from LDS after the barrier instead.
+    const int kk = t >> 2, part4 = t & 3;
+    const int vc = t & 31, vr = t >> 5;
+    f4 k[8], vv[kSub / 8];
+    auto load_k = [&](int32_t c0) {
+        if (kk < min(kSub, j1 - c0)) {
+            const f4 *k4 = reinterpret_cast<const f4 *>(Kc + (int64_t)(c0 + kk) * kv_stride + kvh * kHD) + part4 * 8;
+#pragma unroll
+            for (int d = 0; d < 8; ++d) k[d] = k4[d];
+        }
+    };
+    auto load_v = [&](int32_t c0) {
+        const int n = min(kSub, j1 - c0);
+#pragma unroll
+        for (int u = 0; u < kSub / 8; ++u) {
+            const int j = vr + 8 * u;
+            vv[u] = j < n ? reinterpret_cast<const f4 *>(Vc + (int64_t)(c0 + j) * kv_stride + kvh * kHD)[vc]
+                          : f4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    if (j0 < j1) {
+        load_v(j0);
+        load_k(j0);
+    }
+    // RoPE of the G query heads into LDS: pair i of head g
+    for (int e = t; e < G * half; e += 256) {
+        const int g = e / half, i = e % half;
+        const float *x = QKV + (int64_t)(kvh * G + g) * kHD + 2 * i;
+        const float x0 = x[0], x1 = x[1];
+        float *y = reinterpret_cast<float *>(&qs[g][0]) + 2 * i;
+        if (rot) {
+            const float c = tp[2 * i], sn = tp[2 * i + 1];
+            y[0] = x0 * c - x1 * sn;
+            y[1] = x0 * sn + x1 * c;
+        } else {
+            y[0] = x0;
+            y[1] = x1;
+        }
+    }
+    if (own) {
+        const float *kx = QKV + (int64_t)n_heads * kHD + (int64_t)kvh * kHD;
+        const float *vx = kx + kv_stride;
+        if (t < half) {
+            const float c = tp[2 * t], sn = tp[2 * t + 1];
+            const float x0 = kx[2 * t], x1 = kx[2 * t + 1];
+            const float y0 = x0 * c - x1 * sn, y1 = x0 * sn + x1 * c;
+            float *kq = reinterpret_cast<float *>(kn) + 2 * t;
+            kq[0] = y0;
+            kq[1] = y1;
+            float *kc = Kc + (int64_t)p * kv_stride + (int64_t)kvh * kHD + 2 * t;
+            kc[0] = y0;
+            kc[1] = y1;
+        } else if (t < half + kHD / 4) {
+            const int i = t - half;
+            const f4 v = reinterpret_cast<const f4 *>(vx)[i];
+            vn[i] = v;
+            reinterpret_cast<f4 *>(Vc + (int64_t)p * kv_stride + (int64_t)kvh * kHD)[i] = v;
+        }
+    }
+    __syncthreads();
+    float m[G], l[G];
+    f4 acc[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.f;
+        acc[g] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int32_t c0 = j0; c0 < j1; c0 += kSub) {
+        const int n = min(kSub, j1 - c0);
+        if (c0 + kk == p) {
+#pragma unroll
+            for (int d = 0; d < 8; ++d) k[d] = kn[part4 * 8 + d];
+        }
+#pragma unroll
+        for (int u = 0; u < kSub / 8; ++u)
+            if (c0 + vr + 8 * u == p) vv[u] = vn[vc];
+        float sc[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) sc[g] = -INFINITY;
+        if (kk < n) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float a = 0.f;
+#pragma unroll
+                for (int d = 0; d < 8; ++d) {
+                    const f4 q = qs[g][part4 * 8 + d];
+                    a = fmaf(q.x, k[d].x, a);
+                    a = fmaf(q.y, k[d].y, a);
+                    a = fmaf(q.z, k[d].z, a);
+                    a = fmaf(q.w, k[d].w, a);
+                }
+                a += __shfl_xor(a, 1);
+                a += __shfl_xor(a, 2);
+                sc[g] = a * scale;
+            }
+        }
+        if (c0 + kSub < j1) load_k(c0 + kSub);   // the next sub-chunk's keys, while this one finishes
+        float mn[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float mc = sc[g];
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) mc = fmaxf(mc, __shfl_xor(mc, o));
+            if ((t & 63) == 0) red[t >> 6][g] = mc;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+            mn[g] = fmaxf(m[g], fmaxf(fmaxf(red[0][g], red[1][g]), fmaxf(red[2][g], red[3][g])));
+        __syncthreads();
+        float e[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            e[g] = kk < n ? expf(sc[g] - mn[g]) : 0.f;
+            if (part4 == 0) ps[g][kk] = e[g];
+            const float w = wave_sum(part4 == 0 ? e[g] : 0.f);
+            if ((t & 63) == 0) red[t >> 6][g] = w;
+        }
+        __syncthreads();   // publishes ps and the partial sums
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float lc = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) lc += red[i][g];
+            const float corr = expf(m[g] - mn[g]);   // 0 on the first sub-chunk
+            l[g] = l[g] * corr + lc;
+            f4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < kSub / 8; ++u) {
+                const int j = vr + 8 * u;
+                const float pj = j < n ? ps[g][j] : 0.f;
+                a.x = fmaf(pj, vv[u].x, a.x);
+                a.y = fmaf(pj, vv[u].y, a.y);
+                a.z = fmaf(pj, vv[u].z, a.z);
+                a.w = fmaf(pj, vv[u].w, a.w);
+            }
+            acc[g] = acc[g] * corr + a;
+            m[g] = mn[g];
+        }
+        if (c0 + kSub < j1) load_v(c0 + kSub);
+        __syncthreads();   // ps and red reused by the next sub-chunk
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) accs[vr][g][vc] = acc[g];
+    __syncthreads();
+    for (int e = t; e < G * kHD; e += 256) {
+        const int g = e / kHD, d = e % kHD;
+        const float *af = reinterpret_cast<const float *>(&accs[0][g][0]);
+        float v = 0.f;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) v += af[r * G * kHD + d];
+        part[((int64_t)(kvh * G + g) * n_split + s) * (kHD + 2) + 2 + d] = v;
+    }
+    if (t < G) {
+        float *mine = part + ((int64_t)(kvh * G + t) * n_split + s) * (kHD + 2);
+        float mt = m[0], lt = l[0];
+#pragma unroll
+        for (int g = 1; g < G; ++g) {
+            mt = t == g ? m[g] : mt;
+            lt = t == g ? l[g] : lt;
+        }
+        mine[0] = j1 > j0 ? mt : -INFINITY;
+        mine[1] = j1 > j0 ? lt : 0.f;
+    }
+}
+
 // Combine the splits of head h: o = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M).
-// Every split's (m, l) is loaded in one round, the weights go through LDS,
-// and the accumulators are read eight splits at a time.
+// The accumulators of the first kPre splits are loaded together with every
+// split's (m, l) (one memory round trip), the weights go through LDS, and
+// the accumulators of further splits are read eight at a time.
 __global__ void __launch_bounds__(kHD)
 attn_decode_combine(const float *__restrict__ part, float *__restrict__ O, int32_t n_split)
 {
+    constexpr int kPre = 16;
     __shared__ float ws[kMaxSplit];
     __shared__ float red[2];
     const int h = blockIdx.x, t = threadIdx.x;
     const float *ph = part + (int64_t)h * n_split * (kHD + 2);
+    float vp[kPre];
+#pragma unroll
+    for (int u = 0; u < kPre; ++u) vp[u] = u < n_split ? ph[u * (kHD + 2) + 2 + t] : 0.f;
     const float mt = t < n_split ? ph[t * (kHD + 2)] : -INFINITY;
     const float lt = t < n_split ? ph[t * (kHD + 2) + 1] : 0.f;
     float M = mt;
@@ -367,7 +587,9 @@ attn_decode_combine(const float *__restrict__ part, float *__restrict__ O, int32
     __syncthreads();
     const float lsum = red[0] + red[1];
     float a = 0.f;
-    for (int i0 = 0; i0 < n_split; i0 += 8) {
+#pragma unroll
+    for (int u = 0; u < kPre; ++u) a = fmaf(vp[u], u < n_split ? ws[u] : 0.f, a);
+    for (int i0 = kPre; i0 < n_split; i0 += 8) {
         float v[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) v[u] = i0 + u < n_split ? ph[(i0 + u) * (kHD + 2) + 2 + t] : 0.f;
@@ -575,6 +797,14 @@ int aih_silu_mul(aih_ctx *ctx, const float *G, const float *U, float *Y, int64_t
     return aih_launch_status();
 }
 
+int aih_silu_mul_pairs(aih_ctx *ctx, const float *X, float *Y, int64_t rows, int64_t n)
+{
+    if (!ctx || !X || !Y || rows < 0 || n < 0) return AIH_E_INVALID;
+    if (rows == 0 || n == 0) return AIH_OK;
+    hipLaunchKernelGGL(silu_mul_pairs_kernel, dim3(grid_for(ctx, rows * n)), dim3(256), 0, ctx->stream, X, Y, rows, n);
+    return aih_launch_status();
+}
+
 int aih_add(aih_ctx *ctx, const float *A, const float *B, float *Y, int64_t n)
 {
     if (!ctx || !A || !B || !Y || n < 0) return AIH_E_INVALID;
@@ -616,6 +846,39 @@ int aih_attention(aih_ctx *ctx, const float *Q, const float *Kc, const float *Vc
     if (tiles > 65535) return AIH_E_LIMIT;
     hipLaunchKernelGGL(attn_prefill_kernel, dim3(n_heads, (unsigned)tiles), dim3(256), 0, ctx->stream, Q, Kc, Vc, O,
                        n_q, n_heads, n_kv_heads, start, pos, max_len, scale);
+    return aih_launch_status();
+}
+
+int aih_attention_decode_qkv(aih_ctx *ctx, const float *QKV, float *Kc, float *Vc, float *O, int32_t n_heads,
+                             int32_t n_kv_heads, int32_t head_dim, int32_t start, const int32_t *pos,
+                             const float *table, int32_t table_rows, int32_t max_len, float scale, float *scratch,
+                             int64_t scratch_floats)
+{
+    if (!ctx || !QKV || !Kc || !Vc || !O || !table || n_heads <= 0 || n_kv_heads <= 0 || max_len <= 0)
+        return AIH_E_INVALID;
+    if (n_heads % n_kv_heads) return AIH_E_INVALID;
+    if (head_dim != kHD) return AIH_E_UNSUPPORTED;
+    if (!aligned16(QKV) || !aligned16(Kc) || !aligned16(Vc) || !aligned16(O)) return AIH_E_INVALID;
+    if (table_rows < max_len) return AIH_E_LIMIT;
+    if (!pos && (start < 0 || start >= max_len)) return AIH_E_LIMIT;
+    const int32_t n_split = decode_splits(max_len);
+    const int64_t n_part = (int64_t)n_heads * n_split * (kHD + 2);
+    if (!scratch || scratch_floats < n_part) return AIH_E_INVALID;
+    const dim3 grid(n_kv_heads, n_split);
+    switch (n_heads / n_kv_heads) {
+    case 1: hipLaunchKernelGGL(attn_decode_qkv_partial<1>, grid, dim3(256), 0, ctx->stream, QKV, Kc, Vc, scratch,
+                               n_heads, n_kv_heads, start, pos, table, table_rows, max_len, scale, n_split); break;
+    case 2: hipLaunchKernelGGL(attn_decode_qkv_partial<2>, grid, dim3(256), 0, ctx->stream, QKV, Kc, Vc, scratch,
+                               n_heads, n_kv_heads, start, pos, table, table_rows, max_len, scale, n_split); break;
+    case 4: hipLaunchKernelGGL(attn_decode_qkv_partial<4>, grid, dim3(256), 0, ctx->stream, QKV, Kc, Vc, scratch,
+                               n_heads, n_kv_heads, start, pos, table, table_rows, max_len, scale, n_split); break;
+    case 8: hipLaunchKernelGGL(attn_decode_qkv_partial<8>, grid, dim3(256), 0, ctx->stream, QKV, Kc, Vc, scratch,
+                               n_heads, n_kv_heads, start, pos, table, table_rows, max_len, scale, n_split); break;
+    default: return AIH_E_UNSUPPORTED;
+    }
+    const int rc = aih_launch_status();
+    if (rc) return rc;
+    hipLaunchKernelGGL(attn_decode_combine, dim3(n_heads), dim3(kHD), 0, ctx->stream, scratch, O, n_split);
     return aih_launch_status();
 }
 

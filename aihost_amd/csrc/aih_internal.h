@@ -81,6 +81,6 @@ int aih_launch_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K
 int aih_launch_qmatvec_mfma(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
                             const float *X, int64_t ldx, float *Y, int64_t ldy, int batch);
 int aih_launch_qmatvec_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *X,
-                             const float *X2, float eps, int pre, int accumulate, float *Y);
+                             const float *X2, float eps, int pre, int post, float *Y);
 int aih_launch_embed(aih_ctx *ctx, int type, const void *table, int64_t vocab, int64_t dim,
                      const int32_t *ids, int64_t n, float *out);

@@ -151,6 +151,8 @@ struct Q4K {
         if (s < 8) return {64 * u + 4 * s, 4 * s, 0, false};
         return {64 * u + 32 + 4 * (s - 8), 4 * (s - 8) + 2, 1, true};
     }
+    // unit and step of the 4 activations x[4e .. 4e+3] (step(u, s).src == 4e)
+    __device__ static void inv(int e, int &u, int &s) { u = e >> 4; s = e & 15; }
     // The row starts at byte `off` of `w`; lane offsets are added to off.
     template <class A>
     __device__ static void load(const A &w, uint32_t off, int u, uint32_t *raw)
@@ -214,6 +216,7 @@ struct Q80 {
     static constexpr int kRaw = 17;
     static constexpr int kSums = 2;
     __device__ static Step step(int u, int s) { return {64 * u + 4 * s, 4 * (s >> 1) + 2 * (s & 1), s >> 3, false}; }
+    __device__ static void inv(int e, int &u, int &s) { u = e >> 4; s = e & 15; }
     template <class A>
     __device__ static void load(const A &w, uint32_t off, int u, uint32_t *raw)
     {
@@ -270,6 +273,7 @@ struct Q40 {
         if (r < 4) return {64 * u + 32 * blk + 4 * r, 4 * (4 * blk + r), blk, false};
         return {64 * u + 32 * blk + 16 + 4 * (r - 4), 4 * (4 * blk + r - 4) + 2, 2 + blk, true};
     }
+    __device__ static void inv(int e, int &u, int &s) { u = e >> 4; s = e & 15; }
     template <class A>
     __device__ static void load(const A &w, uint32_t off, int u, uint32_t *raw)
     {
@@ -329,6 +333,13 @@ struct Q6K {
         const int q = s >> 2, m = s & 3;
         const int base = (u >> 2) * 256 + 128 * ((u >> 1) & 1) + 16 * (u & 1);
         return {base + 32 * q + 4 * m, 4 * (2 * m + (q >> 1)) + 2 * (q & 1), q, q >= 2};
+    }
+    // f4 index jb = 32h + 8q + 4t + m within the 256-element block
+    __device__ static void inv(int e, int &u, int &s)
+    {
+        const int jb = e & 63;
+        u = 4 * (e >> 6) + 2 * (jb >> 5) + ((jb >> 2) & 1);
+        s = 4 * ((jb >> 3) & 3) + (jb & 3);
     }
     template <class A>
     __device__ static void load(const A &w, uint32_t off, int u, uint32_t *raw)
@@ -419,6 +430,11 @@ struct XRegs {
 // unit-major layout (each lane's image contiguous) would put the lanes of a
 // read on a few banks and serialise every LDS access several-fold.
 constexpr int kLdsBytesPerUnit = 8 * 16 + 16 * 4;   // groups + step sums, per column
+// Each row of the group and sum arrays holds kLdsPad entries past the team's
+// units: the conversion writes a wave's 64 consecutive 16-byte activation
+// pieces (4 units x 16 steps) to rows `step` and columns `unit`, and the pad
+// spreads those writes over the banks.
+constexpr int kLdsPad = 4;
 template <int B, int S>
 struct XLds {
     const u4 *grp;   // group 0 of column 0 of this lane's unit
@@ -453,15 +469,22 @@ struct Geom {
 //                      every workgroup loads all of x anyway, so it reduces the
 //                      sum of squares itself)
 //   pre = kPreSiluMul: x <- SiLU(x) * x2   (x2 = the up projection, same layout as x)
-//   acc:               Y += W x instead of Y = W x (the residual add)
+//   post = kPostStore:      Y = W x
+//   post = kPostAccumulate: Y += W x (the residual add)
+//   post = kPostSiluPairs:  rows 2i and 2i+1 of W are a gate row and its up
+//                      row (interleaved gate/up weights); Y[i] = SiLU(y[2i]) *
+//                      y[2i+1], so Y holds N/2 values.  Teams 2j and 2j+1 of a
+//                      workgroup compute such a pair for the same row groups
+//                      and meet in LDS at the end.
 // The formulas and their rounding are those of aih_rmsnorm, aih_silu_mul and
 // aih_add; everything happens outside the row loop.
 enum { kPreNone = 0, kPreRmsNorm = 1, kPreSiluMul = 2 };
+enum { kPostStore = 0, kPostAccumulate = 1, kPostSiluPairs = 2 };
 struct Fuse {
     const float *x2;
     float eps;
     int pre;
-    int acc;
+    int post;
 };
 
 __device__ __forceinline__ float silu_f(float g) { return g * (1.0f / (1.0f + expf(-g))); }
@@ -496,7 +519,7 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
                const float *__restrict__ X, int64_t ldx, float *__restrict__ Y, int64_t ldy, Fuse fz)
 {
     extern __shared__ __align__(16) uint32_t xs[];
-    __shared__ float red[2][MAXT / 64][B];
+    __shared__ float red[MAXT / 64][B];   // RMSNorm prologue: per-wave sums
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -523,14 +546,28 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
             T::load(BufRow{wres, (uint32_t)cc * gstride}, toff, u, raw);
     };
 
-    // The 16 conversion steps of every unit are spread over the teams; a
-    // single team converts all 16 itself.
+    // A single team converts the 16 steps of its units itself (into
+    // registers); several teams convert x once into LDS, each team NST of the
+    // 16 steps of every unit.  Teams of several waves (x above 16 KB) read x
+    // instead in consecutive 16-byte pieces, piece k*threads + tid, and put
+    // each piece into its (unit, step) entry: reading a unit's own pieces
+    // puts the 64 lanes of a load on 64 lines, and once x outgrows L1 every
+    // line is fetched again for each of its 8 pieces (on MI355X the 4096 x
+    // 14336 Q4_K product took 0.5 us longer that way).  For single-wave teams
+    // the per-unit reads measured faster (x fits in L1).
     constexpr int NST = 16 / TEAMS;
+    constexpr bool SPREAD = TEAMS > 1 && !ONEWAVE;
+    const int pieces = 16 * geo.units;
+    auto piece = [&](int k) { return k * (int)blockDim.x + tid; };
+    auto src_of = [&](int k) {
+        if constexpr (SPREAD) return piece(k) < pieces ? 4 * piece(k) : 0;
+        else return T::step(u, team * NST + k).src;
+    };
     f4 xv[B][NST];
 #pragma unroll
     for (int b = 0; b < B; ++b)
 #pragma unroll
-        for (int k = 0; k < NST; ++k) xv[b][k] = ldg<f4>(X + b * ldx + T::step(u, team * NST + k).src);
+        for (int k = 0; k < NST; ++k) xv[b][k] = ldg<f4>(X + b * ldx + src_of(k));
     // The second operand of a fused prologue: with several teams (a few
     // steps per thread) it is loaded with x, before the weights, so waiting
     // for it never waits for a weight row; a single team (16 steps per thread,
@@ -538,7 +575,7 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
     constexpr bool X2_EARLY = TEAMS > 1;
     f4 x2v[B][X2_EARLY ? NST : 1];
     auto x2_at = [&](int b, int k) {
-        return ldg<f4>(fz.x2 + (fz.pre == kPreSiluMul ? b * ldx : 0) + T::step(u, team * NST + k).src);
+        return ldg<f4>(fz.x2 + (fz.pre == kPreSiluMul ? b * ldx : 0) + src_of(k));
     };
     if (FUSED && X2_EARLY && fz.pre != kPreNone) {
 #pragma unroll
@@ -574,7 +611,8 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
             }
     } else if (fz.pre == kPreRmsNorm) {
         // The workgroup's threads hold every element of x exactly once
-        // (inactive lanes re-read unit 0 and are left out).
+        // (inactive lanes re-read unit 0, threads past the last piece x[0..3];
+        // both are left out).
         float ss[B];
 #pragma unroll
         for (int b = 0; b < B; ++b) {
@@ -582,12 +620,13 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
 #pragma unroll
             for (int k = 0; k < NST; ++k) {
                 const f4 v = xv[b][k];
-                ss[b] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+                const float q = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+                ss[b] += !SPREAD || piece(k) < pieces ? q : 0.f;
             }
-            float t = active ? ss[b] : 0.f;
+            float t = SPREAD || active ? ss[b] : 0.f;
 #pragma unroll
             for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o);
-            if (lane == 0) red[0][wave][b] = t;
+            if (lane == 0) red[wave][b] = t;
         }
         __syncthreads();
         const int nw = (int)(blockDim.x >> 6);
@@ -595,10 +634,9 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
 #pragma unroll
         for (int b = 0; b < B; ++b) {
             float t = 0.f;
-            for (int w = 0; w < nw; ++w) t += red[0][w][b];
+            for (int w = 0; w < nw; ++w) t += red[w][b];
             rms[b] = sqrtf(t / (float)(geo.units * 64) + fz.eps);
         }
-        __syncthreads();   // red is reused by the row reductions
 #pragma unroll
         for (int k = 0; k < NST; ++k) {
             const f4 w = x2_of(0, k);
@@ -631,31 +669,37 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
         }
     } else {
         // uint32 view of the group array and float view of the sum array
+        // (rows of tp entries: the team's units and the pad)
+        const int tp = team_threads + kLdsPad;
         uint32_t *gw = xs;
-        float *sums = reinterpret_cast<float *>(xs + (size_t)B * 8 * 4 * team_threads);
+        float *sums = reinterpret_cast<float *>(xs + (size_t)B * 8 * 4 * tp);
 #pragma unroll
-        for (int b = 0; b < B; ++b) {
+        for (int k = 0; k < NST; ++k) {
+            int pu = ut, ps = team * NST + k;
+            if constexpr (SPREAD) {
+                if (piece(k) >= pieces) continue;
+                T::inv(piece(k), pu, ps);
+            }
+            const Step st = T::step(SPREAD ? pu : u, ps);
 #pragma unroll
-            for (int k = 0; k < NST; ++k) {
-                const int s = team * NST + k;
-                const Step st = T::step(u, s);
+            for (int b = 0; b < B; ++b) {
                 uint32_t p0, p1;
                 const float sum = convert_step(xv[b][k], st.div16, p0, p1);
-                uint32_t *e = gw + ((size_t)(b * 8 + st.d0 / 4) * team_threads + ut) * 4 + st.d0 % 4;
+                uint32_t *e = gw + ((size_t)(b * 8 + st.d0 / 4) * tp + pu) * 4 + st.d0 % 4;
                 e[0] = p0;
                 e[1] = p1;
-                sums[(b * 16 + s) * team_threads + ut] = sum;
+                sums[(b * 16 + ps) * tp + pu] = sum;
             }
         }
         __syncthreads();
         xa.grp = reinterpret_cast<const u4 *>(xs) + ut;
-        xa.tt = team_threads;
+        xa.tt = tp;
 #pragma unroll
         for (int b = 0; b < B; ++b) {
 #pragma unroll
             for (int k = 0; k < T::kSums; ++k) xa.s[b][k] = 0.f;
 #pragma unroll
-            for (int q = 0; q < 16; ++q) xa.s[b][T::step(u, q).slot] += sums[(b * 16 + q) * team_threads + ut];
+            for (int q = 0; q < 16; ++q) xa.s[b][T::step(u, q).slot] += sums[(b * 16 + q) * tp + ut];
         }
     }
 
@@ -671,11 +715,10 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
     for (int b = 0; b < B; ++b) yb[b] = 0.f;
     int kept = 0;
 
-    // Dot product of one row, reduced over the team into yb.  `par`
-    // alternates the cross-wave scratch so one barrier per row suffices: a
-    // wave that writes red[par] again has passed the barrier of the row in
-    // between, which every wave reaches only after its reads of red[par].
-    auto row = [&](const uint32_t *raw, int par) {
+    // Dot product of one row, reduced over the wave into lane `kept` of yb.
+    // A team of several waves adds its waves' yb once, after the last row:
+    // no barrier inside the loop, so no wave waits for another's loads.
+    auto row = [&](const uint32_t *raw) {
         float acc[B];
 #pragma unroll
         for (int b = 0; b < B; ++b) acc[b] = 0.f;
@@ -683,21 +726,8 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
 #pragma unroll
         for (int b = 0; b < B; ++b) {
             const float v = wave_sum_to_lane63(active ? acc[b] : 0.f);
-            if (ONEWAVE) {
-                const float tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-                yb[b] = lane == kept ? tot : yb[b];
-            } else if (lane == 63) {
-                red[par][wave][b] = v;
-            }
-        }
-        if (!ONEWAVE) {
-            __syncthreads();
-#pragma unroll
-            for (int b = 0; b < B; ++b) {
-                float tot = 0.f;
-                for (int w = 0; w < wr; ++w) tot += red[par][team * wr + w][b];
-                yb[b] = lane == kept ? tot : yb[b];
-            }
+            const float tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+            yb[b] = lane == kept ? tot : yb[b];
         }
         ++kept;
     };
@@ -711,31 +741,60 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
     __builtin_amdgcn_sched_barrier(0);
     int c = c0;   // ra holds row group c, rb row group c + g
     while (c + 3 * g < ng) {
-        row(ra, 0);
+        row(ra);
         load_group(c + 2 * g, ra);
         __builtin_amdgcn_sched_barrier(0);   // reload issued before the other row is consumed
-        row(rb, 1);
+        row(rb);
         load_group(c + 3 * g, rb);
         __builtin_amdgcn_sched_barrier(0);
         c += 2 * g;
     }
     // here c < ng (c0 < ng, and every iteration leaves c + g < ng)
     if (c + 2 * g < ng) {
-        row(ra, 0);
+        row(ra);
         load_group(c + 2 * g, ra);
         __builtin_amdgcn_sched_barrier(0);
-        row(rb, 1);
-        row(ra, 0);
+        row(rb);
+        row(ra);
     } else if (c + g < ng) {
-        row(ra, 0);
-        row(rb, 1);
+        row(ra);
+        row(rb);
     } else {
-        row(ra, 0);
+        row(ra);
+    }
+    if constexpr (!ONEWAVE) {
+        // the team's first wave adds the partial row sums of its waves, in
+        // wave order
+        __shared__ float part[MAXT / 64][B][64];
+#pragma unroll
+        for (int b = 0; b < B; ++b) part[wave][b][lane] = yb[b];
+        __syncthreads();
+        if (ut < 64) {
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                float tot = 0.f;
+                for (int w = 0; w < wr; ++w) tot += part[team * wr + w][b][lane];
+                yb[b] = tot;
+            }
+        }
     }
     const int64_t n = (c0 + (int64_t)lane * g) * TEAMS + team;
+    if constexpr (FUSED && TEAMS % 2 == 0) {
+        if (fz.post == kPostSiluPairs) {
+            __shared__ float pair_y[TEAMS][64];
+            if (leader) pair_y[team][lane] = yb[0];
+            __syncthreads();
+            if (leader && team % 2 == 0 && lane < kept && n < N) {
+                const float gt = pair_y[team][lane], up = pair_y[team + 1][lane];
+                Y[n / 2] = silu_f(gt) * up;
+            }
+            return;
+        }
+    }
     if (leader && lane < kept && n < N) {
 #pragma unroll
-        for (int b = 0; b < B; ++b) Y[b * ldy + n] = FUSED && fz.acc ? Y[b * ldy + n] + yb[b] : yb[b];
+        for (int b = 0; b < B; ++b)
+            Y[b * ldy + n] = FUSED && fz.post == kPostAccumulate ? Y[b * ldy + n] + yb[b] : yb[b];
     }
 }
 
@@ -758,11 +817,13 @@ template <class T, int B, int TEAMS, bool ONEWAVE, int MAXT>
 int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
            const float *X, int64_t ldx, float *Y, int64_t ldy, Fuse fz)
 {
-    // fused prologue / epilogue kernels exist for one column only
-    const bool fused = fz.pre != kPreNone || fz.acc;
+    // fused prologue / epilogue kernels exist for one column only; gate/up
+    // pairs need pairs of teams (an even team count and whole row groups)
+    const bool fused = fz.pre != kPreNone || fz.post != kPostStore;
     if (fused && B != 1) return AIH_E_INVALID;
+    if (fz.post == kPostSiluPairs && (TEAMS % 2 != 0 || N % TEAMS != 0)) return AIH_E_LIMIT;
     const int threads = TEAMS * geo.wr * 64;
-    const size_t lds = TEAMS > 1 ? (size_t)B * kLdsBytesPerUnit * geo.wr * 64 : 0;
+    const size_t lds = TEAMS > 1 ? (size_t)B * kLdsBytesPerUnit * (geo.wr * 64 + kLdsPad) : 0;
     const int64_t cap = ctx->cu_count > 0 ? ctx->cu_count : 256;
     // A workgroup computes at most 64 row groups per launch (its results are
     // held in one register per lane); taller matrices take several launches.
@@ -779,14 +840,16 @@ int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t row_bytes, Geom ge
         const int64_t nr = nmain - r0 < rows_per_launch ? nmain - r0 : rows_per_launch;
         const int64_t ng = nr / TEAMS;
         const int64_t grid = ng < cap ? ng : cap;
+        // gate/up pairs write one value per two rows (r0 is a multiple of TEAMS)
+        float *ys = Y + (fz.post == kPostSiluPairs ? r0 / 2 : r0);
         if (fused)
             hipLaunchKernelGGL((qmatvec_kernel<T, B, TEAMS, ONEWAVE, MAXT, B == 1>), dim3((unsigned)grid),
                                dim3(threads), lds, ctx->stream, W + r0 * row_bytes, nr, row_bytes, geo, X, ldx,
-                               Y + r0, ldy, fz);
+                               ys, ldy, fz);
         else
             hipLaunchKernelGGL((qmatvec_kernel<T, B, TEAMS, ONEWAVE, MAXT, false>), dim3((unsigned)grid),
                                dim3(threads), lds, ctx->stream, W + r0 * row_bytes, nr, row_bytes, geo, X, ldx,
-                               Y + r0, ldy, fz);
+                               ys, ldy, fz);
         const int rc = aih_launch_status();
         if (rc) return rc;
     }
@@ -888,14 +951,14 @@ int aih_launch_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t
     if (rc) return rc;
     // Three or more columns: the MFMA kernel reads W once for all of them.
     if (batch >= kMfmaMinBatch) return aih_launch_qmatvec_mfma(ctx, type, W, N, K, X, ldx, Y, ldy, batch);
-    return dispatch(ctx, type, W, N, K, X, ldx, Y, ldy, batch, Fuse{nullptr, 0.f, kPreNone, 0});
+    return dispatch(ctx, type, W, N, K, X, ldx, Y, ldy, batch, Fuse{nullptr, 0.f, kPreNone, kPostStore});
 }
 
 int aih_launch_qmatvec_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *X,
-                             const float *X2, float eps, int pre, int accumulate, float *Y)
+                             const float *X2, float eps, int pre, int post, float *Y)
 {
     const int rc = check_args(K, W, X, K);
     if (rc) return rc;
     if (pre != kPreNone && reinterpret_cast<uintptr_t>(X2) % 16 != 0) return AIH_E_INVALID;
-    return dispatch(ctx, type, W, N, K, X, K, Y, N, 1, Fuse{X2, eps, pre, accumulate ? 1 : 0});
+    return dispatch(ctx, type, W, N, K, X, K, Y, N, 1, Fuse{X2, eps, pre, post});
 }

@@ -362,19 +362,21 @@ int aih_dequantize(aih_ctx *ctx, int type, const void *q, float *out,
 }
 
 int aih_qmatvec_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *X,
-                      const float *X2, float eps, int pre, int accumulate, float *Y)
+                      const float *X2, float eps, int pre, int post, float *Y)
 {
     if (!ctx) return AIH_E_INVALID;
     if (!aih_is_quant(type)) return AIH_E_UNSUPPORTED;
     aih_block_geom g = aih_geom(type);
     if (N < 0 || K <= 0 || K % g.elems) return AIH_E_INVALID;
     if (pre < AIH_PRE_NONE || pre > AIH_PRE_SILU_MUL) return AIH_E_INVALID;
+    if (post < AIH_POST_STORE || post > AIH_POST_SILU_PAIRS) return AIH_E_INVALID;
+    if (post == AIH_POST_SILU_PAIRS && N % 2) return AIH_E_INVALID;
     if (pre != AIH_PRE_NONE && !X2) return AIH_E_INVALID;
     if (!N) return AIH_OK;
     if (!W || !X || !Y) return AIH_E_INVALID;
     int rc = select_device(ctx);
     if (rc) return rc;
-    return aih_launch_qmatvec_fused(ctx, type, W, N, K, X, X2, eps, pre, accumulate, Y);
+    return aih_launch_qmatvec_fused(ctx, type, W, N, K, X, X2, eps, pre, post, Y);
 }
 
 int aih_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,

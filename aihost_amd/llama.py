@@ -98,17 +98,24 @@ def synth_weights(cfg, seed=42, distinct_layers=None, head_type=Q6_K):
     return out
 
 
-# Weights stored back to back in one device buffer, so that a decode step
-# runs one matvec over all of them (their outputs land back to back too):
-# Q|K|V share the input x, gate|up share the normed x.
-FUSED_GROUPS = (("attn_qkv", ("attn_q", "attn_k", "attn_v")), ("ffn_gate_up", ("ffn_gate", "ffn_up")))
+# Weights of a layer that share their input and are stored in one device
+# buffer, so that a decode step runs one matvec over them:
+#   "concat"      Q|K|V back to back (outputs land back to back too); the
+#                 members stay reachable as views of the buffer
+#   "interleave"  gate and up rows interleaved (row 2i = gate row i, row
+#                 2i+1 = up row i), the layout aih_qmatvec_fused's SiLU-pairs
+#                 epilogue and aih_silu_mul_pairs read; the members are not
+#                 separate matrices any more
+FUSED_GROUPS = (("attn_qkv", "concat", ("attn_q", "attn_k", "attn_v")),
+                ("ffn_gate_up", "interleave", ("ffn_gate", "ffn_up")))
 
 
 class DeviceWeights:
     """Every tensor of a weight dict in device memory, packed blocks verbatim
     (as aih_upload_tensor places them from a GGUF file).  The matrices of each
-    FUSED_GROUPS group of a layer are placed back to back in one buffer and
-    are also reachable under the group name ("blk.<l>.attn_qkv", ...).
+    FUSED_GROUPS group of a layer share one buffer, reachable under the group
+    name ("blk.<l>.attn_qkv", ...), when they have one format and width (and,
+    to interleave, one height); otherwise they are stored separately.
     Entries are (qtype, device pointer, rows, cols)."""
 
     def __init__(self, device, weights):
@@ -118,28 +125,37 @@ class DeviceWeights:
         grouped = {}
         for name in weights:
             if name.startswith("blk."):
-                pre, suf = name.rsplit(".", 1)[0], name.rsplit(".", 1)[1]
-                for gname, members in FUSED_GROUPS:
+                pre, suf = name.rsplit(".", 1)
+                for gname, layout, members in FUSED_GROUPS:
                     if suf in members:
-                        grouped.setdefault(pre + "." + gname, []).append(name)
+                        grouped.setdefault((pre + "." + gname, layout, members), {})[suf] = name
         try:
             done = set()
-            for gname, names in grouped.items():
-                names = sorted(names, key=lambda n: [m for g, ms in FUSED_GROUPS for m in ms].index(n.rsplit(".", 1)[1]))
+            for (gname, layout, members), found in grouped.items():
+                if len(found) != len(members):
+                    continue
+                names = [found[m] for m in members]
                 qts = {weights[n][0] for n in names}
                 cols = {weights[n][3] for n in names}
-                if len(qts) != 1 or len(cols) != 1:
-                    continue                    # mixed formats or widths: stored separately
-                sizes = [np.ascontiguousarray(weights[n][1]).nbytes for n in names]
-                buf = self._alloc(sum(sizes))
-                off = 0
-                for n, sz in zip(names, sizes):
-                    qt, arr, r, c = weights[n]
-                    self._upload(buf.get_pointer() + off, arr, n)
-                    self.t[n] = (qt, buf.get_pointer() + off, r, c)
-                    off += sz
-                    done.add(n)
-                self.t[gname] = (qts.pop(), buf.get_pointer(), sum(weights[n][2] for n in names), cols.pop())
+                rows = {weights[n][2] for n in names}
+                if len(qts) != 1 or len(cols) != 1 or (layout == "interleave" and len(rows) != 1):
+                    continue
+                arrs = [np.ascontiguousarray(weights[n][1]) for n in names]
+                qt, c = qts.pop(), cols.pop()
+                buf = self._alloc(sum(a.nbytes for a in arrs))
+                if layout == "concat":
+                    off = 0
+                    for n, a in zip(names, arrs):
+                        self._upload(buf.get_pointer() + off, a, n)
+                        self.t[n] = (qt, buf.get_pointer() + off, weights[n][2], c)
+                        off += a.nbytes
+                else:
+                    r = rows.pop()
+                    rb = arrs[0].nbytes // r
+                    rows_of = [a.reshape(-1).view(np.uint8).reshape(r, rb) for a in arrs]
+                    self._upload(buf.get_pointer(), np.stack(rows_of, axis=1), gname)
+                done.update(names)
+                self.t[gname] = (qt, buf.get_pointer(), sum(weights[n][2] for n in names), c)
             for name, (qt, arr, r, c) in weights.items():
                 if name in done:
                     continue
@@ -203,10 +219,12 @@ class LlamaDecoder:
         self.x, self.xn = buf(P * c.dim * 4), buf(P * c.dim * 4)
         self.q, self.att, self.tmp = buf(P * qd * 4), buf(P * qd * 4), buf(P * c.dim * 4)
         self.k, self.v = buf(P * c.kv_dim * 4), buf(P * c.kv_dim * 4)
-        self.gate, self.up = buf(P * c.ffn * 4), buf(P * c.ffn * 4)
-        # decode: outputs of the fused Q|K|V and gate|up matvecs
+        # prefill: gate and up (interleaved with a fused gate|up buffer), then
+        # SiLU(gate) * up in self.up
+        self.gate, self.up = buf(P * 2 * c.ffn * 4), buf(P * c.ffn * 4)
+        # decode: outputs of the fused Q|K|V and gate|up (SiLU-pairs) matvecs
         self.qkv = buf((qd + 2 * c.kv_dim) * 4)
-        self.gu = buf(2 * c.ffn * 4)
+        self.gu = buf(c.ffn * 4)
         self.logits = buf(c.vocab * 4)
         self.kc = [buf(self.max_len * c.kv_dim * 4) for _ in range(c.n_layers)]
         self.vc = [buf(self.max_len * c.kv_dim * 4) for _ in range(c.n_layers)]
@@ -223,6 +241,13 @@ class LlamaDecoder:
         nat.check(self.L.aih_rope_table(self.h, self.table, self.max_len, c.head_dim, c.theta), "aih_rope_table")
         self.n_prompt = 0
         self.graph = None
+        # The SiLU-pairs epilogue pairs the row teams of a workgroup: 8 teams
+        # for widths up to 4096, 4 up to 8192, 2 up to 16384; the fused gate|up
+        # height 2*ffn must be a multiple of the team count.
+        teams = 8 if c.dim <= 4096 else 4 if c.dim <= 8192 else 2 if c.dim <= 16384 else 0
+        self.pairs_epilogue = teams > 0 and (2 * c.ffn) % teams == 0
+        # the fused decode attention serves query groups of 1, 2, 4 or 8 heads
+        self.fused_attention = c.n_heads // c.n_kv_heads in (1, 2, 4, 8)
 
     # -- operators (thin checked wrappers)
     def _mm(self, name, X, M, Y):
@@ -233,26 +258,27 @@ class LlamaDecoder:
         nat.check(self.L.aih_rmsnorm(self.h, X, self.w.ptr(name), Y, rows, self.cfg.dim, self.cfg.eps),
                   "rmsnorm %s" % name)
 
-    def _mmf(self, name, X, X2, pre, acc, Y):
-        """Decode matvec with a fused prologue (RMSNorm or SiLU*up) and/or the
-        residual add (aih_qmatvec_fused)."""
+    def _mmf(self, name, X, X2, pre, post, Y):
+        """Decode matvec with a fused prologue (RMSNorm or SiLU*up) and
+        epilogue (residual add or SiLU of gate/up pairs), aih_qmatvec_fused."""
         qt, ptr, n, k = self.w[name]
-        nat.check(self.L.aih_qmatvec_fused(self.h, qt, ptr, n, k, X, X2, self.cfg.eps, pre, acc, Y),
+        nat.check(self.L.aih_qmatvec_fused(self.h, qt, ptr, n, k, X, X2, self.cfg.eps, pre, post, Y),
                   "fused matvec %s" % name)
 
     def layer(self, l, rows, start, pos):
         """One decoder layer over `rows` activation rows at positions start..
         (+*pos when pos is a device pointer).  A single row (decode) runs as
-        seven kernels: Q|K|V matvec with the attention RMSNorm fused in,
-        RoPE + KV cache, attention (two), W_o matvec adding into x, gate|up
-        matvec with the FFN RMSNorm fused in, down matvec with SiLU*up fused
-        in and adding into x.  Several rows (prefill) use the GEMM and the
-        separate operators."""
+        six kernels: Q|K|V matvec with the attention RMSNorm fused in,
+        attention with RoPE and the KV cache store fused in (two kernels),
+        W_o matvec adding into x, gate|up matvec with the FFN RMSNorm fused in
+        and SiLU(gate)*up as its epilogue, down matvec adding into x.
+        Several rows (prefill) use the GEMM and the separate operators."""
         c, L, h, p = self.cfg, self.L, self.h, "blk.%d." % l
         qd = c.n_heads * c.head_dim
-        decode = rows == 1 and p + "attn_qkv" in self.w and p + "ffn_gate_up" in self.w
+        decode = rows == 1 and p + "attn_qkv" in self.w
         if decode:
-            self._mmf(p + "attn_qkv", self.x, self.w.ptr(p + "attn_norm"), nat.PRE_RMSNORM, 0, self.qkv)
+            self._mmf(p + "attn_qkv", self.x, self.w.ptr(p + "attn_norm"), nat.PRE_RMSNORM, nat.POST_STORE,
+                      self.qkv)
             q, k, v = self.qkv, self.qkv + qd * 4, self.qkv + (qd + c.kv_dim) * 4
         else:
             self._norm(p + "attn_norm", self.x, self.xn, rows)
@@ -260,31 +286,44 @@ class LlamaDecoder:
             self._mm(p + "attn_k", self.xn, rows, self.k)
             self._mm(p + "attn_v", self.xn, rows, self.v)
             q, k, v = self.q, self.k, self.v
-        nat.check(L.aih_rope_qkv(h, q, qd, k, c.kv_dim, v, c.kv_dim, self.kc[l], self.vc[l], rows, c.n_heads,
-                                 c.n_kv_heads, c.head_dim, start, pos, self.table, self.max_len, self.max_len),
-                  "rope q, k -> cache, v -> cache")
-        nat.check(L.aih_attention(h, q, self.kc[l], self.vc[l], self.att, rows, c.n_heads, c.n_kv_heads,
-                                  c.head_dim, start, pos, self.max_len, self.scale, self.scratch,
-                                  self.scratch_floats), "attention")
+        if decode and self.fused_attention:
+            nat.check(L.aih_attention_decode_qkv(h, self.qkv, self.kc[l], self.vc[l], self.att, c.n_heads,
+                                                 c.n_kv_heads, c.head_dim, start, pos, self.table, self.max_len,
+                                                 self.max_len, self.scale, self.scratch, self.scratch_floats),
+                      "rope + cache store + attention")
+        else:
+            nat.check(L.aih_rope_qkv(h, q, qd, k, c.kv_dim, v, c.kv_dim, self.kc[l], self.vc[l], rows, c.n_heads,
+                                     c.n_kv_heads, c.head_dim, start, pos, self.table, self.max_len, self.max_len),
+                      "rope q, k -> cache, v -> cache")
+            nat.check(L.aih_attention(h, q, self.kc[l], self.vc[l], self.att, rows, c.n_heads, c.n_kv_heads,
+                                      c.head_dim, start, pos, self.max_len, self.scale, self.scratch,
+                                      self.scratch_floats), "attention")
         if decode:
-            self._mmf(p + "attn_output", self.att, None, nat.PRE_NONE, 1, self.x)
-            self._mmf(p + "ffn_gate_up", self.x, self.w.ptr(p + "ffn_norm"), nat.PRE_RMSNORM, 0, self.gu)
-            self._mmf(p + "ffn_down", self.gu, self.gu + c.ffn * 4, nat.PRE_SILU_MUL, 1, self.x)
+            self._mmf(p + "attn_output", self.att, None, nat.PRE_NONE, nat.POST_ACCUMULATE, self.x)
+        else:
+            self._mm(p + "attn_output", self.att, rows, self.tmp)
+            nat.check(L.aih_add(h, self.x, self.tmp, self.x, rows * c.dim), "residual")
+        if decode and self.pairs_epilogue and p + "ffn_gate_up" in self.w:
+            self._mmf(p + "ffn_gate_up", self.x, self.w.ptr(p + "ffn_norm"), nat.PRE_RMSNORM,
+                      nat.POST_SILU_PAIRS, self.gu)
+            self._mmf(p + "ffn_down", self.gu, None, nat.PRE_NONE, nat.POST_ACCUMULATE, self.x)
             return
-        self._mm(p + "attn_output", self.att, rows, self.tmp)
-        nat.check(L.aih_add(h, self.x, self.tmp, self.x, rows * c.dim), "residual")
         self._norm(p + "ffn_norm", self.x, self.xn, rows)
-        self._mm(p + "ffn_gate", self.xn, rows, self.gate)
-        self._mm(p + "ffn_up", self.xn, rows, self.up)
-        nat.check(L.aih_silu_mul(h, self.gate, self.up, self.gate, rows * c.ffn), "silu*up")
-        self._mm(p + "ffn_down", self.gate, rows, self.tmp)
+        if p + "ffn_gate_up" in self.w:
+            self._mm(p + "ffn_gate_up", self.xn, rows, self.gate)
+            nat.check(L.aih_silu_mul_pairs(h, self.gate, self.up, rows, c.ffn), "silu*up (pairs)")
+        else:
+            self._mm(p + "ffn_gate", self.xn, rows, self.gate)
+            self._mm(p + "ffn_up", self.xn, rows, self.up)
+            nat.check(L.aih_silu_mul(h, self.gate, self.up, self.up, rows * c.ffn), "silu*up")
+        self._mm(p + "ffn_down", self.up, rows, self.tmp)
         nat.check(L.aih_add(h, self.x, self.tmp, self.x, rows * c.dim), "residual")
 
     def head(self, row_ptr, pos, hist_offset):
         """Output norm + vocabulary projection of one row, then the greedy
         token (and history / position update when pos is given)."""
         c = self.cfg
-        self._mmf("output", row_ptr, self.w.ptr("output_norm"), nat.PRE_RMSNORM, 0, self.logits)
+        self._mmf("output", row_ptr, self.w.ptr("output_norm"), nat.PRE_RMSNORM, nat.POST_STORE, self.logits)
         nat.check(self.L.aih_argmax(self.h, self.logits, c.vocab, self.token, pos, self.history, self.history_len,
                                     hist_offset), "argmax")
 

@@ -153,21 +153,28 @@ int aih_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
 
 /* Decode matvec (one column) with the neighbouring element-wise steps of a
  * Llama layer fused in, so that a decode step needs no separate kernels for
- * them:
+ * them.  y[n] = sum_k x[k] W[n, k] with
  *   pre = AIH_PRE_NONE       x = X
  *   pre = AIH_PRE_RMSNORM    x = (X / sqrt(mean(X^2) + eps)) * X2   (X2: norm weights)
  *   pre = AIH_PRE_SILU_MUL   x = SiLU(X) * X2                        (X2: the up projection)
- *   accumulate != 0          Y[n] += sum_k x[k] W[n, k]  (the residual add), else Y[n] = ...
+ * and
+ *   post = AIH_POST_STORE       Y[n] = y[n]
+ *   post = AIH_POST_ACCUMULATE  Y[n] += y[n]                 (the residual add)
+ *   post = AIH_POST_SILU_PAIRS  Y[i] = SiLU(y[2i]) * y[2i+1], i < N/2 (W holds
+ *                               gate and up rows interleaved; K <= 16384)
  * with the formulas of aih_rmsnorm, aih_silu_mul and aih_add.  X, X2 16-byte
  * aligned; Y must not alias X or X2.  Replaces, for a decode step, the
  * LayerNorm / SiLU+Multiply / Add around MatMulWeights in
  * ComputeOps.TransformerLayer (ComputeOps.cs:1250-1356) and FeedForward
  * (ComputeOps.cs:1218-1241). */
-#define AIH_PRE_NONE     0
-#define AIH_PRE_RMSNORM  1
-#define AIH_PRE_SILU_MUL 2
+#define AIH_PRE_NONE        0
+#define AIH_PRE_RMSNORM     1
+#define AIH_PRE_SILU_MUL    2
+#define AIH_POST_STORE      0
+#define AIH_POST_ACCUMULATE 1
+#define AIH_POST_SILU_PAIRS 2
 int aih_qmatvec_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *X,
-                      const float *X2, float eps, int pre, int accumulate, float *Y);
+                      const float *X2, float eps, int pre, int post, float *Y);
 
 /* Prefill GEMM, dequantization fused:  Y[m*N + n] = sum_k X[m*K + k] * W[n, k].
  * X is converted once to fp16 in a context workspace (M*K*2 bytes, grown on
@@ -234,6 +241,11 @@ int aih_store_rows(aih_ctx *ctx, const float *X, int64_t rows, int64_t cols, flo
  * (ComputeOps.cs:1218-1241). */
 int aih_silu_mul(aih_ctx *ctx, const float *G, const float *U, float *Y, int64_t n);
 
+/* Y[r, i] = SiLU(X[r, 2i]) * X[r, 2i+1] for i < n, r < rows: the SiLU * up
+ * step over the output of a GEMM with gate/up rows interleaved (row stride 2n
+ * in X, n in Y). */
+int aih_silu_mul_pairs(aih_ctx *ctx, const float *X, float *Y, int64_t rows, int64_t n);
+
 /* Y = A + B, element-wise (Y may alias A or B).  Replaces ComputeOps.Add
  * (ComputeOps.cs:389). */
 int aih_add(aih_ctx *ctx, const float *A, const float *B, float *Y, int64_t n);
@@ -255,6 +267,23 @@ int64_t aih_attention_scratch_floats(int32_t n_heads, int32_t max_len);
 int aih_attention(aih_ctx *ctx, const float *Q, const float *Kc, const float *Vc, float *O, int64_t n_q,
                   int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t start, const int32_t *pos,
                   int32_t max_len, float scale, float *scratch, int64_t scratch_floats);
+
+/* One decode step's attention with the position steps before it fused in:
+ * for the projection output QKV of one row at position p = start + *pos
+ * (q | k | v: n_heads*head_dim, then n_kv_heads*head_dim twice, as one fused
+ * Q|K|V matvec writes it), RoPE of q and k from `table`, the k and v rows
+ * stored into the caches at row p (when p < max_len), and attention of each
+ * query head over cache rows 0..min(p, max_len - 1).  QKV is not modified.
+ * Same results, bit for bit, as aih_rope_qkv (one row) followed by
+ * aih_attention (one row).  n_heads / n_kv_heads must be 1, 2, 4 or 8
+ * (AIH_E_UNSUPPORTED otherwise), table_rows >= max_len; scratch as for
+ * aih_attention.  Replaces, for a decode step, ApplyRoPEFull, the KV cache
+ * append and FusedMHAGenerate (ComputeOps.cs:959-979, 1015-1043,
+ * InferenceEngine.cs:598-622, shader ComputeShaders.cs:656-733). */
+int aih_attention_decode_qkv(aih_ctx *ctx, const float *QKV, float *Kc, float *Vc, float *O, int32_t n_heads,
+                             int32_t n_kv_heads, int32_t head_dim, int32_t start, const int32_t *pos,
+                             const float *table, int32_t table_rows, int32_t max_len, float scale, float *scratch,
+                             int64_t scratch_floats);
 
 /* Quantized embedding gather: Y[i,:] = dequantized row ids[i] of a [vocab,
  * dim] table of `type` blocks (ids from device memory; an id outside

@@ -1,5 +1,6 @@
 """Decoder operators (aih_rmsnorm, aih_rope_table, aih_rope, aih_store_rows,
-aih_silu_mul, aih_add, aih_attention, aih_embed_q, aih_argmax) vs the oracle
+aih_silu_mul, aih_silu_mul_pairs, aih_add, aih_attention,
+aih_attention_decode_qkv, aih_embed_q, aih_argmax) vs the oracle
 (oracle/llama.py) through the C ABI.
 
 Bars: bit-exact for the row store, add, embedding gather and RoPE applied
@@ -10,7 +11,9 @@ exact sums and numpy's exp); attention within 1e-5 normwise against a
 float64 evaluation.  Shapes are the decoder's (32 query / 8 KV heads of
 128, hidden 4096, FFN 14336) plus edge cases: one key, split boundaries of
 the decode kernel (63/64/65/640 keys), positions from device memory, rows
-past the cache, ids out of range, argmax ties and NaN.
+past the cache, ids out of range, argmax ties and NaN.  The fused decode
+attention (RoPE, cache store and attention in one operator) is bit-exact to
+aih_rope_qkv + aih_attention for query groups of 1, 2, 4 and 8 heads.
 """
 import ctypes
 
@@ -145,6 +148,24 @@ def test_silu_mul(device, bufs):
     assert np.max(np.abs(y - ref) / (np.abs(ref) + 1e-30)) < 2e-6
 
 
+def test_silu_mul_pairs(device, bufs):
+    # rows of interleaved (gate, up) columns, as a GEMM over gate/up rows
+    # interleaved writes them; bit-exact to aih_silu_mul on the split halves
+    rows, n = 3, 14336
+    x = rnd(12, rows, 2 * n, scale=3.0)
+    x[0, :10:2] = [0.0, 88.0, -88.0, -200.0, 20.0]
+    X, Y = bufs.up(x), bufs.empty(rows * n * 4)
+    nat.check(L.aih_silu_mul_pairs(device.handle, X, Y, rows, n), "silu_mul_pairs")
+    y = bufs.read(Y, rows * n).reshape(rows, n)
+    ref = ol.silu_mul(x[:, 0::2], x[:, 1::2])
+    assert np.max(np.abs(y - ref) / (np.abs(ref) + 1e-30)) < 2e-6
+    G, U = bufs.up(np.ascontiguousarray(x[:, 0::2])), bufs.up(np.ascontiguousarray(x[:, 1::2]))
+    nat.check(L.aih_silu_mul(device.handle, G, U, G, rows * n), "silu_mul")
+    assert np.array_equal(bufs.read(G, rows * n).reshape(rows, n), y)
+    assert L.aih_silu_mul_pairs(device.handle, X, Y, -1, n) == nat.AIH_E_INVALID
+    assert L.aih_silu_mul_pairs(device.handle, X, Y, 0, n) == nat.AIH_OK
+
+
 def _attn(device, bufs, n_q, start, L_cache, nh=32, nkv=8, pos_dev=None, seed=11):
     kvd = nkv * 128
     q = rnd(seed, n_q, nh * 128)
@@ -267,3 +288,79 @@ def test_rope_qkv_equals_separate_ops(device, bufs, rows, start, pos_dev):
     assert np.array_equal(kc[p0:p0 + rows], ol.rope(k, pos, nkv, hd, t))
     assert np.array_equal(vc[p0:p0 + rows], v)
     assert not kc[:p0].any() and not vc[p0 + rows:].any()
+
+
+def _decode_qkv_pair(device, bufs, nh, nkv, max_len, p, pos_dev=False, seed=50, table_rows=None):
+    """Run aih_attention_decode_qkv and, on a copy of the same caches,
+    aih_rope_qkv + aih_attention (one row); return both outputs and caches."""
+    hd = 128
+    qd, kvd = nh * hd, nkv * hd
+    table_rows = table_rows or max_len
+    T, t = _table(device, bufs, table_rows)
+    fused = rnd(seed, 1, qd + 2 * kvd)
+    K, V = rnd(seed + 1, max_len, kvd), rnd(seed + 2, max_len, kvd)
+    scale = float(np.float32(1) / np.sqrt(np.float32(hd)))
+    nsc = int(L.aih_attention_scratch_floats(nh, max_len))
+    start, P = (0, bufs.up(np.array([p], np.int32))) if pos_dev else (p, None)
+    res = []
+    for fused_path in (True, False):
+        F, KC, VC = bufs.up(fused), bufs.up(K), bufs.up(V)
+        O, S = bufs.empty(qd * 4), bufs.empty(nsc * 4)
+        if fused_path:
+            nat.check(L.aih_attention_decode_qkv(device.handle, F, KC, VC, O, nh, nkv, hd, start, P, T, table_rows,
+                                                 max_len, scale, S, nsc), "attention_decode_qkv")
+            assert np.array_equal(bufs.read(F, fused.size), fused.reshape(-1))   # QKV not modified
+        else:
+            ld = qd + 2 * kvd
+            nat.check(L.aih_rope_qkv(device.handle, F, ld, F + qd * 4, ld, F + (qd + kvd) * 4, ld, KC, VC, 1, nh, nkv,
+                                     hd, start, P, T, table_rows, max_len), "rope_qkv")
+            nat.check(L.aih_attention(device.handle, F, KC, VC, O, 1, nh, nkv, hd, start, P, max_len, scale, S, nsc),
+                      "attention")
+        res.append((bufs.read(O, qd), bufs.read(KC, max_len * kvd).reshape(max_len, kvd),
+                    bufs.read(VC, max_len * kvd).reshape(max_len, kvd)))
+    return res, fused, K, V, t
+
+
+@pytest.mark.parametrize("nh,nkv", [(32, 8), (8, 4), (4, 4), (32, 4)])
+@pytest.mark.parametrize("p", [0, 63, 64, 65, 517, 639])
+def test_attention_decode_qkv_equals_separate_ops(device, bufs, nh, nkv, p):
+    (o, kc, vc), (o2, kc2, vc2) = _decode_qkv_pair(device, bufs, nh, nkv, 640, p, pos_dev=p % 2 == 1)[0]
+    assert np.array_equal(o, o2)
+    assert np.array_equal(kc, kc2) and np.array_equal(vc, vc2)
+
+
+def test_attention_decode_qkv_vs_oracle(device, bufs):
+    nh, nkv, p, max_len = 32, 8, 300, 640
+    res, fused, K, V, t = _decode_qkv_pair(device, bufs, nh, nkv, max_len, p, pos_dev=True, seed=60)
+    o, kc, vc = res[0]
+    qd, kvd = nh * 128, nkv * 128
+    q = ol.rope(fused[:, :qd], [p], nh, 128, t)
+    K, V = K.copy(), V.copy()
+    K[p] = ol.rope(fused[:, qd:qd + kvd], [p], nkv, 128, t)[0]
+    V[p] = fused[0, qd + kvd:]
+    assert np.array_equal(kc, K) and np.array_equal(vc, V)      # only row p written
+    ref = ol.attention(q, K, V, [p], nh, nkv, 128)[0]
+    assert np.linalg.norm(o - ref) / np.linalg.norm(ref) < 1e-5
+
+
+def test_attention_decode_qkv_long_context_and_past_the_cache(device, bufs):
+    # several sub-chunks per split; a position past the cache attends to the
+    # whole cache and stores nothing, like the separate operators
+    for p in (8999, 5000, 9000, 9100):
+        (o, kc, vc), (o2, kc2, vc2) = _decode_qkv_pair(device, bufs, 8, 2, 9000, p, pos_dev=True, seed=p,
+                                                       table_rows=9200)[0]
+        assert np.array_equal(o, o2), p
+        assert np.array_equal(kc, kc2) and np.array_equal(vc, vc2), p
+
+
+def test_attention_decode_qkv_argument_errors(device, bufs):
+    X = bufs.empty(8192 * 4)
+    h = device.handle
+    f = L.aih_attention_decode_qkv
+    assert f(h, X, X, X, X, 12, 4, 128, 0, None, X, 8, 8, 1.0, X, 8192) == nat.AIH_E_UNSUPPORTED    # group of 3
+    assert f(h, X, X, X, X, 32, 8, 64, 0, None, X, 8, 8, 1.0, X, 8192) == nat.AIH_E_UNSUPPORTED
+    assert f(h, X, X, X, X, 32, 5, 128, 0, None, X, 8, 8, 1.0, X, 8192) == nat.AIH_E_INVALID
+    assert f(h, X, X, X, X, 32, 8, 128, 0, None, X, 4, 8, 1.0, X, 8192) == nat.AIH_E_LIMIT       # table too short
+    assert f(h, X, X, X, X, 32, 8, 128, 8, None, X, 8, 8, 1.0, X, 8192) == nat.AIH_E_LIMIT       # start past the cache
+    assert f(h, X, X, X, X, 32, 8, 128, 0, None, X, 8, 8, 1.0, X, 100) == nat.AIH_E_INVALID      # scratch too small
+    device.synchronize()

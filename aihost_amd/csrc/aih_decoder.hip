@@ -37,11 +37,41 @@ __device__ __forceinline__ int32_t dev_pos(int32_t start, const int32_t *pos)
     return pos ? start + *pos : start;
 }
 
+// Cross-lane steps on the DPP path: a few cycles each, where __shfl_xor goes
+// through an LDS permute of about a hundred cycles of latency.
+__device__ __forceinline__ float xor1(float v)   // lane ^ 1 (quad_perm [1,0,3,2])
+{
+    return __builtin_amdgcn_update_dpp(0.0f, v, 0xB1, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float xor2(float v)   // lane ^ 2 (quad_perm [2,3,0,1])
+{
+    return __builtin_amdgcn_update_dpp(0.0f, v, 0x4E, 0xF, 0xF, false);
+}
+
+// Sum over the 64 lanes of a wave, returned to every lane: pairs, quads,
+// half rows and rows of 16 by DPP, then rows 0+1, 2+3 and 0..3 into lane 63
+// (row_bcast), read back with readlane.
 __device__ __forceinline__ float wave_sum(float v)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    v += xor1(v);
+    v += xor2(v);
+    v += __builtin_amdgcn_update_dpp(0.0f, v, 0x141, 0xF, 0xF, false);   // row_half_mirror
+    v += __builtin_amdgcn_update_dpp(0.0f, v, 0x140, 0xF, 0xF, false);   // row_mirror
+    v += __builtin_amdgcn_update_dpp(0.0f, v, 0x142, 0xA, 0xF, false);   // row_bcast:15 -> rows 1, 3
+    v += __builtin_amdgcn_update_dpp(0.0f, v, 0x143, 0xC, 0xF, false);   // row_bcast:31 -> rows 2, 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Maximum over the 64 lanes of a wave (same steps), returned to every lane.
+__device__ __forceinline__ float wave_max(float v)
+{
+    v = fmaxf(v, __builtin_amdgcn_update_dpp(-INFINITY, v, 0xB1, 0xF, 0xF, false));
+    v = fmaxf(v, __builtin_amdgcn_update_dpp(-INFINITY, v, 0x4E, 0xF, 0xF, false));
+    v = fmaxf(v, __builtin_amdgcn_update_dpp(-INFINITY, v, 0x141, 0xF, 0xF, false));
+    v = fmaxf(v, __builtin_amdgcn_update_dpp(-INFINITY, v, 0x140, 0xF, 0xF, false));
+    v = fmaxf(v, __builtin_amdgcn_update_dpp(-INFINITY, v, 0x142, 0xA, 0xF, false));
+    v = fmaxf(v, __builtin_amdgcn_update_dpp(-INFINITY, v, 0x143, 0xC, 0xF, false));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 // Sum over a workgroup of `NT` threads (multiple of 64); every thread gets it.
@@ -306,13 +336,11 @@ attn_decode_partial(const float *__restrict__ Q, const float *__restrict__ Kc, c
                 a = fmaf(qs[part4 * 32 + 4 * d + 2], k.z, a);
                 a = fmaf(qs[part4 * 32 + 4 * d + 3], k.w, a);
             }
-            a += __shfl_xor(a, 1);
-            a += __shfl_xor(a, 2);
+            a += xor1(a);
+            a += xor2(a);
             sc = a * scale;
         }
-        float mc = sc;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) mc = fmaxf(mc, __shfl_xor(mc, o));
+        const float mc = wave_max(sc);
         if ((t & 63) == 0) red[t >> 6] = mc;
         __syncthreads();
         const float mn = fmaxf(m, fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
@@ -370,13 +398,14 @@ attn_decode_qkv_partial(const float *__restrict__ QKV, float *Kc, float *Vc, flo
                         const float *__restrict__ table, int32_t table_rows, int32_t cache_rows, float scale,
                         int32_t n_split)
 {
+    constexpr int half = kHD / 2;
+    constexpr int QP = (G * half + 255) / 256;   // query pairs per thread
     __shared__ f4 qs[G][kHD / 4];
     __shared__ f4 kn[kHD / 4], vn[kHD / 4];
     __shared__ float ps[G][kSub];
-    __shared__ float red[4][G];
+    __shared__ float red_m[4][G], red_s[4][G];
     __shared__ f4 accs[8][G][kHD / 4];
     const int kvh = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
-    constexpr int half = kHD / 2;
     const int64_t kv_stride = (int64_t)n_kv_heads * kHD;
     const int32_t p = dev_pos(start, pos);
     const int32_t L = max(0, min(p + 1, cache_rows));
@@ -385,11 +414,39 @@ attn_decode_qkv_partial(const float *__restrict__ QKV, float *Kc, float *Vc, flo
     const bool own = j0 <= p && p < j1;   // this split holds the new key
     const bool rot = p >= 0 && p < table_rows;
     const float *tp = table + 2 * (int64_t)(rot ? p : 0) * half;
+    const float *kx = QKV + (int64_t)n_heads * kHD + (int64_t)kvh * kHD;   // the new key row
+    const float *vx = kx + kv_stride;                                       // the new value row
+
+    // Loads in the order they are waited for: the query pairs, their (cos,
+    // sin) and the new K/V rows first, then the K and V rows of the first
+    // sub-chunk (the memory counter drains in order, so the RoPE below does
+    // not wait for the 64 KB of cached rows).  Row p itself, when this split
+    // holds it, is taken from LDS after the barrier.
+    float qx0[QP], qx1[QP], qc[QP], qsn[QP];
+#pragma unroll
+    for (int i = 0; i < QP; ++i) {
+        const int e = t + 256 * i;
+        const int g = min(e / half, G - 1), pi = e % half;
+        const float *x = QKV + (int64_t)(kvh * G + g) * kHD + 2 * pi;
+        qx0[i] = x[0];
+        qx1[i] = x[1];
+        qc[i] = tp[2 * pi];
+        qsn[i] = tp[2 * pi + 1];
+    }
+    float k0 = 0.f, k1 = 0.f, kcs = 0.f, ksn = 0.f;
+    f4 vnew = {0.f, 0.f, 0.f, 0.f};
+    if (own) {
+        if (t < half) {
+            k0 = kx[2 * t];
+            k1 = kx[2 * t + 1];
+            kcs = tp[2 * t];
+            ksn = tp[2 * t + 1];
+        } else if (t < half + kHD / 4) {
+            vnew = reinterpret_cast<const f4 *>(vx)[t - half];
+        }
+    }
     // Thread t scores key t/4 of a sub-chunk over dims 32*(t%4).. and
-    // accumulates V dims 4*(t%32).. for keys t/32 + 8u.  The K and V rows of
-    // the first sub-chunk are loaded before the query phase (their addresses
-    // depend on p only); row p itself, when this split holds it, is taken
-    // from LDS after the barrier instead.
+    // accumulates V dims 4*(t%32).. for keys t/32 + 8u.
     const int kk = t >> 2, part4 = t & 3;
     const int vc = t & 31, vr = t >> 5;
     f4 k[8], vv[kSub / 8];
@@ -409,32 +466,30 @@ attn_decode_qkv_partial(const float *__restrict__ QKV, float *Kc, float *Vc, flo
                           : f4{0.f, 0.f, 0.f, 0.f};
         }
     };
+    __builtin_amdgcn_sched_barrier(0);
     if (j0 < j1) {
-        load_v(j0);
         load_k(j0);
+        load_v(j0);
     }
-    // RoPE of the G query heads into LDS: pair i of head g
-    for (int e = t; e < G * half; e += 256) {
-        const int g = e / half, i = e % half;
-        const float *x = QKV + (int64_t)(kvh * G + g) * kHD + 2 * i;
-        const float x0 = x[0], x1 = x[1];
-        float *y = reinterpret_cast<float *>(&qs[g][0]) + 2 * i;
-        if (rot) {
-            const float c = tp[2 * i], sn = tp[2 * i + 1];
-            y[0] = x0 * c - x1 * sn;
-            y[1] = x0 * sn + x1 * c;
-        } else {
-            y[0] = x0;
-            y[1] = x1;
+    __builtin_amdgcn_sched_barrier(0);
+    // RoPE of the G query heads into LDS: pair pi of head g
+#pragma unroll
+    for (int i = 0; i < QP; ++i) {
+        const int e = t + 256 * i;
+        if (e < G * half) {
+            float *y = reinterpret_cast<float *>(&qs[e / half][0]) + 2 * (e % half);
+            if (rot) {
+                y[0] = qx0[i] * qc[i] - qx1[i] * qsn[i];
+                y[1] = qx0[i] * qsn[i] + qx1[i] * qc[i];
+            } else {
+                y[0] = qx0[i];
+                y[1] = qx1[i];
+            }
         }
     }
     if (own) {
-        const float *kx = QKV + (int64_t)n_heads * kHD + (int64_t)kvh * kHD;
-        const float *vx = kx + kv_stride;
         if (t < half) {
-            const float c = tp[2 * t], sn = tp[2 * t + 1];
-            const float x0 = kx[2 * t], x1 = kx[2 * t + 1];
-            const float y0 = x0 * c - x1 * sn, y1 = x0 * sn + x1 * c;
+            const float y0 = k0 * kcs - k1 * ksn, y1 = k0 * ksn + k1 * kcs;
             float *kq = reinterpret_cast<float *>(kn) + 2 * t;
             kq[0] = y0;
             kq[1] = y1;
@@ -442,10 +497,8 @@ attn_decode_qkv_partial(const float *__restrict__ QKV, float *Kc, float *Vc, flo
             kc[0] = y0;
             kc[1] = y1;
         } else if (t < half + kHD / 4) {
-            const int i = t - half;
-            const f4 v = reinterpret_cast<const f4 *>(vx)[i];
-            vn[i] = v;
-            reinterpret_cast<f4 *>(Vc + (int64_t)p * kv_stride + (int64_t)kvh * kHD)[i] = v;
+            vn[t - half] = vnew;
+            reinterpret_cast<f4 *>(Vc + (int64_t)p * kv_stride + (int64_t)kvh * kHD)[t - half] = vnew;
         }
     }
     __syncthreads();
@@ -457,6 +510,8 @@ attn_decode_qkv_partial(const float *__restrict__ QKV, float *Kc, float *Vc, flo
         l[g] = 0.f;
         acc[g] = f4{0.f, 0.f, 0.f, 0.f};
     }
+    // Two barriers per sub-chunk: red_m, ps and red_s are each written after
+    // the barrier that follows their last reads in the previous sub-chunk.
     for (int32_t c0 = j0; c0 < j1; c0 += kSub) {
         const int n = min(kSub, j1 - c0);
         if (c0 + kk == p) {
@@ -481,39 +536,33 @@ attn_decode_qkv_partial(const float *__restrict__ QKV, float *Kc, float *Vc, flo
                     a = fmaf(q.z, k[d].z, a);
                     a = fmaf(q.w, k[d].w, a);
                 }
-                a += __shfl_xor(a, 1);
-                a += __shfl_xor(a, 2);
+                a += xor1(a);
+                a += xor2(a);
                 sc[g] = a * scale;
             }
         }
         if (c0 + kSub < j1) load_k(c0 + kSub);   // the next sub-chunk's keys, while this one finishes
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float mc = wave_max(sc[g]);
+            if ((t & 63) == 0) red_m[t >> 6][g] = mc;
+        }
+        __syncthreads();
         float mn[G];
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            float mc = sc[g];
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) mc = fmaxf(mc, __shfl_xor(mc, o));
-            if ((t & 63) == 0) red[t >> 6][g] = mc;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-            mn[g] = fmaxf(m[g], fmaxf(fmaxf(red[0][g], red[1][g]), fmaxf(red[2][g], red[3][g])));
-        __syncthreads();
-        float e[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            e[g] = kk < n ? expf(sc[g] - mn[g]) : 0.f;
-            if (part4 == 0) ps[g][kk] = e[g];
-            const float w = wave_sum(part4 == 0 ? e[g] : 0.f);
-            if ((t & 63) == 0) red[t >> 6][g] = w;
+            mn[g] = fmaxf(m[g], fmaxf(fmaxf(red_m[0][g], red_m[1][g]), fmaxf(red_m[2][g], red_m[3][g])));
+            const float e = kk < n ? expf(sc[g] - mn[g]) : 0.f;
+            if (part4 == 0) ps[g][kk] = e;
+            const float w = wave_sum(part4 == 0 ? e : 0.f);
+            if ((t & 63) == 0) red_s[t >> 6][g] = w;
         }
         __syncthreads();   // publishes ps and the partial sums
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             float lc = 0.f;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) lc += red[i][g];
+            for (int i = 0; i < 4; ++i) lc += red_s[i][g];
             const float corr = expf(m[g] - mn[g]);   // 0 on the first sub-chunk
             l[g] = l[g] * corr + lc;
             f4 a = {0.f, 0.f, 0.f, 0.f};
@@ -530,7 +579,6 @@ attn_decode_qkv_partial(const float *__restrict__ QKV, float *Kc, float *Vc, flo
             m[g] = mn[g];
         }
         if (c0 + kSub < j1) load_v(c0 + kSub);
-        __syncthreads();   // ps and red reused by the next sub-chunk
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) accs[vr][g][vc] = acc[g];
@@ -573,9 +621,7 @@ attn_decode_combine(const float *__restrict__ part, float *__restrict__ O, int32
     for (int u = 0; u < kPre; ++u) vp[u] = u < n_split ? ph[u * (kHD + 2) + 2 + t] : 0.f;
     const float mt = t < n_split ? ph[t * (kHD + 2)] : -INFINITY;
     const float lt = t < n_split ? ph[t * (kHD + 2) + 1] : 0.f;
-    float M = mt;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+    float M = wave_max(mt);
     if ((t & 63) == 0) red[t >> 6] = M;
     __syncthreads();
     M = fmaxf(red[0], red[1]);
@@ -650,8 +696,8 @@ attn_prefill_kernel(const float *__restrict__ Q, const float *__restrict__ Kc, c
                 a = fmaf(q[d].z, k.z, a);
                 a = fmaf(q[d].w, k.w, a);
             }
-            a += __shfl_xor(a, 1);
-            a += __shfl_xor(a, 2);
+            a += xor1(a);
+            a += xor2(a);
             if (j0 + jj > p_i) continue;            // causal: key after the query
             const float s = a * scale;
             const float mn = fmaxf(m, s);

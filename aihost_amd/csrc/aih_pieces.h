@@ -143,6 +143,38 @@ struct G6K {
             y[j] = ds * (float)((int)(lo | (hi << 4)) - 32);
         }
     }
+    // fp16 path: the 6-bit code (nibble | 2 high bits << 4) OR-ed into the
+    // mantissa of 0x6400 is the fp16 value 1024 + q, and one fused fp32
+    // multiply-add with fp16 output gives code * ds - 1056 * ds = ds * (q - 32)
+    // (the constant's fp32 rounding moves a weight by at most 2^-24 * 1056 * ds).
+    __device__ static void piece_h(const Raw &r, int c, int s, h8 &lo, h8 &hi8)
+    {
+        const int Q = 2 * (c & 1) + (s >> 1);
+        const float ds = f16_bits(r.d) * (float)(int)(int8_t)(uint8_t)r.sc;
+        const float C = 1056.f * ds;
+        const int ls = 4 * (Q >> 1), hs = 2 * Q;
+        const uint32_t l[4] = {r.ql.x, r.ql.y, r.ql.z, r.ql.w};
+        const uint32_t hb[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+        _Float16 y[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // the four 6-bit codes of bytes 0..3, one per byte, then split
+            // into the pairs (0, 2) and (1, 3)
+            const uint32_t q4 = ((l[i] >> ls) & 0x0F0F0F0Fu) | (((hb[i] >> hs) & 0x03030303u) << 4);
+            const uint32_t ca = (q4 & 0x00FF00FFu) | 0x64006400u;
+            const uint32_t cb = ((q4 >> 8) & 0x00FF00FFu) | 0x64006400u;
+            const h2 a = __builtin_bit_cast(h2, ca), b = __builtin_bit_cast(h2, cb);
+            y[4 * i + 0] = (_Float16)__builtin_fmaf((float)a.x, ds, -C);
+            y[4 * i + 2] = (_Float16)__builtin_fmaf((float)a.y, ds, -C);
+            y[4 * i + 1] = (_Float16)__builtin_fmaf((float)b.x, ds, -C);
+            y[4 * i + 3] = (_Float16)__builtin_fmaf((float)b.y, ds, -C);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            lo[j] = y[j];
+            hi8[j] = y[8 + j];
+        }
+    }
 };
 
 // Q8_0: chunk c is blocks 2c and 2c+1; piece s is elements 16 * (s % 2) ..
@@ -161,6 +193,30 @@ struct G80 {
 #pragma unroll
         for (int j = 0; j < 16; ++j)
             y[j] = f16_bits(r.d) * (float)(int)__builtin_amdgcn_sbfe((int)w[j >> 2], 8 * (j & 3), 8);
+    }
+    // fp16 path: a code byte biased by 128 (xor 0x80) in the mantissa of
+    // 0x6400 is 1024 + q + 128; one fused fp32 multiply-add with fp16 output
+    // gives code * d - 1152 * d = d * q.
+    __device__ static void piece_h(const Raw &r, int, int, h8 &lo, h8 &hi8)
+    {
+        const float d = f16_bits(r.d), C = 1152.f * d;
+        const uint32_t w[4] = {r.qs.x ^ 0x80808080u, r.qs.y ^ 0x80808080u, r.qs.z ^ 0x80808080u,
+                               r.qs.w ^ 0x80808080u};
+        _Float16 y[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const h2 a = __builtin_bit_cast(h2, (w[i] & 0x00FF00FFu) | 0x64006400u);
+            const h2 b = __builtin_bit_cast(h2, ((w[i] >> 8) & 0x00FF00FFu) | 0x64006400u);
+            y[4 * i + 0] = (_Float16)__builtin_fmaf((float)a.x, d, -C);
+            y[4 * i + 2] = (_Float16)__builtin_fmaf((float)a.y, d, -C);
+            y[4 * i + 1] = (_Float16)__builtin_fmaf((float)b.x, d, -C);
+            y[4 * i + 3] = (_Float16)__builtin_fmaf((float)b.y, d, -C);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            lo[j] = y[j];
+            hi8[j] = y[8 + j];
+        }
     }
 };
 
@@ -182,6 +238,32 @@ struct G40 {
         for (int j = 0; j < 16; ++j) {
             const uint32_t q = __builtin_amdgcn_ubfe(w[j >> 2], 8 * (j & 3) + 4 * (s & 1), 4);
             y[j] = f16_bits(r.d) * (float)((int)q - 8);
+        }
+    }
+    // fp16 path as for Q4_K: a nibble in the mantissa of 0x6400 is 1024 + q
+    // (1024 + 16q for a high nibble left in place, with d' = d / 16), and one
+    // fused fp32 multiply-add with fp16 output gives code * d' - (1024 d' + 8 d).
+    __device__ static void piece_h(const Raw &r, int, int s, h8 &lo, h8 &hi8)
+    {
+        const float d = f16_bits(r.d);
+        const float Dp = (s & 1) ? d * 0.0625f : d;
+        const float C = 1024.f * Dp + 8.f * d;
+        const uint32_t mask = (s & 1) ? 0x00F000F0u : 0x000F000Fu;
+        const uint32_t w[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+        _Float16 y[16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const h2 a = __builtin_bit_cast(h2, (w[i] & mask) | 0x64006400u);
+            const h2 b = __builtin_bit_cast(h2, ((w[i] >> 8) & mask) | 0x64006400u);
+            y[4 * i + 0] = (_Float16)__builtin_fmaf((float)a.x, Dp, -C);
+            y[4 * i + 2] = (_Float16)__builtin_fmaf((float)a.y, Dp, -C);
+            y[4 * i + 1] = (_Float16)__builtin_fmaf((float)b.x, Dp, -C);
+            y[4 * i + 3] = (_Float16)__builtin_fmaf((float)b.y, Dp, -C);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            lo[j] = y[j];
+            hi8[j] = y[8 + j];
         }
     }
 };

@@ -46,6 +46,12 @@ def test_benchmark_shapes(device, orc, qtype, n, k, batch):
     (nat.Q8_0, 19, 128, 1), (nat.Q8_0, 9, 64, 2), (nat.Q8_0, 8, 20480, 1), (nat.Q8_0, 5, 4160, 3),
     (nat.Q4_0, 5, 64, 1), (nat.Q4_0, 66, 2048, 2), (nat.Q4_0, 3, 32768, 1),
     (nat.Q4_K, 3, 65536, 1),
+    # batch 3..8 (matrix-core kernel): chunks per wave around the ring depth
+    # (8 sets; 6 for Q6_K) -- tail only, one loop pass, exact multiples, a
+    # shorter last wave
+    (nat.Q4_K, 40, 8192, 3), (nat.Q4_K, 40, 8704, 4), (nat.Q4_K, 33, 7680, 8), (nat.Q4_K, 24, 8960, 3),
+    (nat.Q6_K, 48, 6144, 3), (nat.Q6_K, 48, 6656, 8), (nat.Q6_K, 17, 5632, 5),
+    (nat.Q8_0, 20, 8192, 6), (nat.Q4_0, 20, 8704, 7),
 ])
 def test_edge_shapes(device, orc, qtype, n, k, batch):
     w = synth_weight(qtype, n, k, seed=n * 1000 + k)

@@ -110,6 +110,17 @@ FUSED_GROUPS = (("attn_qkv", "concat", ("attn_q", "attn_k", "attn_v")),
                 ("ffn_gate_up", "interleave", ("ffn_gate", "ffn_up")))
 
 
+def interleave_rows(arrs, rows):
+    """Packed row-major matrices of `rows` rows each -> one byte array with
+    their rows interleaved: row i of matrix j lands at row i*len(arrs) + j
+    (for gate/up: row 2i = gate row i, row 2i+1 = up row i)."""
+    mats = [np.ascontiguousarray(a).reshape(-1).view(np.uint8) for a in arrs]
+    if any(m.size != mats[0].size for m in mats) or mats[0].size % rows:
+        raise ValueError("interleave_rows: matrices of different sizes or a size not divisible by rows")
+    rb = mats[0].size // rows
+    return np.stack([m.reshape(rows, rb) for m in mats], axis=1).reshape(-1)
+
+
 class DeviceWeights:
     """Every tensor of a weight dict in device memory, packed blocks verbatim
     (as aih_upload_tensor places them from a GGUF file).  The matrices of each
@@ -150,10 +161,7 @@ class DeviceWeights:
                         self.t[n] = (qt, buf.get_pointer() + off, weights[n][2], c)
                         off += a.nbytes
                 else:
-                    r = rows.pop()
-                    rb = arrs[0].nbytes // r
-                    rows_of = [a.reshape(-1).view(np.uint8).reshape(r, rb) for a in arrs]
-                    self._upload(buf.get_pointer(), np.stack(rows_of, axis=1), gname)
+                    self._upload(buf.get_pointer(), interleave_rows(arrs, rows.pop()), gname)
                 done.update(names)
                 self.t[gname] = (qt, buf.get_pointer(), sum(weights[n][2] for n in names), c)
             for name, (qt, arr, r, c) in weights.items():

@@ -310,6 +310,8 @@ def main():
         for name, qt, nn, kk, b in (("q4_0_14336x4096_b1", nat.Q4_0, 14336, 4096, 1),
                                     ("q8_0_4096x4096_b1", nat.Q8_0, 4096, 4096, 1),
                                     ("q6_k_4096x14336_b1", nat.Q6_K, 4096, 14336, 1),
+                                    ("q6_k_4096x14336_b2", nat.Q6_K, 4096, 14336, 2),
+                                    ("q6_k_4096x14336_b4", nat.Q6_K, 4096, 14336, 4),
                                     ("q6_k_4096x14336_b8", nat.Q6_K, 4096, 14336, 8),
                                     ("q4_k_4096x14336_b1", nat.Q4_K, 4096, 14336, 1)):
             mb = MatvecBench(dev, qt, nn, kk, b)

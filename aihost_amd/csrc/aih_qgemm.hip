@@ -11,18 +11,17 @@
 //
 // Tiling.  X is first converted to fp16 in the context's workspace, stored in
 // MFMA fragment order.  A workgroup then owns a 128 (M) x 64 (N) tile of Y and
-// walks K in steps of 64 elements (a Q4_K 64-group, a pair of Q8_0 or Q4_0
-// blocks, two quarters of a Q6_K half-block).  Four producer waves dequantize
-// W for the next step into LDS while four consumer waves multiply the current
-// step (two 32x32x16 MFMAs per 16 k per wave), their A fragments loaded
-// straight from the tiled X; one barrier per step.
+// walks K in super-steps of 256 elements: four producer waves dequantize W for
+// the next super-step into LDS while four consumer waves multiply the current
+// one, their A fragments loaded straight from the tiled X (see qgemm_kernel).
 //
 // Precision.  Both operands are rounded to fp16 (11-bit significand) and the
 // products accumulate in fp32: normwise error near 3e-4 against the fp32
 // reference.  bf16 operands (8-bit significand) would give about 2.4e-3, more
 // than the 1e-3 the path is held to.  Weights are dequantized in fp32 with the
 // reference's formulas (ComputeOps.cs:1629-1678 for Q4_K, :1735-1774 for Q6_K,
-// the GGUF definitions for Q8_0 and Q4_0) before the rounding to fp16.
+// the GGUF definitions for Q8_0 and Q4_0), computed as one fused fp32
+// multiply-add per weight with fp16 output (aih_pieces.h).
 #include "aih_pieces.h"
 
 namespace {
@@ -32,8 +31,7 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 128;          // activation rows per workgroup
 constexpr int BN = 64;           // weight rows per workgroup
-constexpr int BK = 64;           // K per step
-constexpr int LDK = BK + 8;      // LDS row stride in halves (16-byte pad against bank conflicts)
+constexpr int BK = 64;           // K granularity (one 64-element chunk)
 
 // Workgroup barrier for LDS traffic only: waits for this wave's LDS
 // operations, then for every wave.  __syncthreads() would also wait for the
@@ -72,159 +70,152 @@ x_tile_kernel(const float *__restrict__ X, int64_t M, int64_t K, _Float16 *__res
     }
 }
 
-// Eight waves per workgroup in two roles, one of each on every SIMD.
-//   Consumers (waves 0..3) each own a 64 (M) x 32 (N) sub-tile of the
-//   128 x 64 output tile (two 32x32 accumulators).  They load their A
-//   fragments straight from the tiled fp16 copy of X into registers, one
-//   step ahead in a ring of two register sets, and read the dequantized
-//   weights (B) from LDS.  The short ring keeps the kernel within 128
-//   registers, so two workgroups share a CU where the grid has enough of
-//   them (on MI355X, the 4096 x 4096 x 512 product ran 39.8 us against 43.2
-//   with four sets, three steps ahead).
-//   Producers (waves 4..7) load the packed weights four steps ahead, dequantize
-//   the next step into the other LDS buffer while the consumers multiply the
-//   current one.
-// One LDS barrier per step joins the roles.  Keeping X out of LDS leaves LDS
-// with the weight tile only (8 KB per step written, 16 KB read).
+// Eight waves per workgroup in two roles, one of each on every SIMD; the
+// workgroup owns a 128 (M) x 64 (N) tile of Y and walks K in super-steps of
+// 256 (a Q4_K/Q6_K super-block, 8 blocks of Q8_0/Q4_0), with one LDS barrier
+// per super-step and two tile buffers.
+//   Producers (waves 4..7) dequantize the next super-step of the 64 weight
+//   rows into LDS: wave p owns rows 16p .. 16p+15, and its 16 lanes per row
+//   take pieces 0..15 of the row's 256-k span (four rows per load, each read
+//   as one contiguous span; four lanes per row, one 64-k step at a time, put
+//   16 rows under every load).  Their packed loads run PR super-steps ahead
+//   in a ring of register sets.
+//   Consumers (waves 0..3): wave w owns rows 32w .. 32w+31 of the M tile and
+//   all 64 columns (two 32x32 accumulators sharing each A fragment).  A
+//   fragments come straight from the tiled fp16 copy of X, one super-step
+//   ahead; B fragments from LDS.
+// On MI355X this ran the 4096 x 4096 x 512 Q4_K product in 38 us per call
+// (with the X conversion), against 42 us for one barrier per 64 k.
+constexpr int SK = 256;            // k per super-step (one barrier)
+constexpr int SC = SK / 64;        // 64-k steps per super-step
+constexpr int LD2 = SK + 8;        // LDS row stride in halves (16-byte pad against bank conflicts)
+// producer ring depth in super-steps (Q6_K's larger raw sets: 2, within 256 registers)
+template <class T> struct GRing { static constexpr int PR = 3; };
+template <> struct GRing<G6K> { static constexpr int PR = 2; };
+
 template <class T>
-__global__ void __launch_bounds__(512, 2)
+__global__ void __launch_bounds__(512)
 qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
              const _Float16 *__restrict__ Xt, int64_t M, float *__restrict__ Y)
 {
-    __shared__ __align__(16) _Float16 wsh[2][BN][LDK];
-
+    constexpr int PR = GRing<T>::PR;
+    __shared__ __align__(16) _Float16 wsh[2][BN][LD2];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const bool producer = wave >= 4;
     const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
-    const int ns = (int)(K / BK);
+    const int nch = (int)(K / 64);
+    const int nss = (nch + SC - 1) / SC;
 
-    if (producer) {
-        // The four lanes of a quad share weight row t/4 and take its pieces
-        // 0..3, so they read the same header and the same 32 bytes of codes.
-        const int ptid = tid - 256;
-        const int wr = ptid >> 2, wp = ptid & 3;
-        const int64_t wn = n0 + wr < N ? n0 + wr : N - 1;
-        const uint8_t *wrow = W + wn * row_bytes;
-        // loads for step kb, clamped so that no load sits behind a branch
-        auto gload = [&](int kb, typename T::Raw &r) {
-            kb = kb < ns ? kb : ns - 1;
-            T::load(wrow, kb, wp, r);
+    if (wave >= 4) {
+        const int pw = wave - 4;
+        const int rl = lane >> 4, p = lane & 15, pc = p >> 2, ps = p & 3;
+        const uint8_t *wrow[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t wn = n0 + 16 * pw + 4 * i + rl;
+            wrow[i] = W + (wn < N ? wn : N - 1) * row_bytes;
+        }
+        auto gload = [&](int ss, typename T::Raw *r) {
+            int c = ss * SC + pc;
+            c = c < nch ? c : nch - 1;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) T::load(wrow[i], c, ps, r[i]);
         };
-        auto stage = [&](int buf, int kb, const typename T::Raw &r) {
-            // The step index is hidden from the optimiser: in the unrolled
-            // loop it would otherwise know kb % 4, find some loaded dwords
-            // unused (e.g. the scale bytes of the other sub-blocks), reuse
-            // their registers while the load is in flight and so wait for it.
-            asm volatile("" : "+s"(kb));
-            h8 lo, hi;
-            piece16h<T>(r, kb, wp, lo, hi);
-            *reinterpret_cast<h8 *>(&wsh[buf][wr][16 * wp]) = lo;
-            *reinterpret_cast<h8 *>(&wsh[buf][wr][16 * wp + 8]) = hi;
+        auto stage = [&](int ss, int buf, const typename T::Raw *r) {
+            asm volatile("" : "+s"(ss));
+            const int c = ss * SC + pc;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                h8 lo, hi;
+                piece16h<T>(r[i], c, ps, lo, hi);
+                if (c >= nch) lo = hi = h8{};
+                _Float16 *d = &wsh[buf][16 * pw + 4 * i + rl][64 * pc + 16 * ps];
+                *reinterpret_cast<h8 *>(d) = lo;
+                *reinterpret_cast<h8 *>(d + 8) = hi;
+            }
         };
-        // Four register sets in a ring: the loads for step kb+4 are issued
-        // while step kb+1 is staged.  The loop has a single exit at the bottom
-        // (an exit between a load and the loop head would make the compiler
-        // wait for every load there); the last one to three steps follow it.
-        typename T::Raw s0, s1, s2, s3;
-        gload(0, s0);
-        gload(1, s1);
-        gload(2, s2);
-        gload(3, s3);
-        stage(0, 0, s0);
-        lds_barrier();
-        int kb = 0;
-        for (; kb + 4 < ns; kb += 4) {
-            gload(kb + 4, s0);
-            __builtin_amdgcn_sched_barrier(0);
-            stage(1, kb + 1, s1);
-            lds_barrier();
-            gload(kb + 5, s1);
-            __builtin_amdgcn_sched_barrier(0);
-            stage(0, kb + 2, s2);
-            lds_barrier();
-            gload(kb + 6, s2);
-            __builtin_amdgcn_sched_barrier(0);
-            stage(1, kb + 3, s3);
-            lds_barrier();
-            gload(kb + 7, s3);
-            __builtin_amdgcn_sched_barrier(0);
-            stage(0, kb + 4, s0);
-            lds_barrier();
+        typename T::Raw ring[PR][4];
+#pragma unroll
+        for (int j = 0; j < PR; ++j) gload(j, ring[j]);
+        __builtin_amdgcn_sched_barrier(0);
+        int ss = 0;
+        for (; ss + 2 * PR <= nss; ss += PR) {
+#pragma unroll
+            for (int j = 0; j < PR; ++j) {
+                stage(ss + j, (ss + j) & 1, ring[j]);
+                gload(ss + j + PR, ring[j]);
+                __builtin_amdgcn_sched_barrier(0);
+                lds_barrier();
+            }
         }
-        if (kb + 1 < ns) {
-            stage(1, kb + 1, s1);
-            lds_barrier();
+#pragma unroll
+        for (int j = 0; j < PR; ++j) {
+            if (ss + j < nss) {
+                stage(ss + j, (ss + j) & 1, ring[j]);
+                if (ss + j + PR < nss) gload(ss + j + PR, ring[j]);
+                lds_barrier();
+            }
         }
-        if (kb + 2 < ns) {
-            stage(0, kb + 2, s2);
-            lds_barrier();
-        }
-        if (kb + 3 < ns) {
-            stage(1, kb + 3, s3);
-            lds_barrier();
+#pragma unroll
+        for (int j = 0; j < PR; ++j) {
+            if (ss + PR + j < nss) {
+                stage(ss + PR + j, (ss + PR + j) & 1, ring[j]);
+                lds_barrier();
+            }
         }
         return;
     }
 
-    // consumer: rows wm .. wm+63 of the M tile (M blocks mb0, mb0+1), columns
-    // wc .. wc+31 of the N tile
-    const int wm = (wave >> 1) * 64, wc = (wave & 1) * 32;
+    // consumer wave w: rows 32w .. 32w+31 of the M tile, all 64 columns
     const int fr = lane & 31, fk = 8 * (lane >> 5);
     const int64_t kc = K / 16, mblocks = (M + 31) / 32;
-    int64_t mb0 = (m0 + wm) / 32, mb1 = mb0 + 1;
-    mb0 = mb0 < mblocks ? mb0 : mblocks - 1;
-    mb1 = mb1 < mblocks ? mb1 : mblocks - 1;
-    const _Float16 *xa0 = Xt + (mb0 * kc * 64 + lane) * 8;
-    const _Float16 *xa1 = Xt + (mb1 * kc * 64 + lane) * 8;
-    struct AF { h8 a0[4], a1[4]; };
+    int64_t mb = (m0 + 32 * wave) / 32;
+    mb = mb < mblocks ? mb : mblocks - 1;
+    const _Float16 *xa = Xt + (mb * kc * 64 + lane) * 8;
+    struct AF { h8 a[4]; };
     auto aload = [&](int kb, AF &f) {
-        kb = kb < ns ? kb : ns - 1;
+        kb = kb < nch ? kb : nch - 1;
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            f.a0[kk] = ldg<h8>(xa0 + ((int64_t)kb * 4 + kk) * 512);
-            f.a1[kk] = ldg<h8>(xa1 + ((int64_t)kb * 4 + kk) * 512);
-        }
+        for (int kk = 0; kk < 4; ++kk) f.a[kk] = ldg<h8>(xa + ((int64_t)kb * 4 + kk) * 512);
     };
     f16v acc0 = {}, acc1 = {};
-    auto mfma = [&](int buf, const AF &f) {
+    auto mm = [&](int buf, int t, const AF &f) {
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-            const h8 b = *reinterpret_cast<const h8 *>(&wsh[buf][wc + fr][16 * kk + fk]);
-            acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a0[kk], b, acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a1[kk], b, acc1, 0, 0, 0);
+            const h8 b0 = *reinterpret_cast<const h8 *>(&wsh[buf][fr][64 * t + 16 * kk + fk]);
+            const h8 b1 = *reinterpret_cast<const h8 *>(&wsh[buf][32 + fr][64 * t + 16 * kk + fk]);
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[kk], b0, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[kk], b1, acc1, 0, 0, 0);
         }
     };
-    // the same barrier sequence as the producers; A loads one step ahead
-    AF f0, f1;
-    aload(0, f0);
-    aload(1, f1);
-    lds_barrier();
-    int kb = 0;
-    for (; kb + 2 < ns; kb += 2) {
-        mfma(kb & 1, f0);
-        aload(kb + 2, f0);
-        __builtin_amdgcn_sched_barrier(0);
-        lds_barrier();
-        mfma((kb + 1) & 1, f1);
-        aload(kb + 3, f1);
-        __builtin_amdgcn_sched_barrier(0);
-        lds_barrier();
-    }
-    mfma(kb & 1, f0);
-    if (kb + 1 < ns) {
-        lds_barrier();
-        mfma((kb + 1) & 1, f1);
-    }
-
-    // acc element r of lane l is C[8*(r/4) + 4*(l/32) + r%4][l%32] of its 32x32 block
-    const int64_t n = n0 + wc + fr;
-    if (n < N) {
+    // A ring of one super-step: slot t holds 64-k step SC*ss + t
+    AF f[SC];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int i = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            const int64_t ma = m0 + wm + i, mb = m0 + wm + 32 + i;
-            if (ma < M) Y[ma * N + n] = acc0[r];
-            if (mb < M) Y[mb * N + n] = acc1[r];
+    for (int t = 0; t < SC; ++t) aload(t, f[t]);
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+    int ss = 0;
+    for (; ss + 2 <= nss; ++ss) {
+        const int buf = ss & 1;
+#pragma unroll
+        for (int t = 0; t < SC; ++t) {
+            mm(buf, t, f[t]);
+            aload(SC * (ss + 1) + t, f[t]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        lds_barrier();
+    }
+#pragma unroll
+    for (int t = 0; t < SC; ++t)
+        if (SC * ss + t < nch) mm(ss & 1, t, f[t]);
+
+    const int64_t na = n0 + fr, nb = n0 + 32 + fr;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int i = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int64_t m = m0 + 32 * wave + i;
+        if (m < M) {
+            if (na < N) Y[m * N + na] = acc0[r];
+            if (nb < N) Y[m * N + nb] = acc1[r];
         }
     }
 }

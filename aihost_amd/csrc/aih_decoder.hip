@@ -381,115 +381,103 @@ attn_decode_partial(const float *__restrict__ Q, const float *__restrict__ Kc, c
     }
 }
 
-// Decode attention of one query row fused with the position steps before it.
-// Workgroup (kvh, s) serves the G = n_heads / n_kv_heads query heads of KV
-// head kvh over split s of the keys 0..L-1 (L = min(p + 1, cache_rows), p =
-// start + *pos), so each cached K/V row is read once for the G heads.  It
-// applies RoPE to the G query heads of the projection output QKV (q | k | v
-// of one row) itself, and the workgroup whose split holds key p ropes that
-// key, stores the key and value rows into the caches at row p and uses them
-// from LDS (no other workgroup reads row p).  Per head, the arithmetic and its
-// order are those of rope_qkv_kernel followed by attn_decode_partial, so the
-// partials are the same bits.
-template <int G>
+// Decode attention of one query row for the G = n_heads / n_kv_heads query
+// heads of one KV head: workgroup (kvh, s) serves those heads over split s of
+// the cache, so each cached K/V row is read once for the G heads.
+//
+// Splits cover fixed key ranges of the cache (chunk = ceil(cache_rows /
+// n_split) keys each), not ranges of the keys 0..p: the first K/V rows are
+// loaded before the position p = start + *pos arrives, and keys past p are
+// masked (a split past p writes an empty partial).
+//
+// Each wave keeps its own online softmax (running max, sum and V
+// accumulator) over its 16 keys of every 64-key sub-chunk, with no barrier
+// inside the key loop; the four waves are merged through LDS at the end.
+// Thread (key lane / 4, dims 32 * (lane % 4) ..) scores, thread lane
+// accumulates V dims 2 * lane, 2 * lane + 1.
+//
+// FUSE: the query comes from the projection output QKV (q | k | v of one
+// row); the kernel applies RoPE to q and to the new key itself, the split
+// holding key p stores the key and value rows into the caches at row p and
+// uses them from LDS (no other workgroup reads row p).  The arithmetic is
+// that of rope_qkv_kernel, so the FUSE and plain forms give the same bits.
+// Plain: the query rows are Q (already rotated) and every key comes from the
+// cache.
+template <int G, bool FUSE>
 __global__ void __launch_bounds__(256)
-attn_decode_qkv_partial(const float *__restrict__ QKV, float *Kc, float *Vc, float *__restrict__ part,
-                        int32_t n_heads, int32_t n_kv_heads, int32_t start, const int32_t *pos,
-                        const float *__restrict__ table, int32_t table_rows, int32_t cache_rows, float scale,
-                        int32_t n_split)
+attn_decode_gqa(const float *__restrict__ Qsrc, float *Kc, float *Vc, float *__restrict__ part, int32_t n_heads,
+                int32_t n_kv_heads, int32_t start, const int32_t *pos, const float *__restrict__ table,
+                int32_t table_rows, int32_t cache_rows, float scale, int32_t n_split)
 {
     constexpr int half = kHD / 2;
     constexpr int QP = (G * half + 255) / 256;   // query pairs per thread
     __shared__ f4 qs[G][kHD / 4];
     __shared__ f4 kn[kHD / 4], vn[kHD / 4];
-    __shared__ float ps[G][kSub];
-    __shared__ float red_m[4][G], red_s[4][G];
-    __shared__ f4 accs[8][G][kHD / 4];
-    const int kvh = blockIdx.x, s = blockIdx.y, t = threadIdx.x;
+    __shared__ float ps[4][G][16];
+    __shared__ float wm[4][G], wl[4][G];
+    __shared__ float wacc[4][G][kHD];
+    const int kvh = blockIdx.x, s = blockIdx.y, t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int kk = lane >> 2, part4 = lane & 3;
     const int64_t kv_stride = (int64_t)n_kv_heads * kHD;
-    const int32_t p = dev_pos(start, pos);
-    const int32_t L = max(0, min(p + 1, cache_rows));
-    const int32_t chunk = (L + n_split - 1) / n_split;
-    const int32_t j0 = min(s * chunk, L), j1 = min(L, j0 + chunk);
-    const bool own = j0 <= p && p < j1;   // this split holds the new key
-    const bool rot = p >= 0 && p < table_rows;
-    const float *tp = table + 2 * (int64_t)(rot ? p : 0) * half;
-    const float *kx = QKV + (int64_t)n_heads * kHD + (int64_t)kvh * kHD;   // the new key row
-    const float *vx = kx + kv_stride;                                       // the new value row
+    const int32_t chunk = (cache_rows + n_split - 1) / n_split;
+    const int32_t j0 = s * chunk, jc = min(j0 + chunk, cache_rows);   // the split, whatever p
+    const float *kbase = Kc + (int64_t)kvh * kHD + part4 * 32;
+    const float *vbase = Vc + (int64_t)kvh * kHD + 2 * lane;
 
-    // Loads in the order they are waited for: the query pairs, their (cos,
-    // sin) and the new K/V rows first, then the K and V rows of the first
-    // sub-chunk (the memory counter drains in order, so the RoPE below does
-    // not wait for the 64 KB of cached rows).  Row p itself, when this split
-    // holds it, is taken from LDS after the barrier.
-    float qx0[QP], qx1[QP], qc[QP], qsn[QP];
-#pragma unroll
-    for (int i = 0; i < QP; ++i) {
-        const int e = t + 256 * i;
-        const int g = min(e / half, G - 1), pi = e % half;
-        const float *x = QKV + (int64_t)(kvh * G + g) * kHD + 2 * pi;
-        qx0[i] = x[0];
-        qx1[i] = x[1];
-        qc[i] = tp[2 * pi];
-        qsn[i] = tp[2 * pi + 1];
-    }
-    float k0 = 0.f, k1 = 0.f, kcs = 0.f, ksn = 0.f;
-    f4 vnew = {0.f, 0.f, 0.f, 0.f};
-    if (own) {
-        if (t < half) {
-            k0 = kx[2 * t];
-            k1 = kx[2 * t + 1];
-            kcs = tp[2 * t];
-            ksn = tp[2 * t + 1];
-        } else if (t < half + kHD / 4) {
-            vnew = reinterpret_cast<const f4 *>(vx)[t - half];
-        }
-    }
-    // Thread t scores key t/4 of a sub-chunk over dims 32*(t%4).. and
-    // accumulates V dims 4*(t%32).. for keys t/32 + 8u.
-    const int kk = t >> 2, part4 = t & 3;
-    const int vc = t & 31, vr = t >> 5;
-    f4 k[8], vv[kSub / 8];
+    // first sub-chunk's K and V rows: issued before the position is read
+    f4 k[8];
+    float2 v[16];
     auto load_k = [&](int32_t c0) {
-        if (kk < min(kSub, j1 - c0)) {
-            const f4 *k4 = reinterpret_cast<const f4 *>(Kc + (int64_t)(c0 + kk) * kv_stride + kvh * kHD) + part4 * 8;
+        const int32_t j = c0 + 16 * w + kk;
+        if (j < jc) {
+            const f4 *k4 = reinterpret_cast<const f4 *>(kbase + (int64_t)j * kv_stride);
 #pragma unroll
             for (int d = 0; d < 8; ++d) k[d] = k4[d];
         }
     };
     auto load_v = [&](int32_t c0) {
-        const int n = min(kSub, j1 - c0);
 #pragma unroll
-        for (int u = 0; u < kSub / 8; ++u) {
-            const int j = vr + 8 * u;
-            vv[u] = j < n ? reinterpret_cast<const f4 *>(Vc + (int64_t)(c0 + j) * kv_stride + kvh * kHD)[vc]
-                          : f4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < 16; ++i) {
+            const int32_t j = c0 + 16 * w + i;
+            v[i] = j < jc ? *reinterpret_cast<const float2 *>(vbase + (int64_t)j * kv_stride) : float2{0.f, 0.f};
         }
     };
-    __builtin_amdgcn_sched_barrier(0);
-    if (j0 < j1) {
-        load_k(j0);
-        load_v(j0);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // RoPE of the G query heads into LDS: pair pi of head g
+    load_k(j0);
+    load_v(j0);
+
+    const int32_t p = dev_pos(start, pos);
+    const int32_t L = max(0, min(p + 1, cache_rows));
+    const int32_t j1 = min(jc, L);                      // active keys: j0 .. j1-1
+    const bool own = FUSE && j0 <= p && p < j1;        // this split holds the new key
+    const bool rot = p >= 0 && p < table_rows;
+    const float *tp = table + 2 * (int64_t)(rot ? p : 0) * half;
+
+    // query heads into LDS (rotated here when FUSE), the new key row when owned
 #pragma unroll
     for (int i = 0; i < QP; ++i) {
         const int e = t + 256 * i;
         if (e < G * half) {
-            float *y = reinterpret_cast<float *>(&qs[e / half][0]) + 2 * (e % half);
-            if (rot) {
-                y[0] = qx0[i] * qc[i] - qx1[i] * qsn[i];
-                y[1] = qx0[i] * qsn[i] + qx1[i] * qc[i];
+            const int g = e / half, pi = e % half;
+            const float *x = Qsrc + (int64_t)(kvh * G + g) * kHD + 2 * pi;
+            const float x0 = x[0], x1 = x[1];
+            float *y = reinterpret_cast<float *>(&qs[g][0]) + 2 * pi;
+            if (FUSE && rot) {
+                const float c = tp[2 * pi], sn = tp[2 * pi + 1];
+                y[0] = x0 * c - x1 * sn;
+                y[1] = x0 * sn + x1 * c;
             } else {
-                y[0] = qx0[i];
-                y[1] = qx1[i];
+                y[0] = x0;
+                y[1] = x1;
             }
         }
     }
     if (own) {
+        const float *kx = Qsrc + (int64_t)n_heads * kHD + (int64_t)kvh * kHD;
+        const float *vx = kx + kv_stride;
         if (t < half) {
-            const float y0 = k0 * kcs - k1 * ksn, y1 = k0 * ksn + k1 * kcs;
+            const float c = tp[2 * t], sn = tp[2 * t + 1];
+            const float x0 = kx[2 * t], x1 = kx[2 * t + 1];
+            const float y0 = x0 * c - x1 * sn, y1 = x0 * sn + x1 * c;
             float *kq = reinterpret_cast<float *>(kn) + 2 * t;
             kq[0] = y0;
             kq[1] = y1;
@@ -497,36 +485,46 @@ attn_decode_qkv_partial(const float *__restrict__ QKV, float *Kc, float *Vc, flo
             kc[0] = y0;
             kc[1] = y1;
         } else if (t < half + kHD / 4) {
-            vn[t - half] = vnew;
-            reinterpret_cast<f4 *>(Vc + (int64_t)p * kv_stride + (int64_t)kvh * kHD)[t - half] = vnew;
+            const f4 vv = reinterpret_cast<const f4 *>(vx)[t - half];
+            vn[t - half] = vv;
+            reinterpret_cast<f4 *>(Vc + (int64_t)p * kv_stride + (int64_t)kvh * kHD)[t - half] = vv;
         }
     }
     __syncthreads();
+
     float m[G], l[G];
-    f4 acc[G];
+    float2 acc[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         m[g] = -INFINITY;
         l[g] = 0.f;
-        acc[g] = f4{0.f, 0.f, 0.f, 0.f};
+        acc[g] = float2{0.f, 0.f};
     }
-    // Two barriers per sub-chunk: red_m, ps and red_s are each written after
-    // the barrier that follows their last reads in the previous sub-chunk.
-    for (int32_t c0 = j0; c0 < j1; c0 += kSub) {
-        const int n = min(kSub, j1 - c0);
-        if (c0 + kk == p) {
+    for (int32_t c0 = j0; c0 < j1; c0 += 64) {
+        const int32_t jk = c0 + 16 * w + kk;              // this thread's key
+        if (own && jk == p) {
 #pragma unroll
             for (int d = 0; d < 8; ++d) k[d] = kn[part4 * 8 + d];
         }
+        if (own) {
 #pragma unroll
-        for (int u = 0; u < kSub / 8; ++u)
-            if (c0 + vr + 8 * u == p) vv[u] = vn[vc];
-        float sc[G];
+            for (int i = 0; i < 16; ++i)
+                if (c0 + 16 * w + i == p) v[i] = reinterpret_cast<const float2 *>(vn)[lane];
+        }
+        // rows past p were loaded before p was known: their weights are 0,
+        // and their values are zeroed too (a stale row may hold NaN)
 #pragma unroll
-        for (int g = 0; g < G; ++g) sc[g] = -INFINITY;
-        if (kk < n) {
+        for (int i = 0; i < 16; ++i)
+            if (c0 + 16 * w + i >= j1) v[i] = float2{0.f, 0.f};
+        // query heads in blocks of at most four (the block's scores, weights
+        // and corrections in registers; K and V rows shared by all blocks)
+        constexpr int GB = G < 4 ? G : 4;
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
+        for (int g0 = 0; g0 < G; g0 += GB) {
+            float sc[GB];
+#pragma unroll
+            for (int gb = 0; gb < GB; ++gb) {
+                const int g = g0 + gb;
                 float a = 0.f;
 #pragma unroll
                 for (int d = 0; d < 8; ++d) {
@@ -538,69 +536,66 @@ attn_decode_qkv_partial(const float *__restrict__ QKV, float *Kc, float *Vc, flo
                 }
                 a += xor1(a);
                 a += xor2(a);
-                sc[g] = a * scale;
+                sc[gb] = jk < j1 ? a * scale : -INFINITY;
+            }
+            float corr[GB];
+#pragma unroll
+            for (int gb = 0; gb < GB; ++gb) {
+                const int g = g0 + gb;
+                const float mn = fmaxf(m[g], wave_max(sc[gb]));
+                const float e = jk < j1 ? expf(sc[gb] - mn) : 0.f;
+                if (part4 == 0) ps[w][g][kk] = e;
+                const float lw = wave_sum(part4 == 0 ? e : 0.f);
+                corr[gb] = mn == -INFINITY ? 1.f : expf(m[g] - mn);
+                l[g] = l[g] * corr[gb] + lw;
+                m[g] = mn;
+            }
+            // ps[w] is written and read by this wave only (LDS order within a wave)
+#pragma unroll
+            for (int gb = 0; gb < GB; ++gb) {
+                const int g = g0 + gb;
+                float2 a = {0.f, 0.f};
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const float pi = ps[w][g][i];
+                    a.x = fmaf(pi, v[i].x, a.x);
+                    a.y = fmaf(pi, v[i].y, a.y);
+                }
+                acc[g].x = acc[g].x * corr[gb] + a.x;
+                acc[g].y = acc[g].y * corr[gb] + a.y;
             }
         }
-        if (c0 + kSub < j1) load_k(c0 + kSub);   // the next sub-chunk's keys, while this one finishes
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float mc = wave_max(sc[g]);
-            if ((t & 63) == 0) red_m[t >> 6][g] = mc;
-        }
-        __syncthreads();
-        float mn[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            mn[g] = fmaxf(m[g], fmaxf(fmaxf(red_m[0][g], red_m[1][g]), fmaxf(red_m[2][g], red_m[3][g])));
-            const float e = kk < n ? expf(sc[g] - mn[g]) : 0.f;
-            if (part4 == 0) ps[g][kk] = e;
-            const float w = wave_sum(part4 == 0 ? e : 0.f);
-            if ((t & 63) == 0) red_s[t >> 6][g] = w;
-        }
-        __syncthreads();   // publishes ps and the partial sums
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float lc = 0.f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) lc += red_s[i][g];
-            const float corr = expf(m[g] - mn[g]);   // 0 on the first sub-chunk
-            l[g] = l[g] * corr + lc;
-            f4 a = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int u = 0; u < kSub / 8; ++u) {
-                const int j = vr + 8 * u;
-                const float pj = j < n ? ps[g][j] : 0.f;
-                a.x = fmaf(pj, vv[u].x, a.x);
-                a.y = fmaf(pj, vv[u].y, a.y);
-                a.z = fmaf(pj, vv[u].z, a.z);
-                a.w = fmaf(pj, vv[u].w, a.w);
-            }
-            acc[g] = acc[g] * corr + a;
-            m[g] = mn[g];
-        }
-        if (c0 + kSub < j1) load_v(c0 + kSub);
+        if (c0 + 64 < j1) load_k(c0 + 64);   // the next sub-chunk's keys
+        if (c0 + 64 < j1) load_v(c0 + 64);
     }
+
+    // merge the four waves: M = max of the wave maxima; weights e^(m_w - M)
 #pragma unroll
-    for (int g = 0; g < G; ++g) accs[vr][g][vc] = acc[g];
+    for (int g = 0; g < G; ++g) {
+        if (lane == 0) {
+            wm[w][g] = m[g];
+            wl[w][g] = l[g];
+        }
+        wacc[w][g][2 * lane] = acc[g].x;
+        wacc[w][g][2 * lane + 1] = acc[g].y;
+    }
     __syncthreads();
     for (int e = t; e < G * kHD; e += 256) {
         const int g = e / kHD, d = e % kHD;
-        const float *af = reinterpret_cast<const float *>(&accs[0][g][0]);
-        float v = 0.f;
+        const float M = fmaxf(fmaxf(wm[0][g], wm[1][g]), fmaxf(wm[2][g], wm[3][g]));
+        float o = 0.f, lt = 0.f;
 #pragma unroll
-        for (int r = 0; r < 8; ++r) v += af[r * G * kHD + d];
-        part[((int64_t)(kvh * G + g) * n_split + s) * (kHD + 2) + 2 + d] = v;
-    }
-    if (t < G) {
-        float *mine = part + ((int64_t)(kvh * G + t) * n_split + s) * (kHD + 2);
-        float mt = m[0], lt = l[0];
-#pragma unroll
-        for (int g = 1; g < G; ++g) {
-            mt = t == g ? m[g] : mt;
-            lt = t == g ? l[g] : lt;
+        for (int ww = 0; ww < 4; ++ww) {
+            const float f = wm[ww][g] == -INFINITY ? 0.f : expf(wm[ww][g] - M);
+            o = fmaf(wacc[ww][g][d], f, o);
+            lt = fmaf(wl[ww][g], f, lt);
         }
-        mine[0] = j1 > j0 ? mt : -INFINITY;
-        mine[1] = j1 > j0 ? lt : 0.f;
+        float *mine = part + ((int64_t)(kvh * G + g) * n_split + s) * (kHD + 2);
+        mine[2 + d] = o;
+        if (d == 0) {
+            mine[0] = M;          // -inf for a split with no key at or before p
+            mine[1] = lt;
+        }
     }
 }
 
@@ -770,6 +765,31 @@ bool aligned16(const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0;
 
 }  // namespace
 
+namespace {
+
+// Grouped decode attention for query groups of 1, 2, 4 or 8 heads
+// (AIH_E_UNSUPPORTED otherwise); FUSE selects aih_attention_decode_qkv's form.
+template <bool FUSE>
+int launch_gqa(aih_ctx *ctx, int group, dim3 grid, const float *Qsrc, float *Kc, float *Vc, float *part,
+               int32_t n_heads, int32_t n_kv_heads, int32_t start, const int32_t *pos, const float *table,
+               int32_t table_rows, int32_t cache_rows, float scale, int32_t n_split)
+{
+    switch (group) {
+    case 1: hipLaunchKernelGGL((attn_decode_gqa<1, FUSE>), grid, dim3(256), 0, ctx->stream, Qsrc, Kc, Vc, part,
+                               n_heads, n_kv_heads, start, pos, table, table_rows, cache_rows, scale, n_split); break;
+    case 2: hipLaunchKernelGGL((attn_decode_gqa<2, FUSE>), grid, dim3(256), 0, ctx->stream, Qsrc, Kc, Vc, part,
+                               n_heads, n_kv_heads, start, pos, table, table_rows, cache_rows, scale, n_split); break;
+    case 4: hipLaunchKernelGGL((attn_decode_gqa<4, FUSE>), grid, dim3(256), 0, ctx->stream, Qsrc, Kc, Vc, part,
+                               n_heads, n_kv_heads, start, pos, table, table_rows, cache_rows, scale, n_split); break;
+    case 8: hipLaunchKernelGGL((attn_decode_gqa<8, FUSE>), grid, dim3(256), 0, ctx->stream, Qsrc, Kc, Vc, part,
+                               n_heads, n_kv_heads, start, pos, table, table_rows, cache_rows, scale, n_split); break;
+    default: return AIH_E_UNSUPPORTED;
+    }
+    return aih_launch_status();
+}
+
+}  // namespace
+
 extern "C" {
 
 int aih_rmsnorm(aih_ctx *ctx, const float *X, const float *W, float *Y, int64_t rows, int64_t cols, float eps)
@@ -881,9 +901,16 @@ int aih_attention(aih_ctx *ctx, const float *Q, const float *Kc, const float *Vc
         const int32_t n_split = decode_splits(max_len);
         const int64_t n_part = (int64_t)n_heads * n_split * (kHD + 2);
         if (!scratch || scratch_floats < n_part) return AIH_E_INVALID;
-        hipLaunchKernelGGL(attn_decode_partial, dim3(n_heads, n_split), dim3(256), 0, ctx->stream, Q, Kc, Vc, scratch,
-                           n_heads, n_kv_heads, start, pos, max_len, scale, n_split);
-        const int rc = aih_launch_status();
+        // query groups of 1, 2, 4 or 8 heads: the grouped kernel (the plain
+        // form of aih_attention_decode_qkv's); others: one workgroup per head
+        int rc = launch_gqa<false>(ctx, n_heads / n_kv_heads, dim3(n_kv_heads, n_split), Q,
+                                   const_cast<float *>(Kc), const_cast<float *>(Vc), scratch, n_heads, n_kv_heads,
+                                   start, pos, nullptr, 0, max_len, scale, n_split);
+        if (rc == AIH_E_UNSUPPORTED) {
+            hipLaunchKernelGGL(attn_decode_partial, dim3(n_heads, n_split), dim3(256), 0, ctx->stream, Q, Kc, Vc,
+                               scratch, n_heads, n_kv_heads, start, pos, max_len, scale, n_split);
+            rc = aih_launch_status();
+        }
         if (rc) return rc;
         hipLaunchKernelGGL(attn_decode_combine, dim3(n_heads), dim3(kHD), 0, ctx->stream, scratch, O, n_split);
         return aih_launch_status();
@@ -910,19 +937,8 @@ int aih_attention_decode_qkv(aih_ctx *ctx, const float *QKV, float *Kc, float *V
     const int32_t n_split = decode_splits(max_len);
     const int64_t n_part = (int64_t)n_heads * n_split * (kHD + 2);
     if (!scratch || scratch_floats < n_part) return AIH_E_INVALID;
-    const dim3 grid(n_kv_heads, n_split);
-    switch (n_heads / n_kv_heads) {
-    case 1: hipLaunchKernelGGL(attn_decode_qkv_partial<1>, grid, dim3(256), 0, ctx->stream, QKV, Kc, Vc, scratch,
-                               n_heads, n_kv_heads, start, pos, table, table_rows, max_len, scale, n_split); break;
-    case 2: hipLaunchKernelGGL(attn_decode_qkv_partial<2>, grid, dim3(256), 0, ctx->stream, QKV, Kc, Vc, scratch,
-                               n_heads, n_kv_heads, start, pos, table, table_rows, max_len, scale, n_split); break;
-    case 4: hipLaunchKernelGGL(attn_decode_qkv_partial<4>, grid, dim3(256), 0, ctx->stream, QKV, Kc, Vc, scratch,
-                               n_heads, n_kv_heads, start, pos, table, table_rows, max_len, scale, n_split); break;
-    case 8: hipLaunchKernelGGL(attn_decode_qkv_partial<8>, grid, dim3(256), 0, ctx->stream, QKV, Kc, Vc, scratch,
-                               n_heads, n_kv_heads, start, pos, table, table_rows, max_len, scale, n_split); break;
-    default: return AIH_E_UNSUPPORTED;
-    }
-    const int rc = aih_launch_status();
+    const int rc = launch_gqa<true>(ctx, n_heads / n_kv_heads, dim3(n_kv_heads, n_split), QKV, Kc, Vc, scratch,
+                                    n_heads, n_kv_heads, start, pos, table, table_rows, max_len, scale, n_split);
     if (rc) return rc;
     hipLaunchKernelGGL(attn_decode_combine, dim3(n_heads), dim3(kHD), 0, ctx->stream, scratch, O, n_split);
     return aih_launch_status();

@@ -364,3 +364,10 @@ def test_attention_decode_qkv_argument_errors(device, bufs):
     assert f(h, X, X, X, X, 32, 8, 128, 8, None, X, 8, 8, 1.0, X, 8192) == nat.AIH_E_LIMIT       # start past the cache
     assert f(h, X, X, X, X, 32, 8, 128, 0, None, X, 8, 8, 1.0, X, 100) == nat.AIH_E_INVALID      # scratch too small
     device.synchronize()
+
+
+@pytest.mark.parametrize("nh,nkv,keys", [(12, 4, 100), (6, 1, 640), (24, 8, 65), (8, 8, 1)])
+def test_attention_decode_other_group_sizes(device, bufs, nh, nkv, keys):
+    # groups of 3 and 6 heads take the one-workgroup-per-head kernel; 1 the
+    # grouped one with a single head
+    _attn(device, bufs, 1, keys - 1, 640, nh=nh, nkv=nkv)

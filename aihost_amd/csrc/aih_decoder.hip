@@ -725,18 +725,61 @@ argmax_kernel(const float *__restrict__ X, int64_t n, int32_t *token, int32_t *p
               int64_t hist_len, int32_t hist_offset)
 {
     __shared__ float bv[16];
-    __shared__ int64_t bi[16];
+    __shared__ int32_t bi[16];
+    // the position is read now, while the scan runs (n < 2^31: 32-bit indices)
+    const int32_t p0 = pos && threadIdx.x == 0 ? *pos : 0;
+    const int32_t nn = (int32_t)n;
     float v = -INFINITY;
-    int64_t idx = INT64_MAX;
-    for (int64_t i = threadIdx.x; i < n; i += 1024) {
-        const float x = X[i];
-        if (x > v || (idx == INT64_MAX && x == v)) { v = x; idx = i; }
+    int32_t idx = INT32_MAX;
+    // 32 elements per thread per round, all loads issued before the
+    // comparisons (one memory round trip for a vocabulary up to 32768), which
+    // then run in index order; positions past n read as NaN, which never wins.
+    // A 16-byte aligned X is read as 8 vectors per thread (plus a tail of at
+    // most 3 elements), otherwise element by element.
+    auto take = [&](float x, int32_t i) {
+        if (x > v || (idx == INT32_MAX && x == v)) { v = x; idx = i; }
+    };
+    if ((reinterpret_cast<uintptr_t>(X) & 15) == 0) {
+        const f4 *X4 = reinterpret_cast<const f4 *>(X);
+        const int32_t n4 = nn >> 2;
+        const f4 nan4 = {__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")};
+        for (int32_t b0 = 0; b0 < n4; b0 += 1024 * 8) {
+            f4 xs[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int64_t i4 = (int64_t)b0 + j * 1024 + threadIdx.x;
+                xs[j] = i4 < n4 ? X4[i4] : nan4;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int32_t i = 4 * (b0 + j * 1024 + (int32_t)threadIdx.x);
+                take(xs[j].x, i);
+                take(xs[j].y, i + 1);
+                take(xs[j].z, i + 2);
+                take(xs[j].w, i + 3);
+            }
+            if (n4 - b0 <= 1024 * 8) break;
+        }
+        if ((int32_t)threadIdx.x < nn - 4 * n4) take(X[4 * n4 + threadIdx.x], 4 * n4 + (int32_t)threadIdx.x);
+    } else {
+        constexpr int U = 32;
+        for (int32_t b0 = 0; b0 < nn; b0 += 1024 * U) {
+            float xs[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int64_t i = (int64_t)b0 + u * 1024 + threadIdx.x;
+                xs[u] = i < nn ? X[i] : __builtin_nanf("");
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) take(xs[u], b0 + u * 1024 + (int32_t)threadIdx.x);
+            if (nn - b0 <= 1024 * U) break;
+        }
     }
     // (value desc, index asc) reduction
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(v, o);
-        const int64_t oi = __shfl_xor(idx, o);
+        const int32_t oi = __shfl_xor(idx, o);
         if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
     }
     if ((threadIdx.x & 63) == 0) { bv[threadIdx.x >> 6] = v; bi[threadIdx.x >> 6] = idx; }
@@ -744,12 +787,12 @@ argmax_kernel(const float *__restrict__ X, int64_t n, int32_t *token, int32_t *p
     if (threadIdx.x == 0) {
         for (int w = 1; w < 16; ++w)
             if (bv[w] > v || (bv[w] == v && bi[w] < idx)) { v = bv[w]; idx = bi[w]; }
-        const int32_t tok = idx == INT64_MAX ? 0 : (int32_t)idx;
+        const int32_t tok = idx == INT32_MAX ? 0 : idx;
         *token = tok;
         if (pos) {
-            const int64_t k = (int64_t)*pos - hist_offset;
+            const int64_t k = (int64_t)p0 - hist_offset;
             if (history && k >= 0 && k < hist_len) history[k] = tok;
-            *pos = *pos + 1;
+            *pos = p0 + 1;
         }
     }
 }

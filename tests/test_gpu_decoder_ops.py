@@ -371,3 +371,30 @@ def test_attention_decode_other_group_sizes(device, bufs, nh, nkv, keys):
     # groups of 3 and 6 heads take the one-workgroup-per-head kernel; 1 the
     # grouped one with a single head
     _attn(device, bufs, 1, keys - 1, 640, nh=nh, nkv=nkv)
+
+
+@pytest.mark.parametrize("n,where", [(1, 0), (32768, 32767), (32769, 32768), (100000, 70001), (128256, 5)])
+def test_argmax_sizes(device, bufs, n, where):
+    # one and several rounds of the batched scan; the maximum anywhere
+    x = rnd(n % 97 + 3, n)
+    x[where] = 99.0
+    X, T = bufs.up(x), bufs.empty(16)
+    nat.check(L.aih_argmax(device.handle, X, n, T, None, None, 0, 0), "argmax")
+    assert bufs.read(T, 1, np.int32)[0] == where == ol.argmax(x)
+
+
+def test_argmax_all_nan_gives_zero(device, bufs):
+    x = np.full(40000, np.nan, np.float32)
+    X, T = bufs.up(x), bufs.empty(16, fill=0x7F)
+    nat.check(L.aih_argmax(device.handle, X, x.size, T, None, None, 0, 0), "argmax")
+    assert bufs.read(T, 1, np.int32)[0] == 0
+
+
+@pytest.mark.parametrize("n,where,offset", [(32003, 32002, 0), (10, 9, 1), (70001, 70000, 0), (70001, 3, 3)])
+def test_argmax_unaligned_and_tails(device, bufs, n, where, offset):
+    # vector path with a 1-3 element tail, and an X not 16-byte aligned
+    x = rnd(n + offset, n + offset)
+    x[offset + where] = 77.0
+    X, T = bufs.up(x), bufs.empty(16)
+    nat.check(L.aih_argmax(device.handle, X + 4 * offset, n, T, None, None, 0, 0), "argmax")
+    assert bufs.read(T, 1, np.int32)[0] == where == ol.argmax(x[offset:])

@@ -6,6 +6,7 @@
 #include <cstddef>
 #include <mutex>
 #include <unordered_map>
+#include <vector>
 
 #include "../../include/aihost_hip.h"
 
@@ -47,15 +48,18 @@ struct aih_ctx {
     size_t tracked_bytes = 0;
     int cu_count = 0;
     // Grow-only device workspace for kernels that stage data (the GEMM's fp16
-    // copy of X).  Not counted in tracked_bytes; freed by aih_destroy.
+    // copy of X, the small-batch matvec's partial sums).  Not counted in
+    // tracked_bytes.  A smaller one that a larger replaced stays allocated
+    // (graphs captured earlier still point at it); all are freed by aih_destroy.
     void *work = nullptr;
     size_t work_bytes = 0;
+    std::vector<void *> work_retired;
 };
 
-// Device workspace of at least `bytes` on the context's device.  Grows by
-// reallocating (hipFree waits for the device), which is refused while the
-// stream is being captured into a graph: run the operation once outside the
-// capture first.  Returns AIH_OK or a status.
+// Device workspace of at least `bytes` on the context's device.  Growing it
+// allocates, which is refused while the stream is being captured into a graph
+// (AIH_E_LIMIT): run the operation once outside the capture first.  Returns
+// AIH_OK or a status.
 int aih_workspace(aih_ctx *ctx, size_t bytes, void **out);
 
 #define AIH_TRY(expr)                                  \

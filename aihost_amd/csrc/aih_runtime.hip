@@ -31,6 +31,7 @@ int release(aih_ctx *ctx)
     for (int i = 0; i < aih_ctx::kEvents; ++i)
         if (ctx->ev[i]) (void)hipEventDestroy(ctx->ev[i]);
     if (ctx->work) (void)hipFree(ctx->work);
+    for (void *p : ctx->work_retired) (void)hipFree(p);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return AIH_OK;
@@ -47,18 +48,18 @@ int aih_workspace(aih_ctx *ctx, size_t bytes, void **out)
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     AIH_TRY(hipStreamIsCapturing(ctx->stream, &cs));
     if (cs != hipStreamCaptureStatusNone) return AIH_E_LIMIT;
-    if (ctx->work) {
-        AIH_TRY(hipFree(ctx->work));
-        ctx->work = nullptr;
-        ctx->work_bytes = 0;
-    }
-    const size_t sz = (bytes + ((size_t)1 << 20) - 1) & ~(((size_t)1 << 20) - 1);   // whole MiB
-    hipError_t e = hipMalloc(&ctx->work, sz);
+    // whole MiB, at least double the current size (the retired ones then
+    // add up to less than the current one)
+    size_t sz = (bytes + ((size_t)1 << 20) - 1) & ~(((size_t)1 << 20) - 1);
+    if (sz < 2 * ctx->work_bytes) sz = 2 * ctx->work_bytes;
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, sz);
     if (e != hipSuccess) {
         (void)hipGetLastError();
-        ctx->work = nullptr;
         return (int)e;
     }
+    if (ctx->work) ctx->work_retired.push_back(ctx->work);
+    ctx->work = p;
     ctx->work_bytes = sz;
     *out = ctx->work;
     return AIH_OK;

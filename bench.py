@@ -58,6 +58,7 @@ class MatvecBench:
         self.x = dev.create_buffer(self.x_host.nbytes)
         self.x.write(self.x_host)
         self.y = dev.create_buffer(batch * n * 4)
+        self._launch(self.w[0])   # sizes the library's workspace (batch 3..8), which cannot grow during capture
         dev.synchronize()
         L, h = nat.lib(), dev.handle
         nat.check(L.aih_capture_begin(h), "aih_capture_begin")

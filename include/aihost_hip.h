@@ -145,7 +145,10 @@ int aih_dequantize(aih_ctx *ctx, int type, const void *q, float *out,
 
 /* Decode matvec, dequantization fused:
  *   Y[b*ldy + n] = sum_k X[b*ldx + k] * W[n, k],   b < batch (1..8), n < N.
- * K must be a whole number of blocks.  fp32 accumulation.
+ * K must be a whole number of blocks.  fp32 accumulation.  For batch 3..8, K
+ * is split over workgroups and the partial sums (splits x batch x N floats)
+ * go through the context workspace (see aih_qgemm); a call captured into a
+ * graph before the workspace is large enough runs with one split instead.
  * Replaces TempF32 + ComputeOps.MatMulWeights for M = batch <= 8
  * (TransformerBase.cs:254-271, ComputeOps.cs:275-309, ComputeShaders.cs:93-129). */
 int aih_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
@@ -182,7 +185,8 @@ int aih_qmatvec_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t 
  * fp16 and contracted on MFMA with fp32 accumulation.  K must be a multiple
  * of 64 (else AIH_E_LIMIT) and X 16-byte aligned.  The workspace cannot grow
  * while the stream is being captured (AIH_E_LIMIT): run the largest GEMM once
- * before capturing.  Replaces TempF32 + ComputeOps.MatMulWeights for M > 8. */
+ * before capturing.  A workspace replaced by a larger one stays allocated
+ * until aih_destroy, so graphs captured earlier stay valid.  Replaces TempF32 + ComputeOps.MatMulWeights for M > 8. */
 int aih_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
               const float *X, int64_t M, float *Y);
 

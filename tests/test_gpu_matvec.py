@@ -6,6 +6,8 @@ Covers the benchmark shapes (Q8_0 4096x4096; Q4_0 and Q4_K 14336x4096; Q6_K
 multi-wave K (14336), K beyond 256 units (1024-thread variant), odd batch,
 matrices taller than one launch, padded strides, and argument errors.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -52,6 +54,11 @@ def test_benchmark_shapes(device, orc, qtype, n, k, batch):
     (nat.Q4_K, 40, 8192, 3), (nat.Q4_K, 40, 8704, 4), (nat.Q4_K, 33, 7680, 8), (nat.Q4_K, 24, 8960, 3),
     (nat.Q6_K, 48, 6144, 3), (nat.Q6_K, 48, 6656, 8), (nat.Q6_K, 17, 5632, 5),
     (nat.Q8_0, 20, 8192, 6), (nat.Q4_0, 20, 8704, 7),
+    # batch 3..8 with K split over workgroups (sizes for 256 CUs): splits of
+    # several rounds with a partial last unit (Q4_0, 17 units of which the
+    # last holds 2 blocks, 3 splits of 6/6/5 units); rounds of 2 + 1 units
+    # (Q6_K); one split per row tile, Y stored directly (Q8_0, 1032 tiles)
+    (nat.Q4_0, 21888, 4160, 4), (nat.Q6_K, 21888, 2048, 8), (nat.Q8_0, 66000, 256, 5),
 ])
 def test_edge_shapes(device, orc, qtype, n, k, batch):
     w = synth_weight(qtype, n, k, seed=n * 1000 + k)
@@ -72,6 +79,69 @@ def test_tall_matrices(device, orc, qtype, n, k, batch):
     y = qmatvec(device, qtype, w, n, k, x)
     ref = orc.matvec(qtype, w, n, k, x, nthreads=8)
     assert_close(y, ref, TOL, "type %d %dx%d b%d" % (qtype, n, k, batch))
+
+
+def test_small_batch_in_graphs(orc):
+    """Batch 3..8 captured into a graph: before the workspace is sized the
+    call runs with one split (no workspace); after it, with the split path,
+    whose replays equal the eager call bit for bit (the splits are added in a
+    fixed order).  Replays alternate with eager work."""
+    from aihost_amd.compute import HipComputeDevice
+    L = nat.lib()
+    n, k, batch = 4096, 7168, 4
+    w = synth_weight(nat.Q6_K, n, k, seed=3)
+    x = x_of(k, batch, seed=4)
+    ref = orc.matvec(nat.Q6_K, w, n, k, x, nthreads=8)
+    dev = HipComputeDevice(0)   # a fresh context: empty workspace
+    bufs = []
+    try:
+        wb, xb = upload(dev, w), upload(dev, x)
+        ya, yb = dev.create_buffer(batch * n * 4), dev.create_buffer(batch * n * 4)
+        bufs = [wb, xb, ya, yb]
+
+        def call(y):
+            nat.check(L.aih_qmatvec(dev.handle, nat.Q6_K, wb.get_pointer(), n, k, xb.get_pointer(), k,
+                                    y.get_pointer(), n, batch), "aih_qmatvec")
+
+        def capture(y):
+            nat.check(L.aih_capture_begin(dev.handle), "capture_begin")
+            call(y)
+            g = ctypes.c_void_p()
+            nat.check(L.aih_capture_end(dev.handle, ctypes.byref(g)), "capture_end")
+            return g.value
+
+        def read(y):
+            return y.read_range(0, batch * n, np.float32).reshape(batch, n)
+
+        g1 = capture(ya)                      # workspace empty: one split
+        outs = []
+        for _ in range(3):
+            nat.check(L.aih_memset(dev.handle, ya.get_pointer(), 0xFF, batch * n * 4), "memset")
+            nat.check(L.aih_graph_launch(dev.handle, g1), "graph_launch")
+            outs.append(read(ya))
+            call(yb)                          # eager work between replays (sizes the workspace)
+            dev.synchronize()
+        for o in outs:
+            assert_close(o, ref, TOL, "one-split graph")
+            assert np.array_equal(o, outs[0])
+        eager = read(yb)
+        assert_close(eager, ref, TOL, "split path")
+        g2 = capture(ya)                      # workspace sized: split path in the graph
+        for _ in range(3):
+            nat.check(L.aih_memset(dev.handle, ya.get_pointer(), 0xFF, batch * n * 4), "memset")
+            nat.check(L.aih_graph_launch(dev.handle, g2), "graph_launch")
+            assert np.array_equal(read(ya), eager)
+            call(yb)
+            dev.synchronize()
+        # the first graph still runs after the workspace grew
+        nat.check(L.aih_graph_launch(dev.handle, g1), "graph_launch")
+        assert np.array_equal(read(ya), outs[0])
+        L.aih_graph_destroy(g1)
+        L.aih_graph_destroy(g2)
+    finally:
+        for b in bufs:
+            b.dispose()
+        dev.dispose()
 
 
 def test_padded_strides_leave_gaps_untouched(device, orc):

@@ -440,9 +440,10 @@ int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t row_byt
     if (ntiles > 0x7FFFFFFF || nunits > 0x7FFFFFFF) return AIH_E_LIMIT;
     // buffer resources: a tile's rows and all of X within 31-bit offsets
     if (RWG * row_bytes > 0x7FFFFFFF || ((int64_t)(batch - 1) * ldx + K) * 4 > 0x7FFFFFFF) return AIH_E_LIMIT;
-    // Splits: about four resident workgroups per CU (four waves each).
+    // Splits: about two workgroups per CU (four waves each); measured within a
+    // few per cent of one, four and eight per CU at the benchmark shapes.
     const int64_t cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
-    int64_t S = std::min<int64_t>(nunits, std::max<int64_t>(1, (4 * cu + ntiles - 1) / ntiles));
+    int64_t S = std::min<int64_t>(nunits, std::max<int64_t>(1, (2 * cu + ntiles - 1) / ntiles));
     int64_t per = (nunits + S - 1) / S;
     S = (nunits + per - 1) / per;
     const int64_t np = ntiles * RWG;

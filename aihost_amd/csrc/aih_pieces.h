@@ -40,6 +40,39 @@ __device__ __forceinline__ uint32_t byte_of(const u4 &v, int j)
     return (w >> (8 * (j & 3))) & 0xFFu;
 }
 
+// fp16 pair (1024 + c0, 1024 + c1) from code bytes 0, 1 (lo) or 2, 3 (hi) of
+// c: a code byte under the exponent byte 0x64 is the fp16 value 1024 + code.
+__device__ __forceinline__ uint32_t magic_lo(uint32_t c)
+{
+    return __builtin_amdgcn_perm(0x64646464u, c, 0x04010400u);
+}
+__device__ __forceinline__ uint32_t magic_hi(uint32_t c)
+{
+    return __builtin_amdgcn_perm(0x64646464u, c, 0x04030402u);
+}
+
+// Two weights (1024 + c) * s - cst from such a pair, computed in fp32 (one
+// v_fma_mix_f32 each) and rounded to fp16 as a pair (v_cvt_pk_f16_f32).  The
+// empty asm keeps the compiler from fusing them into v_fma_mixlo/mixhi, which
+// issue at half rate on gfx950.  Rounding cst = 1024 s + m to fp32 moves a
+// weight by at most 2^-24 * 1056 * |s| + 2^-24 |m|, far below its fp16 rounding.
+__device__ __forceinline__ uint32_t weights2(uint32_t p, float s, float cst)
+{
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const h2 h = __builtin_bit_cast(h2, p);
+    float a = __builtin_fmaf((float)h.x, s, -cst), b = __builtin_fmaf((float)h.y, s, -cst);
+    asm("" : "+v"(a), "+v"(b));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, h2));
+}
+
+// Eight weights from the code bytes of w0, then w1, in order.
+__device__ __forceinline__ h8 weights8(uint32_t w0, uint32_t w1, float s, float cst)
+{
+    const u4 r = {weights2(magic_lo(w0), s, cst), weights2(magic_hi(w0), s, cst),
+                  weights2(magic_lo(w1), s, cst), weights2(magic_hi(w1), s, cst)};
+    return __builtin_bit_cast(h8, r);
+}
+
 // Q4_K: chunk c is 64-group g = c % 4 of block c / 4; elements 0..31 of the
 // group are the low nibbles of qs[32g .. 32g+31] (sub-block 2g), elements
 // 32..63 the high nibbles (sub-block 2g+1) (ComputeOps.cs:1642-1675).
@@ -75,44 +108,24 @@ struct G4K {
             y[j] = D * (float)q - Mn;
         }
     }
-    // The same 16 weights as fp16, in about 1.5 instructions per weight: a
-    // nibble OR-ed into the mantissa of 0x6400 is the fp16 value 1024 + q
-    // (1024 + 16q for a high nibble left in place), and one fused fp32
-    // multiply-add with fp16 output gives code * D' - (1024 * D' + Mn), with
-    // D' = D (D / 16 for a high nibble).  Rounding the constant to fp32 moves
-    // a weight by at most 2^-24 * 1024 * D', far below its fp16 rounding.
+    // The same 16 weights as fp16: a nibble under 0x64 is 1024 + q (a high
+    // nibble left in place is 1024 + 16q, with the scale divided by 16), and
+    // (1024 + q) * D - (1024 D + Mn) = D q - Mn.  The scale and min of
+    // sub-block j come from shifted header words (get_scale_min_k4 without
+    // per-lane byte selects).
     __device__ static void piece_h(const Raw &r, int c, int s, h8 &lo, h8 &hi8)
     {
         const int hi = s >> 1;
-        const int sb = 2 * (c & 3) + hi;
-        uint32_t sc, mn;
-        if (sb < 4) {
-            sc = byte_of(r.hdr, 4 + sb) & 63u;
-            mn = byte_of(r.hdr, 8 + sb) & 63u;
-        } else {
-            sc = (byte_of(r.hdr, 8 + sb) & 0xFu) | ((byte_of(r.hdr, sb) >> 6) << 4);
-            mn = (byte_of(r.hdr, 8 + sb) >> 4) | ((byte_of(r.hdr, 4 + sb) >> 6) << 4);
-        }
+        const int j = 2 * (c & 3) + hi, sh = 8 * (j & 3);
+        const uint32_t a = r.hdr.y >> sh, b = r.hdr.z >> sh, w = r.hdr.w >> sh;
+        const uint32_t sc = j < 4 ? (a & 63u) : ((w & 0xFu) | ((a >> 2) & 0x30u));
+        const uint32_t mn = j < 4 ? (b & 63u) : (((w >> 4) & 0xFu) | ((b >> 2) & 0x30u));
         const float D = f16_bits(r.hdr.x) * (float)sc, Mn = f16_bits(r.hdr.x >> 16) * (float)mn;
         const float Dp = hi ? D * 0.0625f : D;
         const float C = 1024.f * Dp + Mn;
-        const uint32_t mask = hi ? 0x00F000F0u : 0x000F000Fu;
-        const uint32_t w[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
-        _Float16 y[16];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const h2 a = __builtin_bit_cast(h2, (w[i] & mask) | 0x64006400u);
-            const h2 b = __builtin_bit_cast(h2, ((w[i] >> 8) & mask) | 0x64006400u);
-            y[4 * i + 0] = (_Float16)__builtin_fmaf((float)a.x, Dp, -C);
-            y[4 * i + 2] = (_Float16)__builtin_fmaf((float)a.y, Dp, -C);
-            y[4 * i + 1] = (_Float16)__builtin_fmaf((float)b.x, Dp, -C);
-            y[4 * i + 3] = (_Float16)__builtin_fmaf((float)b.y, Dp, -C);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            lo[j] = y[j];
-            hi8[j] = y[8 + j];
-        }
+        const uint32_t m = hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+        lo = weights8(r.qs.x & m, r.qs.y & m, Dp, C);
+        hi8 = weights8(r.qs.z & m, r.qs.w & m, Dp, C);
     }
 };
 
@@ -143,10 +156,8 @@ struct G6K {
             y[j] = ds * (float)((int)(lo | (hi << 4)) - 32);
         }
     }
-    // fp16 path: the 6-bit code (nibble | 2 high bits << 4) OR-ed into the
-    // mantissa of 0x6400 is the fp16 value 1024 + q, and one fused fp32
-    // multiply-add with fp16 output gives code * ds - 1056 * ds = ds * (q - 32)
-    // (the constant's fp32 rounding moves a weight by at most 2^-24 * 1056 * ds).
+    // fp16 path: the 6-bit code (nibble | 2 high bits << 4) under 0x64 is
+    // 1024 + q, and (1024 + q) * ds - 1056 * ds = ds * (q - 32).
     __device__ static void piece_h(const Raw &r, int c, int s, h8 &lo, h8 &hi8)
     {
         const int Q = 2 * (c & 1) + (s >> 1);
@@ -155,25 +166,11 @@ struct G6K {
         const int ls = 4 * (Q >> 1), hs = 2 * Q;
         const uint32_t l[4] = {r.ql.x, r.ql.y, r.ql.z, r.ql.w};
         const uint32_t hb[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
-        _Float16 y[16];
+        uint32_t q[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            // the four 6-bit codes of bytes 0..3, one per byte, then split
-            // into the pairs (0, 2) and (1, 3)
-            const uint32_t q4 = ((l[i] >> ls) & 0x0F0F0F0Fu) | (((hb[i] >> hs) & 0x03030303u) << 4);
-            const uint32_t ca = (q4 & 0x00FF00FFu) | 0x64006400u;
-            const uint32_t cb = ((q4 >> 8) & 0x00FF00FFu) | 0x64006400u;
-            const h2 a = __builtin_bit_cast(h2, ca), b = __builtin_bit_cast(h2, cb);
-            y[4 * i + 0] = (_Float16)__builtin_fmaf((float)a.x, ds, -C);
-            y[4 * i + 2] = (_Float16)__builtin_fmaf((float)a.y, ds, -C);
-            y[4 * i + 1] = (_Float16)__builtin_fmaf((float)b.x, ds, -C);
-            y[4 * i + 3] = (_Float16)__builtin_fmaf((float)b.y, ds, -C);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            lo[j] = y[j];
-            hi8[j] = y[8 + j];
-        }
+        for (int i = 0; i < 4; ++i) q[i] = ((l[i] >> ls) & 0x0F0F0F0Fu) | (((hb[i] >> hs) << 4) & 0x30303030u);
+        lo = weights8(q[0], q[1], ds, C);
+        hi8 = weights8(q[2], q[3], ds, C);
     }
 };
 
@@ -194,29 +191,13 @@ struct G80 {
         for (int j = 0; j < 16; ++j)
             y[j] = f16_bits(r.d) * (float)(int)__builtin_amdgcn_sbfe((int)w[j >> 2], 8 * (j & 3), 8);
     }
-    // fp16 path: a code byte biased by 128 (xor 0x80) in the mantissa of
-    // 0x6400 is 1024 + q + 128; one fused fp32 multiply-add with fp16 output
-    // gives code * d - 1152 * d = d * q.
+    // fp16 path: a code byte biased by 128 (xor 0x80) under 0x64 is
+    // 1024 + 128 + q, and (1152 + q) * d - 1152 * d = d * q.
     __device__ static void piece_h(const Raw &r, int, int, h8 &lo, h8 &hi8)
     {
         const float d = f16_bits(r.d), C = 1152.f * d;
-        const uint32_t w[4] = {r.qs.x ^ 0x80808080u, r.qs.y ^ 0x80808080u, r.qs.z ^ 0x80808080u,
-                               r.qs.w ^ 0x80808080u};
-        _Float16 y[16];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const h2 a = __builtin_bit_cast(h2, (w[i] & 0x00FF00FFu) | 0x64006400u);
-            const h2 b = __builtin_bit_cast(h2, ((w[i] >> 8) & 0x00FF00FFu) | 0x64006400u);
-            y[4 * i + 0] = (_Float16)__builtin_fmaf((float)a.x, d, -C);
-            y[4 * i + 2] = (_Float16)__builtin_fmaf((float)a.y, d, -C);
-            y[4 * i + 1] = (_Float16)__builtin_fmaf((float)b.x, d, -C);
-            y[4 * i + 3] = (_Float16)__builtin_fmaf((float)b.y, d, -C);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            lo[j] = y[j];
-            hi8[j] = y[8 + j];
-        }
+        lo = weights8(r.qs.x ^ 0x80808080u, r.qs.y ^ 0x80808080u, d, C);
+        hi8 = weights8(r.qs.z ^ 0x80808080u, r.qs.w ^ 0x80808080u, d, C);
     }
 };
 
@@ -240,31 +221,17 @@ struct G40 {
             y[j] = f16_bits(r.d) * (float)((int)q - 8);
         }
     }
-    // fp16 path as for Q4_K: a nibble in the mantissa of 0x6400 is 1024 + q
-    // (1024 + 16q for a high nibble left in place, with d' = d / 16), and one
-    // fused fp32 multiply-add with fp16 output gives code * d' - (1024 d' + 8 d).
+    // fp16 path as for Q4_K: a nibble under 0x64 is 1024 + q (1024 + 16q for
+    // a high nibble left in place, with d' = d / 16), and
+    // (1024 + q) * d' - (1024 d' + 8 d) = d' q - 8 d.
     __device__ static void piece_h(const Raw &r, int, int s, h8 &lo, h8 &hi8)
     {
         const float d = f16_bits(r.d);
         const float Dp = (s & 1) ? d * 0.0625f : d;
         const float C = 1024.f * Dp + 8.f * d;
-        const uint32_t mask = (s & 1) ? 0x00F000F0u : 0x000F000Fu;
-        const uint32_t w[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
-        _Float16 y[16];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const h2 a = __builtin_bit_cast(h2, (w[i] & mask) | 0x64006400u);
-            const h2 b = __builtin_bit_cast(h2, ((w[i] >> 8) & mask) | 0x64006400u);
-            y[4 * i + 0] = (_Float16)__builtin_fmaf((float)a.x, Dp, -C);
-            y[4 * i + 2] = (_Float16)__builtin_fmaf((float)a.y, Dp, -C);
-            y[4 * i + 1] = (_Float16)__builtin_fmaf((float)b.x, Dp, -C);
-            y[4 * i + 3] = (_Float16)__builtin_fmaf((float)b.y, Dp, -C);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            lo[j] = y[j];
-            hi8[j] = y[8 + j];
-        }
+        const uint32_t m = (s & 1) ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+        lo = weights8(r.qs.x & m, r.qs.y & m, Dp, C);
+        hi8 = weights8(r.qs.z & m, r.qs.w & m, Dp, C);
     }
 };
 

@@ -120,6 +120,9 @@ qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
 #pragma unroll
             for (int i = 0; i < 4; ++i) T::load(wrow[i], c, ps, r[i]);
         };
+        // chunks past K exist only in a last, partial super-step; they are
+        // staged as zeros
+        const int tail_ss = nch % SC ? nss - 1 : nss;
         auto stage = [&](int ss, int buf, const typename T::Raw *r) {
             asm volatile("" : "+s"(ss));
             const int c = ss * SC + pc;
@@ -127,7 +130,7 @@ qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
             for (int i = 0; i < 4; ++i) {
                 h8 lo, hi;
                 piece16h<T>(r[i], c, ps, lo, hi);
-                if (c >= nch) lo = hi = h8{};
+                if (ss == tail_ss && c >= nch) lo = hi = h8{};
                 _Float16 *d = &wsh[buf][16 * pw + 4 * i + rl][64 * pc + 16 * ps];
                 *reinterpret_cast<h8 *>(d) = lo;
                 *reinterpret_cast<h8 *>(d + 8) = hi;

@@ -32,13 +32,12 @@
 // kernel adds the splits in a fixed order (the result does not depend on
 // timing).  With one split the first kernel stores Y itself.
 //
-// Dequantization.  A code byte c placed under the exponent byte 0x64 is the
-// fp16 value 1024 + c (v_perm_b32 builds two such halves from two bytes), and
-// one fused fp32 multiply-add with fp16 output (v_fma_mix) gives
+// Dequantization (aih_pieces.h weights8).  A code byte c placed under the
+// exponent byte 0x64 is the fp16 value 1024 + c (v_perm_b32 builds two such
+// halves from two bytes); one fp32 multiply-add each (v_fma_mix_f32) gives
 // (1024 + c) * s - (1024 * s + m) = c * s - m with the reference's scale s and
-// offset m (ComputeOps.cs:1629-1678 Q4_K, :1735-1774 Q6_K; GGUF Q8_0/Q4_0).
-// Rounding the constant to fp32 moves a weight by at most 2^-24 * 1056 * s,
-// far below its fp16 rounding.
+// offset m (ComputeOps.cs:1629-1678 Q4_K, :1735-1774 Q6_K; GGUF Q8_0/Q4_0),
+// rounded to fp16 in pairs (v_cvt_pk_f16_f32).
 //
 // This replaces TempF32 + ComputeOps.MatMulWeights for M = batch in 3..8
 // (AIHost/AIHost/Compute/TransformerBase.cs:254-271, ComputeOps.cs:275-309).
@@ -53,33 +52,6 @@ constexpr int TW = 4;            // waves per workgroup
 constexpr int RWG = 16 * TW;     // weight rows per workgroup
 constexpr int UNIT = 256;        // k per unit
 constexpr int MAXB = 8;          // batch columns
-
-// Bytes 0, 1 (lo) or 2, 3 (hi) of c as the fp16 pair (1024 + c0, 1024 + c1).
-__device__ __forceinline__ uint32_t pair_lo(uint32_t c)
-{
-    return __builtin_amdgcn_perm(0x64646464u, c, 0x04010400u);
-}
-__device__ __forceinline__ uint32_t pair_hi(uint32_t c)
-{
-    return __builtin_amdgcn_perm(0x64646464u, c, 0x04030402u);
-}
-
-// Eight fp16 weights c_j * s - m from the code bytes of w0, then w1, in
-// order: (1024 + c) * s - cst with cst = 1024 s + m in fp32 (v_fma_mix), then
-// rounded to fp16 in pairs.  (A v_fma_mixlo/mixhi pair writes the halves
-// directly but issues at half rate.)
-__device__ __forceinline__ h8 frag8(uint32_t w0, uint32_t w1, float s, float cst)
-{
-    const uint32_t p[4] = {pair_lo(w0), pair_hi(w0), pair_lo(w1), pair_hi(w1)};
-    h8 a;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const h2 h = __builtin_bit_cast(h2, p[j]);
-        a[2 * j] = (_Float16)__builtin_fmaf((float)h.x, s, -cst);
-        a[2 * j + 1] = (_Float16)__builtin_fmaf((float)h.y, s, -cst);
-    }
-    return a;
-}
 
 // Weights are read with buffer loads from a resource over the workgroup's 64
 // rows: a lane's byte offsets are set up once (Lane), a unit's offset is the
@@ -143,8 +115,8 @@ struct UQ4K {
         const uint32_t w[8] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w, r.qb.x, r.qb.y, r.qb.z, r.qb.w};
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-            a[m] = frag8(w[2 * m] & 0x0F0F0F0Fu, w[2 * m + 1] & 0x0F0F0F0Fu, s0, c0);
-            a[m + 4] = frag8(w[2 * m] & 0xF0F0F0F0u, w[2 * m + 1] & 0xF0F0F0F0u, s1, c1);
+            a[m] = weights8(w[2 * m] & 0x0F0F0F0Fu, w[2 * m + 1] & 0x0F0F0F0Fu, s0, c0);
+            a[m + 4] = weights8(w[2 * m] & 0xF0F0F0F0u, w[2 * m + 1] & 0xF0F0F0F0u, s1, c1);
         }
     }
 };
@@ -196,8 +168,8 @@ struct UQ6K {
         const int sb = (int)(int8_t)(uint8_t)(sw >> (8 * (2 * (Q & 1) + t)));
         const float ds = d * (float)sb, cst = 1056.f * ds;
         const u4 &l = (Q & 1) ? r.lb : r.la;
-        a[2 * Q] = frag8(codes<Q>(l.x, r.qh.x), codes<Q>(l.y, r.qh.y), ds, cst);
-        a[2 * Q + 1] = frag8(codes<Q>(l.z, r.qh.z), codes<Q>(l.w, r.qh.w), ds, cst);
+        a[2 * Q] = weights8(codes<Q>(l.x, r.qh.x), codes<Q>(l.y, r.qh.y), ds, cst);
+        a[2 * Q + 1] = weights8(codes<Q>(l.z, r.qh.z), codes<Q>(l.w, r.qh.w), ds, cst);
     }
     __device__ static void frags(const Raw &r, int q, h8 *a)
     {
@@ -238,8 +210,8 @@ struct UQ80 {
         const uint32_t v[8] = {r.q1a.x, r.q1a.y, r.q1a.z, r.q1a.w, r.q1b.x, r.q1b.y, r.q1b.z, r.q1b.w};
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-            a[m] = frag8(w[2 * m] ^ 0x80808080u, w[2 * m + 1] ^ 0x80808080u, d0, 1152.f * d0);
-            a[m + 4] = frag8(v[2 * m] ^ 0x80808080u, v[2 * m + 1] ^ 0x80808080u, d1, 1152.f * d1);
+            a[m] = weights8(w[2 * m] ^ 0x80808080u, w[2 * m + 1] ^ 0x80808080u, d0, 1152.f * d0);
+            a[m + 4] = weights8(v[2 * m] ^ 0x80808080u, v[2 * m + 1] ^ 0x80808080u, d1, 1152.f * d1);
         }
     }
 };
@@ -270,10 +242,10 @@ struct UQ40 {
         for (int b = 0; b < 2; ++b) {
             const float d = dd[b], dh = d * 0.0625f;
             const uint32_t w[4] = {qq[b].x, qq[b].y, qq[b].z, qq[b].w};
-            a[4 * b + 0] = frag8(w[0] & 0x0F0F0F0Fu, w[1] & 0x0F0F0F0Fu, d, 1024.f * d + 8.f * d);
-            a[4 * b + 1] = frag8(w[2] & 0x0F0F0F0Fu, w[3] & 0x0F0F0F0Fu, d, 1024.f * d + 8.f * d);
-            a[4 * b + 2] = frag8(w[0] & 0xF0F0F0F0u, w[1] & 0xF0F0F0F0u, dh, 1024.f * dh + 8.f * d);
-            a[4 * b + 3] = frag8(w[2] & 0xF0F0F0F0u, w[3] & 0xF0F0F0F0u, dh, 1024.f * dh + 8.f * d);
+            a[4 * b + 0] = weights8(w[0] & 0x0F0F0F0Fu, w[1] & 0x0F0F0F0Fu, d, 1024.f * d + 8.f * d);
+            a[4 * b + 1] = weights8(w[2] & 0x0F0F0F0Fu, w[3] & 0x0F0F0F0Fu, d, 1024.f * d + 8.f * d);
+            a[4 * b + 2] = weights8(w[0] & 0xF0F0F0F0u, w[1] & 0xF0F0F0F0u, dh, 1024.f * dh + 8.f * d);
+            a[4 * b + 3] = weights8(w[2] & 0xF0F0F0F0u, w[3] & 0xF0F0F0F0u, dh, 1024.f * dh + 8.f * d);
         }
     }
 };

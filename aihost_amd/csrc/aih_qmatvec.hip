@@ -489,6 +489,14 @@ struct Fuse {
 
 __device__ __forceinline__ float silu_f(float g) { return g * (1.0f / (1.0f + expf(-g))); }
 
+// Workgroup barrier for LDS data only: waits for this wave's LDS operations,
+// then for every wave.  __syncthreads() also waits for every global load in
+// flight (s_waitcnt vmcnt(0)), which would drain the weight prefetch.
+__device__ __forceinline__ void lds_barrier()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // A workgroup is TEAMS row teams of geo.wr waves (ONEWAVE: geo.wr == 1).
 // Team t of workgroup w visits the row groups c = w, w + gridDim.x, ... and
 // computes row c*TEAMS + t of each.
@@ -628,7 +636,7 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
             for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o);
             if (lane == 0) red[wave][b] = t;
         }
-        __syncthreads();
+        lds_barrier();
         const int nw = (int)(blockDim.x >> 6);
         float rms[B];
 #pragma unroll
@@ -691,7 +699,7 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
                 sums[(b * 16 + ps) * tp + pu] = sum;
             }
         }
-        __syncthreads();
+        lds_barrier();
         xa.grp = reinterpret_cast<const u4 *>(xs) + ut;
         xa.tt = tp;
 #pragma unroll

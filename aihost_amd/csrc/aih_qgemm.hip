@@ -181,13 +181,22 @@ qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
         for (int kk = 0; kk < 4; ++kk) f.a[kk] = ldg<h8>(xa + ((int64_t)kb * 4 + kk) * 512);
     };
     f16v acc0 = {}, acc1 = {};
-    auto mm = [&](int buf, int t, const AF &f) {
+    // B fragments of one 64-k step (both 32-column halves, four k16 slices),
+    // read from LDS one step ahead of their MFMAs so that the reads' latency
+    // is covered by the previous step's matrix work
+    struct BF { h8 b0[4], b1[4]; };
+    auto bload = [&](int buf, int t, BF &b) {
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-            const h8 b0 = *reinterpret_cast<const h8 *>(&wsh[buf][fr][64 * t + 16 * kk + fk]);
-            const h8 b1 = *reinterpret_cast<const h8 *>(&wsh[buf][32 + fr][64 * t + 16 * kk + fk]);
-            acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[kk], b0, acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[kk], b1, acc1, 0, 0, 0);
+            b.b0[kk] = *reinterpret_cast<const h8 *>(&wsh[buf][fr][64 * t + 16 * kk + fk]);
+            b.b1[kk] = *reinterpret_cast<const h8 *>(&wsh[buf][32 + fr][64 * t + 16 * kk + fk]);
+        }
+    };
+    auto mm = [&](const AF &f, const BF &b) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[kk], b.b0[kk], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[kk], b.b1[kk], acc1, 0, 0, 0);
         }
     };
     // A ring of one super-step: slot t holds 64-k step SC*ss + t
@@ -196,20 +205,29 @@ qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
     for (int t = 0; t < SC; ++t) aload(t, f[t]);
     __builtin_amdgcn_sched_barrier(0);
     lds_barrier();
+    BF bb[2];
     int ss = 0;
     for (; ss + 2 <= nss; ++ss) {
         const int buf = ss & 1;
+        bload(buf, 0, bb[0]);
 #pragma unroll
         for (int t = 0; t < SC; ++t) {
-            mm(buf, t, f[t]);
+            if (t + 1 < SC) bload(buf, t + 1, bb[(t + 1) & 1]);
+            mm(f[t], bb[t & 1]);
             aload(SC * (ss + 1) + t, f[t]);
             __builtin_amdgcn_sched_barrier(0);
         }
         lds_barrier();
     }
+    {
+        const int buf = ss & 1;
+        bload(buf, 0, bb[0]);
 #pragma unroll
-    for (int t = 0; t < SC; ++t)
-        if (SC * ss + t < nch) mm(ss & 1, t, f[t]);
+        for (int t = 0; t < SC; ++t) {
+            if (t + 1 < SC && SC * ss + t + 1 < nch) bload(buf, t + 1, bb[(t + 1) & 1]);
+            if (SC * ss + t < nch) mm(f[t], bb[t & 1]);
+        }
+    }
 
     const int64_t na = n0 + fr, nb = n0 + 32 + fr;
 #pragma unroll

@@ -55,7 +55,9 @@ constexpr int MAXB = 8;          // batch columns
 
 // Weights are read with buffer loads from a resource over the workgroup's 64
 // rows: a lane's byte offsets are set up once (Lane), a unit's offset is the
-// scalar `so` plus an immediate.  Reads past the resource return zero.
+// scalar `so`.  Every weight read stays inside its row; only activation
+// chunks that are not needed are given offsets past the resource (which read
+// as zero).
 typedef __amdgpu_buffer_rsrc_t Rsrc;
 __device__ __forceinline__ Rsrc make_rsrc(const void *base, uint32_t bytes)
 {
@@ -187,20 +189,20 @@ struct UQ6K {
 // (xor 0x80) gives (1024 + 128 + q) * d - 1152 * d.
 struct UQ80 {
     static constexpr int kBytes = 272, kBlocks = 8, kBlockElems = 32;
-    struct Lane { uint32_t b; };
+    struct Lane { uint32_t row, b; };
     struct Raw { u4 q0a, q0b, q1a, q1b; uint32_t d0, d1; };
-    __device__ static Lane lane(uint32_t rowoff, int q) { return {rowoff + 68 * (uint32_t)q}; }
+    __device__ static Lane lane(uint32_t rowoff, int q) { return {rowoff, rowoff + 68 * (uint32_t)q}; }
     __device__ static void load(Rsrc r, const Lane &L, uint32_t so, int q, int nb, Raw &w)
     {
-        w.q0a = bld16(r, L.b + 2, so);
-        w.q0b = bld16(r, L.b + 18, so);
-        w.q1a = bld16(r, L.b + 36, so);
-        w.q1b = bld16(r, L.b + 52, so);
-        w.d0 = bld2(r, L.b, so);
-        w.d1 = bld2(r, L.b + 34, so);
-        // blocks past the row's end (only in a last, partial unit) get scale 0
-        if (2 * q >= nb) w.d0 = 0u;
-        if (2 * q + 1 >= nb) w.d1 = 0u;
+        // a block past the row's end (only in a last, partial unit) re-reads
+        // block 0 of the unit, so no read leaves the row, and gets scale 0
+        const uint32_t o0 = 2 * q < nb ? L.b : L.row, o1 = 2 * q + 1 < nb ? L.b + 34 : L.row;
+        w.q0a = bld16(r, o0 + 2, so);
+        w.q0b = bld16(r, o0 + 18, so);
+        w.q1a = bld16(r, o1 + 2, so);
+        w.q1b = bld16(r, o1 + 18, so);
+        w.d0 = 2 * q < nb ? bld2(r, o0, so) : 0u;
+        w.d1 = 2 * q + 1 < nb ? bld2(r, o1, so) : 0u;
     }
     __device__ static int xoff(int q, int m) { return 64 * q + 8 * m; }
     __device__ static void frags(const Raw &r, int, h8 *a)
@@ -221,17 +223,16 @@ struct UQ80 {
 // nibbles; y = d * (q - 8).
 struct UQ40 {
     static constexpr int kBytes = 144, kBlocks = 8, kBlockElems = 32;
-    struct Lane { uint32_t b; };
+    struct Lane { uint32_t row, b; };
     struct Raw { u4 q0, q1; uint32_t d0, d1; };
-    __device__ static Lane lane(uint32_t rowoff, int q) { return {rowoff + 36 * (uint32_t)q}; }
+    __device__ static Lane lane(uint32_t rowoff, int q) { return {rowoff, rowoff + 36 * (uint32_t)q}; }
     __device__ static void load(Rsrc r, const Lane &L, uint32_t so, int q, int nb, Raw &w)
     {
-        w.q0 = bld16(r, L.b + 2, so);
-        w.q1 = bld16(r, L.b + 20, so);
-        w.d0 = bld2(r, L.b, so);
-        w.d1 = bld2(r, L.b + 18, so);
-        if (2 * q >= nb) w.d0 = 0u;
-        if (2 * q + 1 >= nb) w.d1 = 0u;
+        const uint32_t o0 = 2 * q < nb ? L.b : L.row, o1 = 2 * q + 1 < nb ? L.b + 18 : L.row;
+        w.q0 = bld16(r, o0 + 2, so);
+        w.q1 = bld16(r, o1 + 2, so);
+        w.d0 = 2 * q < nb ? bld2(r, o0, so) : 0u;
+        w.d1 = 2 * q + 1 < nb ? bld2(r, o1, so) : 0u;
     }
     __device__ static int xoff(int q, int m) { return 64 * q + 8 * m; }
     __device__ static void frags(const Raw &r, int, h8 *a)

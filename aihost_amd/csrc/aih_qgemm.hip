@@ -24,6 +24,8 @@
 // multiply-add per weight with fp16 output (aih_pieces.h).
 #include "aih_pieces.h"
 
+#include <type_traits>
+
 namespace {
 
 using namespace aih_pieces;
@@ -120,17 +122,16 @@ qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
 #pragma unroll
             for (int i = 0; i < 4; ++i) T::load(wrow[i], c, ps, r[i]);
         };
-        // chunks past K exist only in a last, partial super-step; they are
-        // staged as zeros
-        const int tail_ss = nch % SC ? nss - 1 : nss;
-        auto stage = [&](int ss, int buf, const typename T::Raw *r) {
+        // chunks past K exist only in a last, partial super-step, staged as
+        // zeros: only the stages after the main loop test for them
+        auto stage = [&](auto tail, int ss, int buf, const typename T::Raw *r) {
             asm volatile("" : "+s"(ss));
             const int c = ss * SC + pc;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 h8 lo, hi;
                 piece16h<T>(r[i], c, ps, lo, hi);
-                if (ss == tail_ss && c >= nch) lo = hi = h8{};
+                if (decltype(tail)::value && c >= nch) lo = hi = h8{};
                 _Float16 *d = &wsh[buf][16 * pw + 4 * i + rl][64 * pc + 16 * ps];
                 *reinterpret_cast<h8 *>(d) = lo;
                 *reinterpret_cast<h8 *>(d + 8) = hi;
@@ -144,7 +145,7 @@ qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
         for (; ss + 2 * PR <= nss; ss += PR) {
 #pragma unroll
             for (int j = 0; j < PR; ++j) {
-                stage(ss + j, (ss + j) & 1, ring[j]);
+                stage(std::false_type{}, ss + j, (ss + j) & 1, ring[j]);
                 gload(ss + j + PR, ring[j]);
                 __builtin_amdgcn_sched_barrier(0);
                 lds_barrier();
@@ -153,7 +154,7 @@ qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
 #pragma unroll
         for (int j = 0; j < PR; ++j) {
             if (ss + j < nss) {
-                stage(ss + j, (ss + j) & 1, ring[j]);
+                stage(std::true_type{}, ss + j, (ss + j) & 1, ring[j]);
                 if (ss + j + PR < nss) gload(ss + j + PR, ring[j]);
                 lds_barrier();
             }
@@ -161,7 +162,7 @@ qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
 #pragma unroll
         for (int j = 0; j < PR; ++j) {
             if (ss + PR + j < nss) {
-                stage(ss + PR + j, (ss + PR + j) & 1, ring[j]);
+                stage(std::true_type{}, ss + PR + j, (ss + PR + j) & 1, ring[j]);
                 lds_barrier();
             }
         }

@@ -55,9 +55,8 @@ constexpr int MAXB = 8;          // batch columns
 
 // Weights are read with buffer loads from a resource over the workgroup's 64
 // rows: a lane's byte offsets are set up once (Lane), a unit's offset is the
-// scalar `so`.  Every weight read stays inside its row; only activation
-// chunks that are not needed are given offsets past the resource (which read
-// as zero).
+// scalar `so`.  Every weight read stays inside its row, and activation chunks
+// outside the batch or K are not loaded.
 typedef __amdgpu_buffer_rsrc_t Rsrc;
 __device__ __forceinline__ Rsrc make_rsrc(const void *base, uint32_t bytes)
 {

@@ -153,7 +153,8 @@ def test_padded_strides_leave_gaps_untouched(device, orc):
     assert np.all(np.isnan(y[:, n:]))  # memset 0xFF pattern untouched
 
 
-def test_subnormal_and_extreme_scales(device, orc):
+@pytest.mark.parametrize("batch", [2, 5])   # dot2 kernel (fp32 scales), MFMA kernel (fp16 weights)
+def test_subnormal_and_extreme_scales(device, orc, batch):
     # random bytes with small finite scales: exercises every code value
     rng = np.random.default_rng(5)
     n, k = 64, 1024
@@ -165,9 +166,9 @@ def test_subnormal_and_extreme_scales(device, orc):
             h = rng.integers(0x0001, 0x2400, nb).astype(np.uint16)   # subnormal .. 2^-6
             data[:, off:off + 2] = h.view(np.uint8).reshape(nb, 2)
         data = data.reshape(-1)
-        x = x_of(k, 2, seed=qtype)
+        x = x_of(k, batch, seed=qtype)
         assert_close(qmatvec(device, qtype, data, n, k, x), orc.matvec(qtype, data, n, k, x), TOL,
-                     "type %d" % qtype)
+                     "type %d batch %d" % (qtype, batch))
 
 
 @pytest.mark.parametrize("batch_path", [2, 3])   # dot2 kernel (1-2 columns), MFMA kernel (3-8)

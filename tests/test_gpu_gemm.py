@@ -36,6 +36,9 @@ def test_prefill_workload(device, orc):
     (nat.Q6_K, 64, 256, 128), (nat.Q6_K, 100, 768, 77), (nat.Q6_K, 130, 4096, 40),
     (nat.Q8_0, 64, 64, 128), (nat.Q8_0, 63, 320, 200), (nat.Q8_0, 257, 128, 17),
     (nat.Q4_0, 64, 64, 128), (nat.Q4_0, 99, 2048, 65), (nat.Q4_0, 5, 192, 130),
+    # 25 64-k chunks: full super-steps in the producers' main loop, a partial
+    # last one (one chunk) staged after it
+    (nat.Q8_0, 70, 1600, 40), (nat.Q4_0, 33, 1600, 100),
 ])
 def test_shapes(device, orc, qtype, n, k, m):
     w = synth_weight(qtype, n, k, seed=n * 7 + k)

@@ -188,6 +188,19 @@ def cpu_baseline(packed, x, n, k, seconds, threads=1):
     return reps, el
 
 
+def host_threads():
+    """Host threads for the multi-threaded CPU baseline: OMP_NUM_THREADS when
+    set (the share of host cores this process may use), else the CPUs in this
+    process's affinity mask; at most 16."""
+    try:
+        n = int(os.environ.get("OMP_NUM_THREADS", "0"))
+    except ValueError:
+        n = 0
+    if n <= 0:
+        n = len(os.sched_getaffinity(0))
+    return max(1, min(16, n))
+
+
 def decoder_bench(dev, distinct_layers, prompt=512, gen=128, cpu=True):
     """Full Llama decoder of the 8B shape (32 layers, hidden 4096, 32/8 heads
     of 128, FFN 14336, vocab 32000), Q4_K weights with a Q6_K head: prefill of
@@ -352,12 +365,18 @@ def main():
     if not args.no_decoder:
         decode = decoder_bench(dev, args.decoder_distinct_layers, cpu=not args.no_cpu_baseline)
 
-    cpu = None
+    cpu = cpu_mt = None
     if not args.no_cpu_baseline:
         reps, el = cpu_baseline(packed, x_host.reshape(1, k), n, k, args.cpu_seconds, threads=1)
         cpu = {"value": round(nbytes * reps / el / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
                "sample": "%d full passes of the 14336x4096 Q4_K batch-1 matvec (row dequant + sequential fp32 dot, "
                          "oracle/oracle.c -O2 -ffp-contract=off) in %.1f s, one thread" % (reps, el)}
+        # the same port with its rows split over the host cores (OpenMP, static schedule)
+        nt = host_threads()
+        reps, el = cpu_baseline(packed, x_host.reshape(1, k), n, k, args.cpu_seconds / 2, threads=nt)
+        cpu_mt = {"value": round(nbytes * reps / el / 1e9, 3), "unit": "GB/s", "cores": nt, "kind": "port",
+                  "sample": "%d full passes of the same matvec in %.1f s, rows split over %d OpenMP threads"
+                            % (reps, el, nt)}
     dev.dispose()
 
     out = {
@@ -381,6 +400,7 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel_us": round(ms_kernel * 1e3, 3), "bytes_per_launch": nbytes},
         "cpu_baseline": cpu,
+        "cpu_baseline_threads": cpu_mt,
         "decode": decode,
         "also": extra,
         "y_checksum": float(np.sum(y_check.astype(np.float64))),

@@ -502,11 +502,20 @@ __device__ __forceinline__ void lds_barrier()
 // computes row c*TEAMS + t of each.
 //
 // Software pipeline: the packed bytes of the team's first row are loaded
-// before the activation conversion and its second row right after; from then
-// on each of the two register buffers is reloaded with the row two ahead as
-// soon as its row is computed, so a wave always has one row of loads in
-// flight while it computes.  The loop is unrolled twice so that each buffer
-// keeps fixed registers.
+// before the activation conversion, or right after it where several teams of
+// several waves share x through LDS, and its second row once x is in
+// place; from then on each of the two register buffers is reloaded with the
+// row two ahead as soon as its row is computed, so a wave always has one row
+// of loads in flight while it computes.  The loop is unrolled twice so that
+// each buffer keeps fixed registers.
+//
+// Several teams of several waves read a wide x (16-64 KB; 57 KB at K = 14336)
+// that every workgroup fetches whole, which takes about two round trips of
+// the CU's outstanding misses.  Issued behind the weight rows of all 256
+// workgroups, those loads wait in a loaded memory system: on MI355X, loading
+// the first row after the conversion instead ran the Q6_K 4096 x 14336
+// product in 12.3-12.6 us instead of 13.0, and also loading the second row
+// before the conversion's barrier measured 13.0 again.
 //
 // Loads complete in issue order, so waiting for the current row leaves the
 // other buffer's loads in flight; the activation loads are issued first.
@@ -598,7 +607,7 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
     // re-reads the team's first row instead.
     const int ng = (int)ngroups, g = (int)gridDim.x, c0 = (int)blockIdx.x;
     uint32_t ra[T::kRaw], rb[T::kRaw];
-    load_group(c0, ra);
+    if constexpr (!SPREAD) load_group(c0, ra);
     // keep the weight loads here, in flight during the conversion below
     __builtin_amdgcn_sched_barrier(0);
 
@@ -698,6 +707,11 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
                 e[1] = p1;
                 sums[(b * 16 + ps) * tp + pu] = sum;
             }
+        }
+        if constexpr (SPREAD) {
+            // the first row, in flight during the barrier and the sums below
+            load_group(c0, ra);
+            __builtin_amdgcn_sched_barrier(0);
         }
         lds_barrier();
         xa.grp = reinterpret_cast<const u4 *>(xs) + ut;

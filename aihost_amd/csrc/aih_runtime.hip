@@ -58,7 +58,16 @@ int aih_workspace(aih_ctx *ctx, size_t bytes, void **out)
         (void)hipGetLastError();
         return (int)e;
     }
-    if (ctx->work) ctx->work_retired.push_back(ctx->work);
+    if (ctx->work) {
+        // kept until aih_destroy (graphs captured earlier hold its address);
+        // the list may allocate on the host: nothing may throw across the C ABI
+        try {
+            ctx->work_retired.push_back(ctx->work);
+        } catch (...) {
+            (void)hipFree(p);
+            return (int)hipErrorOutOfMemory;
+        }
+    }
     ctx->work = p;
     ctx->work_bytes = sz;
     *out = ctx->work;
@@ -147,9 +156,15 @@ int aih_malloc(aih_ctx *ctx, size_t bytes, void **dptr)
         (void)hipGetLastError();  // clear the sticky error so later calls are unaffected
         return (int)e;
     }
-    std::lock_guard<std::mutex> g(ctx->lock);
-    ctx->allocs[p] = bytes;
-    ctx->tracked_bytes += bytes;
+    // the table insert may allocate on the host: nothing may throw across the C ABI
+    try {
+        std::lock_guard<std::mutex> g(ctx->lock);
+        ctx->allocs[p] = bytes;
+        ctx->tracked_bytes += bytes;
+    } catch (...) {
+        (void)hipFree(p);
+        return (int)hipErrorOutOfMemory;
+    }
     *dptr = p;
     return AIH_OK;
 }

@@ -48,6 +48,12 @@ def test_benchmark_shapes(device, orc, qtype, n, k, batch):
     (nat.Q8_0, 19, 128, 1), (nat.Q8_0, 9, 64, 2), (nat.Q8_0, 8, 20480, 1), (nat.Q8_0, 5, 4160, 3),
     (nat.Q4_0, 5, 64, 1), (nat.Q4_0, 66, 2048, 2), (nat.Q4_0, 3, 32768, 1),
     (nat.Q4_K, 3, 65536, 1),
+    # batch 1-2, several teams of several waves sharing x through LDS (the
+    # first weight row is loaded after the conversion): four teams of two
+    # waves (K 4160..8192), two teams of three waves (K 12288), and an odd N
+    # whose last row goes to the single-team launch
+    (nat.Q4_K, 70, 8192, 1), (nat.Q6_K, 41, 6144, 2), (nat.Q4_0, 9, 5120, 1), (nat.Q8_0, 23, 12288, 2),
+    (nat.Q6_K, 51, 14336, 1),
     # batch 3..8 (matrix-core kernel): chunks per wave around the ring depth
     # (8 sets; 6 for Q6_K) -- tail only, one loop pass, exact multiples, a
     # shorter last wave

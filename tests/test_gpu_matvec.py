@@ -54,6 +54,10 @@ def test_benchmark_shapes(device, orc, qtype, n, k, batch):
     # whose last row goes to the single-team launch
     (nat.Q4_K, 70, 8192, 1), (nat.Q6_K, 41, 6144, 2), (nat.Q4_0, 9, 5120, 1), (nat.Q8_0, 23, 12288, 2),
     (nat.Q6_K, 51, 14336, 1),
+    # taller than one launch covers (at most 64 row groups per workgroup, one
+    # workgroup per CU: 131072 rows of eight-team workgroups on 256 CUs): a
+    # second launch at a row offset, then the odd rows' single-team launch
+    (nat.Q4_0, 131101, 256, 1), (nat.Q4_K, 131101, 256, 2),
     # batch 3..8 (matrix-core kernel): chunks per wave around the ring depth
     # (8 sets; 6 for Q6_K) -- tail only, one loop pass, exact multiples, a
     # shorter last wave

@@ -57,8 +57,10 @@ def _gpu_op(device, fn, *arrays, n):
             b.dispose()
 
 
+# the last shape is taller than one launch covers (131072 rows of eight-team
+# workgroups on 256 CUs), with five odd rows for the single-team launch
 SHAPES = [(nat.Q4_K, 6144, 4096), (nat.Q4_K, 4096, 14336), (nat.Q6_K, 32000, 4096), (nat.Q4_K, 8, 65536),
-          (nat.Q4_K, 4101, 4096), (nat.Q8_0, 1030, 4096)]
+          (nat.Q4_K, 4101, 4096), (nat.Q8_0, 1030, 4096), (nat.Q4_0, 131101, 256)]
 
 
 @pytest.mark.parametrize("qtype,n,k", SHAPES)

@@ -610,9 +610,12 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
     // permutation of w that gives each XCD a contiguous piece of every band
     // of g row groups (XCD x: groups x*g/8 .. (x+1)*g/8 - 1 of the band); on
     // MI355X that ran the 14336 x 4096 Q4_0 and the 4096 x 14336 Q4_K / Q6_K
-    // products about 3% faster than c0 = w.
+    // products about 3% faster than c0 = w.  The fused decode-step kernels
+    // keep c0 = w: with the permutation the whole 8B-shaped decode step ran
+    // 1.6% slower (1.476 -> 1.499 ms per token).
     const int ng = (int)ngroups, g = (int)gridDim.x;
-    const int c0 = g % 8 == 0 ? (int)(blockIdx.x % 8) * (g / 8) + (int)(blockIdx.x / 8) : (int)blockIdx.x;
+    const int c0 = !FUSED && g % 8 == 0 ? (int)(blockIdx.x % 8) * (g / 8) + (int)(blockIdx.x / 8)
+                                        : (int)blockIdx.x;
     uint32_t ra[T::kRaw], rb[T::kRaw];
     if constexpr (!SPREAD) load_group(c0, ra);
     // keep the weight loads here, in flight during the conversion below

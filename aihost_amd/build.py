@@ -29,8 +29,12 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 # Per-file extras: the bit-exact dequantizer must not contract a*b-c into FMA;
-# the decoder operators round their element-wise formulas like the reference.
-EXTRA = {"aih_dequant.hip": ["-ffp-contract=off"], "aih_decoder.hip": ["-ffp-contract=off"]}
+# the decoder operators round their element-wise formulas like the reference;
+# the batch-1/2 matvec writes its fused multiply-adds out, so that every
+# activation column is computed by the same instructions (and its fused
+# prologues round like the separate decoder operators).
+EXTRA = {"aih_dequant.hip": ["-ffp-contract=off"], "aih_decoder.hip": ["-ffp-contract=off"],
+         "aih_qmatvec.hip": ["-ffp-contract=off"]}
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-pthread"]
 
 

@@ -21,20 +21,28 @@
 // DPP inside a wave and through LDS across the waves of a team; row results
 // stay in registers until the end of the launch.
 //
-// Arithmetic.  A 4-bit (or 6-bit, or biased 8-bit) code q becomes the fp16
-// value 1024 + q by OR-ing it into the mantissa of 0x6400, two codes per
-// 32-bit register, and is contracted against fp16 activations with
-// v_dot2_f32_f16, which accumulates in fp32.  The 1024 * sum(x) bias (and the
-// format offset: -8 for Q4_0, -32 for Q6_K, +128 for the biased Q8_0 code) is
-// removed by starting the accumulator at -(1024 + offset) * sum(x).  Codes in
-// a high nibble are used in place (value 16*q): the activations they meet
-// are stored pre-divided by 16.  Sub-block scales and mins are applied once
-// per sub-block in fp32:
+// Arithmetic (fp32-equivalent).  A 4-bit (or 6-bit, or biased 8-bit) code q
+// masked out of its packed word, two codes per 32-bit register, IS the fp16
+// subnormal q * 2^-24: the exponent field stays zero, so the code needs no
+// conversion and carries no bias.  Codes in a high nibble are used in place
+// (value 16q * 2^-24) against activations stored pre-divided by 16.  Each
+// activation is held as two fp16 numbers, hi = fp16(x') and lo =
+// fp16((x' - hi) * 2^11), which together carry 22 significant bits, and every
+// code pair is contracted with both by v_dot2_f32_f16 (the products of two
+// fp16 numbers are exact in fp32; the sums accumulate in fp32).  x' is x times
+// a power of two chosen per column from max|x| (every workgroup reduces it
+// over the x it loads anyway), so that the largest activation lands in
+// [2^13, 2^14): no activation overflows fp16, and every one within 2^-27 of
+// the largest keeps all 22 bits.  Accumulators therefore hold
+// R * sum(q * x) with R = 2^-24 * (the power of two); the format offsets
+// (-8 for Q4_0, -32 for Q6_K, +128 for the biased Q8_0 code) enter as
+// -offset * R * sum(x), with sum(x) taken in fp32 from x itself.  Sub-block
+// scales and mins are applied once per sub-block in fp32:
 //   Q4_K: d*sc*S - dmin*mn*X      (S = sum q*x, X = sum x over the sub-block)
 //   Q6_K: d*sc*sum((q-32)*x)      Q8_0: d*sum(q*x)      Q4_0: d*sum((q-8)*x)
-// The only rounding beyond fp32 accumulation is that of x to fp16 (relative
-// 2^-11 per element), which gives a normwise error near 2e-4, inside the 1e-3
-// bound this path is held to.
+// and each row's total is divided by R once, after the wave reduction.  The
+// measured normwise error against the reference's sequential fp32 product is
+// about 1e-6 (the earlier fp16-activation form: 2e-4).
 #include "aih_internal.h"
 
 namespace {
@@ -50,21 +58,12 @@ __device__ __forceinline__ float dot2(uint32_t p, uint32_t x, float acc)
 }
 // (a & mask) | b as one v_and_or_b32.  Written out because VOP3 encodings on
 // this architecture take no literal operand and read at most one scalar
-// register, so with a literal mask and a literal b the compiler emits a
-// v_and_b32 + v_or_b32 pair instead.  Here the mask travels in an SGPR and b
-// (the fp16 exponent pattern) in a VGPR.
+// register, so with a literal mask the compiler emits a v_and_b32 + v_or_b32
+// pair instead.  Here the mask travels in an SGPR.
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t b)
 {
     uint32_t r;
     asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(b));
-    return r;
-}
-// The fp16 exponent pattern (1024, 1024) in a VGPR, opaque to the optimiser so
-// it stays a register operand of v_and_or_b32.
-__device__ __forceinline__ uint32_t magic_vgpr()
-{
-    uint32_t r;
-    asm("v_mov_b32 %0, 0x64006400" : "=v"(r));
     return r;
 }
 __device__ __forceinline__ float f16lo(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xFFFFu)); }
@@ -76,7 +75,6 @@ __device__ __forceinline__ h2 pack2(float a, float b)
     r.y = (_Float16)b;
     return r;
 }
-__device__ __forceinline__ float hsum(h2 v) { return __builtin_amdgcn_fdot2(v, pack2(1.0f, 1.0f), 0.0f, false); }
 
 template <class T>
 __device__ __forceinline__ T ldg(const void *p)
@@ -124,33 +122,44 @@ struct BufRow {
 };
 
 // One prep step turns 4 consecutive activations x[src..src+3] (one 16-byte
-// load) into the fp16 pairs (x0, x2) and (x1, x3), stored at image dwords d0
-// and d0+1, and adds their sum to sum slot `slot`.  Steps with div16 feed
-// high-nibble codes: their activations are stored divided by 16 (the sum is
-// not).  A unit needs 16 steps; d0, slot and div16 depend only on the step.
-// The 32 image dwords form 8 groups of 4 that a format's dot product reads
-// one group (one 16-byte LDS read) at a time.
+// load) into their three limb words (word `step` of each limb image of the
+// unit; see convert_step) and adds their fp32 sum to sum slot `slot`.  A unit
+// needs 16 steps; the step's place in the unit and its slot depend only on
+// the step.  A limb image
+// is 16 words in 4 groups of 4 steps that a format's dot product reads one
+// group (one 16-byte read) at a time: group(b, l, i) is group i of limb l of
+// column b.
 struct Step {
     int src;
-    int d0, slot;
-    bool div16;
+    int slot;
 };
+
+// Signed 8-bit integer dot product of four byte pairs, accumulated in int32
+// (v_dot4_i32_i8): exact.
+__device__ __forceinline__ int sdot4(uint32_t codes, uint32_t limb, int acc)
+{
+    return __builtin_amdgcn_sdot4((int)codes, (int)limb, acc, false);
+}
+
+// sum over the three limbs of one code stream (limb l holds digit l, of
+// weight 2^(8l)): A0 + 2^8 A1 + 2^16 A2 as fp32 (each term is exact in fp32;
+// the sum is rounded once or twice)
+__device__ __forceinline__ float limbs_f(const int *a)
+{
+    return __builtin_fmaf((float)a[2], 65536.f, __builtin_fmaf((float)a[1], 256.f, (float)a[0]));
+}
 
 // ---------------------------------------------------------------- Q4_K ----
 // Unit u: block u/4, 64-group g = u%4 -> qs bytes 32g..32g+31 of the block,
 // low nibbles are sub-block 2g (k0 + 0..31), high nibbles sub-block 2g+1
 // (k0 + 32..63), k0 = 64u.  (Element order: ComputeOps.cs:1642-1675.)
-// Image group i (i < 8): (x[k0+4i], x[k0+4i+2]), (x[k0+4i+1], x[k0+4i+3]),
-// then the same two pairs for k0+32+4i.. divided by 16.
+// qs word k (k < 8) holds the low-nibble codes of elements 4k..4k+3 (step k)
+// and the high-nibble codes of elements 32+4k.. (step 8+k).
 // Sums: 0 low sub-block, 1 high sub-block.
 struct Q4K {
     static constexpr int kRaw = 12;
     static constexpr int kSums = 2;
-    __device__ static Step step(int u, int s)
-    {
-        if (s < 8) return {64 * u + 4 * s, 4 * s, 0, false};
-        return {64 * u + 32 + 4 * (s - 8), 4 * (s - 8) + 2, 1, true};
-    }
+    __device__ static Step step(int u, int s) { return {64 * u + 4 * s, s >> 3}; }
     // unit and step of the 4 activations x[4e .. 4e+3] (step(u, s).src == 4e)
     __device__ static void inv(int e, int &u, int &s) { u = e >> 4; s = e & 15; }
     // The row starts at byte `off` of `w`; lane offsets are added to off.
@@ -166,7 +175,6 @@ struct Q4K {
     template <int B, class XA>
     __device__ static void dot(const uint32_t *raw, const XA &xa, int u, float *out)
     {
-        const uint32_t M = magic_vgpr();
         // 6-bit (scale, min) of sub-blocks 2g and 2g+1 (get_scale_min_k4,
         // QuantizationFormats.cs:157-165), branch-free per lane.
         const int g = u & 3;
@@ -180,28 +188,27 @@ struct Q4K {
         const uint32_t mn1 = __builtin_amdgcn_ubfe(a_mn, s0 + 8 + moff, wlo) | (__builtin_amdgcn_ubfe(raw[2], s0 + 14, whi) << 4);
         const float d = f16lo(raw[0]), dmin = f16hi(raw[0]);
         const float fsc0 = (float)sc0, fsc1 = (float)sc1, fmn0 = (float)mn0, fmn1 = (float)mn1;
-        float alo[B], ahi[B];
-#pragma unroll
-        for (int b = 0; b < B; ++b) { alo[b] = -1024.f * xa.sum(b, 0); ahi[b] = -64.f * xa.sum(b, 1); }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t w = raw[4 + i], w8 = w >> 8;
-            const uint32_t p0 = and_or(w, 0x000F000Fu, M), p1 = and_or(w, 0x00F000F0u, M);
-            const uint32_t p2 = and_or(w8, 0x000F000Fu, M), p3 = and_or(w8, 0x00F000F0u, M);
-#pragma unroll
-            for (int b = 0; b < B; ++b) {
-                const u4 x = xa.group(b, i);
-                alo[b] = dot2(p0, x.x, alo[b]);
-                alo[b] = dot2(p2, x.y, alo[b]);
-                ahi[b] = dot2(p1, x.z, ahi[b]);
-                ahi[b] = dot2(p3, x.w, ahi[b]);
-            }
-        }
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            const float s = fsc0 * alo[b] + fsc1 * ahi[b];
-            const float m = fmn0 * xa.sum(b, 0) + fmn1 * xa.sum(b, 1);
-            out[b] += d * s - dmin * m;
+            int lo[3] = {0, 0, 0}, hi[3] = {0, 0, 0};
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const u4 gl[3] = {xa.group(b, 0, i), xa.group(b, 1, i), xa.group(b, 2, i)};
+                const u4 gh[3] = {xa.group(b, 0, 2 + i), xa.group(b, 1, 2 + i), xa.group(b, 2, 2 + i)};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t w = raw[4 + 4 * i + j];
+                    const uint32_t cl = w & 0x0F0F0F0Fu, ch = (w >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+                    for (int l = 0; l < 3; ++l) {
+                        lo[l] = sdot4(cl, gl[l][j], lo[l]);
+                        hi[l] = sdot4(ch, gh[l][j], hi[l]);
+                    }
+                }
+            }
+            const float s = __builtin_fmaf(fsc0, limbs_f(lo), fsc1 * limbs_f(hi));
+            const float m = __builtin_fmaf(fmn0, xa.sum(b, 0), fmn1 * xa.sum(b, 1));
+            out[b] = __builtin_fmaf(__builtin_fmaf(d, s, -dmin * m), xa.inv(b), out[b]);
         }
     }
 };
@@ -209,13 +216,12 @@ struct Q4K {
 // ---------------------------------------------------------------- Q8_0 ----
 // Unit u: blocks 2u and 2u+1 (68 bytes, 4-byte aligned), k0 = 64u.
 // Block A: d at byte 0, qs at 2..33 (realigned with alignbyte); block B: d at
-// 34..35, qs at 36..67.  Codes are biased by +128 (xor 0x80) to make them
-// unsigned before the fp16 trick.  Image group m (m < 8) holds, for i = 2m
-// and 2m+1: (x[4i], x[4i+2]), (x[4i+1], x[4i+3]).  Sums: block A, block B.
+// 34..35, qs at 36..67.  The int8 codes enter the dot products as they are.
+// Code word m of block A (elements 4m..4m+3) is step m, of block B step 8+m.
 struct Q80 {
     static constexpr int kRaw = 17;
-    static constexpr int kSums = 2;
-    __device__ static Step step(int u, int s) { return {64 * u + 4 * s, 4 * (s >> 1) + 2 * (s & 1), s >> 3, false}; }
+    static constexpr int kSums = 1;
+    __device__ static Step step(int u, int s) { return {64 * u + 4 * s, 0}; }
     __device__ static void inv(int e, int &u, int &s) { u = e >> 4; s = e & 15; }
     template <class A>
     __device__ static void load(const A &w, uint32_t off, int u, uint32_t *raw)
@@ -231,48 +237,36 @@ struct Q80 {
     template <int B, class XA>
     __device__ static void dot(const uint32_t *raw, const XA &xa, int, float *out)
     {
-        const uint32_t M = magic_vgpr();
         const float dA = f16lo(raw[0]), dB = f16hi(raw[8]);
-        float aA[B], aB[B];
 #pragma unroll
-        for (int b = 0; b < B; ++b) { aA[b] = -1152.f * xa.sum(b, 0); aB[b] = -1152.f * xa.sum(b, 1); }
+        for (int b = 0; b < B; ++b) {
+            int aA[3] = {0, 0, 0}, aB[3] = {0, 0, 0};
 #pragma unroll
-        for (int m = 0; m < 8; ++m) {
-            const int i0 = 2 * m, i1 = 2 * m + 1;
-            const uint32_t w0 = (i0 < 8 ? __builtin_amdgcn_alignbyte(raw[i0 + 1], raw[i0], 2) : raw[i0 + 1]) ^ 0x80808080u;
-            const uint32_t w1 = (i1 < 8 ? __builtin_amdgcn_alignbyte(raw[i1 + 1], raw[i1], 2) : raw[i1 + 1]) ^ 0x80808080u;
-            const uint32_t p0 = and_or(w0, 0x00FF00FFu, M), p1 = and_or(w0 >> 8, 0x00FF00FFu, M);
-            const uint32_t q0 = and_or(w1, 0x00FF00FFu, M), q1 = and_or(w1 >> 8, 0x00FF00FFu, M);
+            for (int i = 0; i < 4; ++i) {
+                const u4 gr[3] = {xa.group(b, 0, i), xa.group(b, 1, i), xa.group(b, 2, i)};
 #pragma unroll
-            for (int b = 0; b < B; ++b) {
-                const u4 x = xa.group(b, m);
-                float &a = m < 4 ? aA[b] : aB[b];
-                a = dot2(p0, x.x, a);
-                a = dot2(p1, x.y, a);
-                a = dot2(q0, x.z, a);
-                a = dot2(q1, x.w, a);
+                for (int j = 0; j < 4; ++j) {
+                    const int s = 4 * i + j;   // step: code word s % 8 of block s / 8
+                    const uint32_t c = s < 8 ? __builtin_amdgcn_alignbyte(raw[s + 1], raw[s], 2) : raw[s + 1];
+                    int *acc = s < 8 ? aA : aB;
+#pragma unroll
+                    for (int l = 0; l < 3; ++l) acc[l] = sdot4(c, gr[l][j], acc[l]);
+                }
             }
+            out[b] = __builtin_fmaf(__builtin_fmaf(dA, limbs_f(aA), dB * limbs_f(aB)), xa.inv(b), out[b]);
         }
-#pragma unroll
-        for (int b = 0; b < B; ++b) out[b] += dA * aA[b] + dB * aB[b];
     }
 };
 
 // ---------------------------------------------------------------- Q4_0 ----
 // Unit u: blocks 2u and 2u+1 (36 bytes, 4-byte aligned), k0 = 64u.  In each
-// block qs[j] holds element j (low nibble) and j+16 (high nibble).
-// Image group 4*blk + i (blk < 2, i < 4): (x[4i], x[4i+2]), (x[4i+1],
-// x[4i+3]) of the block, then the same for elements 16+4i.. divided by 16.
-// Sums: blk low half, then 2+blk high half.
+// block qs[j] holds element j (low nibble) and j+16 (high nibble): qs word i
+// (i < 4) of block A holds the codes of steps i (low) and 4+i (high), of
+// block B steps 8+i and 12+i.  Sums: block A, block B.
 struct Q40 {
     static constexpr int kRaw = 9;
-    static constexpr int kSums = 4;
-    __device__ static Step step(int u, int s)
-    {
-        const int blk = s >> 3, r = s & 7;
-        if (r < 4) return {64 * u + 32 * blk + 4 * r, 4 * (4 * blk + r), blk, false};
-        return {64 * u + 32 * blk + 16 + 4 * (r - 4), 4 * (4 * blk + r - 4) + 2, 2 + blk, true};
-    }
+    static constexpr int kSums = 2;
+    __device__ static Step step(int u, int s) { return {64 * u + 4 * s, s >> 3}; }
     __device__ static void inv(int e, int &u, int &s) { u = e >> 4; s = e & 15; }
     template <class A>
     __device__ static void load(const A &w, uint32_t off, int u, uint32_t *raw)
@@ -286,32 +280,30 @@ struct Q40 {
     template <int B, class XA>
     __device__ static void dot(const uint32_t *raw, const XA &xa, int, float *out)
     {
-        const uint32_t M = magic_vgpr();
         const float d[2] = {f16lo(raw[0]), f16hi(raw[4])};
 #pragma unroll
-        for (int blk = 0; blk < 2; ++blk) {
-            float a[B];
-            // sum((q-8)*x) over the block: low-nibble codes meet x, high-nibble
-            // codes (value 16q) meet x/16; the bias of both halves is removed here.
+        for (int b = 0; b < B; ++b) {
+            float t = 0.f;
 #pragma unroll
-            for (int b = 0; b < B; ++b) a[b] = -1032.f * xa.sum(b, blk) - 72.f * xa.sum(b, 2 + blk);
+            for (int blk = 0; blk < 2; ++blk) {
+                // sum((q-8)*x) over the block: the offset enters as -8 * sum(x)
+                int a[3] = {0, 0, 0};
+                const u4 gl[3] = {xa.group(b, 0, 2 * blk), xa.group(b, 1, 2 * blk), xa.group(b, 2, 2 * blk)};
+                const u4 gh[3] = {xa.group(b, 0, 2 * blk + 1), xa.group(b, 1, 2 * blk + 1),
+                                  xa.group(b, 2, 2 * blk + 1)};
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t w = blk == 0 ? __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], 2) : raw[5 + i];
-                const uint32_t w8 = w >> 8;
-                const uint32_t p0 = and_or(w, 0x000F000Fu, M), p1 = and_or(w, 0x00F000F0u, M);
-                const uint32_t p2 = and_or(w8, 0x000F000Fu, M), p3 = and_or(w8, 0x00F000F0u, M);
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t w = blk == 0 ? __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], 2) : raw[5 + i];
+                    const uint32_t cl = w & 0x0F0F0F0Fu, ch = (w >> 4) & 0x0F0F0F0Fu;
 #pragma unroll
-                for (int b = 0; b < B; ++b) {
-                    const u4 x = xa.group(b, 4 * blk + i);
-                    a[b] = dot2(p0, x.x, a[b]);
-                    a[b] = dot2(p2, x.y, a[b]);
-                    a[b] = dot2(p1, x.z, a[b]);
-                    a[b] = dot2(p3, x.w, a[b]);
+                    for (int l = 0; l < 3; ++l) {
+                        a[l] = sdot4(cl, gl[l][i], a[l]);
+                        a[l] = sdot4(ch, gh[l][i], a[l]);
+                    }
                 }
+                t = __builtin_fmaf(d[blk], __builtin_fmaf(-8.f, xa.sum(b, blk), limbs_f(a)), t);
             }
-#pragma unroll
-            for (int b = 0; b < B; ++b) out[b] += d[blk] * a[b];
+            out[b] = __builtin_fmaf(t, xa.inv(b), out[b]);
         }
     }
 };
@@ -321,10 +313,9 @@ struct Q40 {
 // ql[64h+16t .. +15] (quarters 0 and 2), ql[64h+32+16t .. +15] (quarters 1
 // and 3) and qh[32h+16t .. +15] (high 2 bits of all four quarters), i.e.
 // elements 128h + 32*quarter + 16t + i, i < 16 (ComputeOps.cs:1748-1771).
-// Each quarter's 16 elements form one sub-block with an int8 scale.
-// Image group 2m + (q >> 1) (m < 4) holds quarters q = 0, 1 (or 2, 3):
-// (x[4m], x[4m+2]), (x[4m+1], x[4m+3]) of each, quarters 2 and 3 divided by
-// 16.  Sums: one per quarter.
+// Each quarter's 16 elements form one sub-block with an int8 scale; code
+// word m (elements 4m..4m+3) of quarter Q is step 4Q + m.  Sums: one per
+// quarter.
 struct Q6K {
     static constexpr int kRaw = 15;
     static constexpr int kSums = 4;
@@ -332,7 +323,7 @@ struct Q6K {
     {
         const int q = s >> 2, m = s & 3;
         const int base = (u >> 2) * 256 + 128 * ((u >> 1) & 1) + 16 * (u & 1);
-        return {base + 32 * q + 4 * m, 4 * (2 * m + (q >> 1)) + 2 * (q & 1), q, q >= 2};
+        return {base + 32 * q + 4 * m, q};
     }
     // f4 index jb = 32h + 8q + 4t + m within the 256-element block
     __device__ static void inv(int e, int &u, int &s)
@@ -358,90 +349,114 @@ struct Q6K {
     template <int B, class XA>
     __device__ static void dot(const uint32_t *raw, const XA &xa, int u, float *out)
     {
-        const uint32_t M = magic_vgpr();
         const uint32_t t8 = (u & 1) * 8;
         // int8 sub-block scales (signed extract, then signed conversion)
-        const float sc0 = (float)(int)__builtin_amdgcn_sbfe((int)raw[12], t8, 8);
-        const float sc1 = (float)(int)__builtin_amdgcn_sbfe((int)raw[12], t8 + 16, 8);
-        const float sc2 = (float)(int)__builtin_amdgcn_sbfe((int)raw[13], t8, 8);
-        const float sc3 = (float)(int)__builtin_amdgcn_sbfe((int)raw[13], t8 + 16, 8);
+        const float sc[4] = {(float)(int)__builtin_amdgcn_sbfe((int)raw[12], t8, 8),
+                             (float)(int)__builtin_amdgcn_sbfe((int)raw[12], t8 + 16, 8),
+                             (float)(int)__builtin_amdgcn_sbfe((int)raw[13], t8, 8),
+                             (float)(int)__builtin_amdgcn_sbfe((int)raw[13], t8 + 16, 8)};
         const float d = f16lo(raw[14]);
-        float a0[B], a1[B], a2[B], a3[B];
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            a0[b] = -1056.f * xa.sum(b, 0); a1[b] = -1056.f * xa.sum(b, 1);
-            a2[b] = -96.f * xa.sum(b, 2);   a3[b] = -96.f * xa.sum(b, 3);
-        }
+            float s = 0.f;
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const uint32_t w = raw[m], v = raw[4 + m], hb = raw[8 + m];
-            const uint32_t w8 = w >> 8, v8 = v >> 8, hb4 = hb << 4, hb2 = hb << 2, hr4 = hb >> 4, hr6 = hb >> 6;
-            // quarter 0: low nibble of ql[A] + qh bits 0-1; quarter 2: high nibble of ql[A] + bits 4-5 (x16)
-            // quarter 1: low nibble of ql[B] + qh bits 2-3; quarter 3: high nibble of ql[B] + bits 6-7 (x16)
-            const uint32_t q0e = and_or(hb4, 0x00300030u, and_or(w, 0x000F000Fu, M));
-            const uint32_t q2e = and_or(hb4, 0x03000300u, and_or(w, 0x00F000F0u, M));
-            const uint32_t q1e = and_or(hb2, 0x00300030u, and_or(v, 0x000F000Fu, M));
-            const uint32_t q3e = and_or(hb2, 0x03000300u, and_or(v, 0x00F000F0u, M));
-            const uint32_t q0o = and_or(hr4, 0x00300030u, and_or(w8, 0x000F000Fu, M));
-            const uint32_t q2o = and_or(hr4, 0x03000300u, and_or(w8, 0x00F000F0u, M));
-            const uint32_t q1o = and_or(hr6, 0x00300030u, and_or(v8, 0x000F000Fu, M));
-            const uint32_t q3o = and_or(hr6, 0x03000300u, and_or(v8, 0x00F000F0u, M));
+            for (int Q = 0; Q < 4; ++Q) {
+                int a[3] = {0, 0, 0};
+                const u4 gr[3] = {xa.group(b, 0, Q), xa.group(b, 1, Q), xa.group(b, 2, Q)};
 #pragma unroll
-            for (int b = 0; b < B; ++b) {
-                const u4 xl = xa.group(b, 2 * m), xh = xa.group(b, 2 * m + 1);
-                a0[b] = dot2(q0o, xl.y, dot2(q0e, xl.x, a0[b]));
-                a1[b] = dot2(q1o, xl.w, dot2(q1e, xl.z, a1[b]));
-                a2[b] = dot2(q2o, xh.y, dot2(q2e, xh.x, a2[b]));
-                a3[b] = dot2(q3o, xh.w, dot2(q3e, xh.z, a3[b]));
+                for (int m = 0; m < 4; ++m) {
+                    // 6-bit codes: nibble Q/2 of the quarter's ql word, bits
+                    // 2Q, 2Q+1 of the qh word at bits 4, 5
+                    const uint32_t l = (Q & 1) ? raw[4 + m] : raw[m], hb = raw[8 + m];
+                    const uint32_t nib = (Q >> 1) ? (l >> 4) & 0x0F0F0F0Fu : l & 0x0F0F0F0Fu;
+                    const uint32_t hsh = Q == 0 ? hb << 4 : Q == 1 ? hb << 2 : Q == 2 ? hb : hb >> 2;
+                    const uint32_t c = and_or(hsh, 0x30303030u, nib);
+#pragma unroll
+                    for (int li = 0; li < 3; ++li) a[li] = sdot4(c, gr[li][m], a[li]);
+                }
+                s = __builtin_fmaf(sc[Q], __builtin_fmaf(-32.f, xa.sum(b, Q), limbs_f(a)), s);
             }
+            out[b] = __builtin_fmaf(d * s, xa.inv(b), out[b]);
         }
-#pragma unroll
-        for (int b = 0; b < B; ++b)
-            out[b] += d * (sc0 * a0[b] + sc1 * a1[b] + sc2 * a2[b] + sc3 * a3[b]);
     }
 };
 
-// Convert one step's 4 activations: two fp16 pairs and their (unscaled) sum.
-__device__ __forceinline__ float convert_step(f4 v, bool div16, uint32_t &p0, uint32_t &p1)
+// Per-unit activation scale.  From the biased exponent e of max|x| over the
+// unit's 64 activations (x after any fused prologue; e = 255 for inf or NaN),
+// clamped to [22, 254]: every activation of the unit becomes the integer
+// X = round(x * S), S = 2^(148 - e), so that |X| < 2^22 (the largest lands in
+// [2^21, 2^22]).  Products of codes and X are summed exactly in int32; the
+// unit's contribution to a row is multiplied by 1/S = 2^(e - 148).  S and 1/S
+// are built from their exponent fields (exact, normal fp32 over the clamped
+// range).  A non-finite activation makes every row NaN (1/S = NaN).
+struct ColScale {
+    float s, inv_s;
+};
+__device__ __forceinline__ ColScale col_scale(uint32_t maxabs_bits)
 {
-    const float f = div16 ? 0.0625f : 1.0f;
-    const h2 a = pack2(v.x * f, v.z * f), c = pack2(v.y * f, v.w * f);
-    p0 = __builtin_bit_cast(uint32_t, a);
-    p1 = __builtin_bit_cast(uint32_t, c);
-    const float s = hsum(a) + hsum(c);
-    return div16 ? 16.f * s : s;
+    const int e0 = (int)(maxabs_bits >> 23);
+    const int e = e0 < 22 ? 22 : e0 > 254 ? 254 : e0;
+    return {__uint_as_float((uint32_t)(275 - e) << 23),
+            e0 == 255 ? __uint_as_float(0x7FC00000u) : __uint_as_float((uint32_t)(e - 21) << 23)};
 }
 
-// Activation image of one unit in registers (used when a workgroup is a
-// single row team and nothing is shared).
+// Limb words of one step's 4 activations.  Y = round(x * S) + 0x808080 lies
+// in [0, 2^24); byte l of Y minus 128 (byte XOR 0x80) is the balanced signed
+// digit d_l, with X = d_0 + 2^8 d_1 + 2^16 d_2 (|d_2| <= 64).  Limb word l
+// packs d_l of x0..x3 as four int8 (x0 in the low byte), the operand layout
+// of v_dot4_i32_i8.
+__device__ __forceinline__ void convert_step(f4 v, float S, uint32_t &w0, uint32_t &w1, uint32_t &w2)
+{
+    const uint32_t ya = (uint32_t)__builtin_rintf(__builtin_fmaf(v.x, S, 8421504.f));
+    const uint32_t yb = (uint32_t)__builtin_rintf(__builtin_fmaf(v.y, S, 8421504.f));
+    const uint32_t yc = (uint32_t)__builtin_rintf(__builtin_fmaf(v.z, S, 8421504.f));
+    const uint32_t yd = (uint32_t)__builtin_rintf(__builtin_fmaf(v.w, S, 8421504.f));
+    const uint32_t ab = __builtin_amdgcn_perm(yb, ya, 0x05010400u);   // a0 b0 a1 b1
+    const uint32_t cd = __builtin_amdgcn_perm(yd, yc, 0x05010400u);   // c0 d0 c1 d1
+    const uint32_t ab2 = __builtin_amdgcn_perm(yb, ya, 0x0c0c0602u);  // a2 b2 0 0
+    const uint32_t cd2 = __builtin_amdgcn_perm(yd, yc, 0x0c0c0602u);  // c2 d2 0 0
+    w0 = __builtin_amdgcn_perm(cd, ab, 0x05040100u) ^ 0x80808080u;
+    w1 = __builtin_amdgcn_perm(cd, ab, 0x07060302u) ^ 0x80808080u;
+    w2 = __builtin_amdgcn_perm(cd2, ab2, 0x05040100u) ^ 0x80808080u;
+}
+__device__ __forceinline__ float sum4(f4 v) { return (v.x + v.y) + (v.z + v.w); }
+
+// Limb images of one unit in registers (a single row team whose image does
+// not fit in LDS converts its own; with one column, the LDS image is copied
+// into them), with the unit's step sums (pre-scaled by S) and 1/S.
 template <int B, int S>
 struct XRegs {
-    u4 g[B][8];
+    u4 g[B][3][4];
     float s[B][S];
-    __device__ __forceinline__ u4 group(int b, int i) const { return g[b][i]; }
+    float iv[B];
+    __device__ __forceinline__ u4 group(int b, int l, int i) const { return g[b][l][i]; }
     __device__ __forceinline__ float sum(int b, int k) const { return s[b][k]; }
+    __device__ __forceinline__ float inv(int b) const { return iv[b]; }
 };
 
-// Activation image in LDS, shared by the teams of a workgroup (one entry per
-// unit, i.e. per lane of a team).  Laid out unit-minor so that the lanes of a
-// wave touch consecutive LDS words: group i (16 bytes) of unit u for column b
-// is entry (b*8 + i)*tt + u of the group array, and step sum s is entry
-// (b*16 + s)*tt + u of the sum array that follows (tt = lanes per team).  A
-// unit-major layout (each lane's image contiguous) would put the lanes of a
-// read on a few banks and serialise every LDS access several-fold.
-constexpr int kLdsBytesPerUnit = 8 * 16 + 16 * 4;   // groups + step sums, per column
+// Limb images in LDS, shared by the teams of a workgroup (one entry per unit,
+// i.e. per lane of a team).  Laid out unit-minor so that the lanes of a wave
+// touch consecutive LDS words: group i (16 bytes) of limb l of unit u for
+// column b is entry ((b*3 + l)*4 + i)*tt + u of the group array, step sum s
+// (times S) is entry (b*16 + s)*tt + u of the sum array that follows, and 1/S
+// entry b*tt + u of the scale array after it (tt = lanes per team).  A unit-major layout (each lane's image contiguous) would put the
+// lanes of a read on a few banks and serialise every LDS access several-fold.
+constexpr int kLdsBytesPerUnit = 3 * 4 * 16 + 16 * 4 + 4;   // limb groups, step sums, 1/S; per column
 // Each row of the group and sum arrays holds kLdsPad entries past the team's
-// units: the conversion writes a wave's 64 consecutive 16-byte activation
-// pieces (4 units x 16 steps) to rows `step` and columns `unit`, and the pad
-// spreads those writes over the banks.
+// units: the conversion writes a wave's 64 consecutive activation steps
+// (4 units x 16 steps) to rows `step` and columns `unit`, and the pad spreads
+// those writes over the banks.
 constexpr int kLdsPad = 4;
+constexpr size_t kLdsMax = 160 * 1024;   // LDS per workgroup on gfx950
 template <int B, int S>
 struct XLds {
-    const u4 *grp;   // group 0 of column 0 of this lane's unit
+    const u4 *grp;   // group 0 of limb 0 of column 0 of this lane's unit
     int tt;          // lanes per team
     float s[B][S];
-    __device__ __forceinline__ u4 group(int b, int i) const { return grp[(b * 8 + i) * tt]; }
+    float iv[B];
+    __device__ __forceinline__ u4 group(int b, int l, int i) const { return grp[((b * 3 + l) * 4 + i) * tt]; }
     __device__ __forceinline__ float sum(int b, int k) const { return s[b][k]; }
+    __device__ __forceinline__ float inv(int b) const { return iv[b]; }
 };
 
 // Sum over the 64 lanes of a wave; the total lands in lane 63.
@@ -453,6 +468,17 @@ __device__ __forceinline__ float wave_sum_to_lane63(float v)
     v += __builtin_amdgcn_update_dpp(0.0f, v, 0x140, 0xF, 0xF, false);  // row_mirror
     v += __builtin_amdgcn_update_dpp(0.0f, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 -> rows 1, 3
     v += __builtin_amdgcn_update_dpp(0.0f, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 -> rows 2, 3
+    return v;
+}
+
+// Maximum of v over the 16 lanes of each DPP row (unsigned), in every lane
+// of the row.
+__device__ __forceinline__ uint32_t row16_max_u32(uint32_t v)
+{
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));  // row_mirror
     return v;
 }
 
@@ -530,13 +556,17 @@ __device__ __forceinline__ void lds_barrier()
 //     compiler then waits at the head for loads meant to stay in flight.
 // W is deliberately not __restrict__: that would let the compiler sink the
 // first weight loads below the LDS barrier of the activation exchange.
-template <class T, int B, int TEAMS, bool ONEWAVE, int MAXT, bool FUSED>
+template <class T, int B, int TEAMS, bool ONEWAVE, int MAXT, bool FUSED, bool REGS>
 __global__ void __launch_bounds__(MAXT)
 qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
                const float *__restrict__ X, int64_t ldx, float *__restrict__ Y, int64_t ldy, Fuse fz)
 {
     extern __shared__ __align__(16) uint32_t xs[];
-    __shared__ float red[MAXT / 64][B];   // RMSNorm prologue: per-wave sums
+    __shared__ float red[MAXT / 64][B];    // RMSNorm prologue: per-wave sums of squares
+    // With one column the limb image is copied from LDS into registers once
+    // (48 VGPRs), so the row loop reads no LDS; two columns read it from LDS
+    // per row.
+    constexpr bool HOIST = !REGS && B == 1;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -563,23 +593,23 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
             T::load(BufRow{wres, (uint32_t)cc * gstride}, toff, u, raw);
     };
 
-    // A single team converts the 16 steps of its units itself (into
-    // registers); several teams convert x once into LDS, each team NST of the
-    // 16 steps of every unit.  Teams of several waves (x above 16 KB) read x
-    // instead in consecutive 16-byte pieces, piece k*threads + tid, and put
-    // each piece into its (unit, step) entry: reading a unit's own pieces
-    // puts the 64 lanes of a load on 64 lines, and once x outgrows L1 every
-    // line is fetched again for each of its 8 pieces (on MI355X the 4096 x
-    // 14336 Q4_K product took 0.5 us longer that way).  For single-wave teams
-    // the per-unit reads measured faster (x fits in L1).
+    // Conversion mapping.  Several teams: piece p = k*blockDim.x + tid
+    // (k < NST) is step p % 16 of unit p / 16, so the 16 lanes of a DPP row
+    // hold the 16 steps of one unit and reduce its max|x| among themselves,
+    // and a wave reads one contiguous KB of x (the order of the elements
+    // inside a unit, T::step, only permutes lanes within it).  One team:
+    // thread ut converts the 16 steps of its own unit.
     constexpr int NST = 16 / TEAMS;
+    constexpr bool PIECES = TEAMS > 1;
+    // Several teams of several waves share a wide x: their first weight row
+    // is issued once x has landed (below); everyone else issues it now.
     constexpr bool SPREAD = TEAMS > 1 && !ONEWAVE;
     const int pieces = 16 * geo.units;
     auto piece = [&](int k) { return k * (int)blockDim.x + tid; };
-    auto src_of = [&](int k) {
-        if constexpr (SPREAD) return piece(k) < pieces ? 4 * piece(k) : 0;
-        else return T::step(u, team * NST + k).src;
-    };
+    auto valid = [&](int k) { return PIECES ? piece(k) < pieces : active; };
+    auto unit_of = [&](int k) { return PIECES ? (valid(k) ? piece(k) >> 4 : 0) : u; };
+    auto step_of = [&](int k) { return PIECES ? piece(k) & 15 : k; };
+    auto src_of = [&](int k) { return T::step(unit_of(k), step_of(k)).src; };
     f4 xv[B][NST];
 #pragma unroll
     for (int b = 0; b < B; ++b)
@@ -622,9 +652,7 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
     __builtin_amdgcn_sched_barrier(0);
 
     auto x2_of = [&](int b, int k) { return X2_EARLY ? x2v[b][X2_EARLY ? k : 0] : x2_at(b, k); };
-    if (!FUSED) {
-        // plain product: x as given
-    } else if (fz.pre == kPreSiluMul) {
+    if (FUSED && fz.pre == kPreSiluMul) {
 #pragma unroll
         for (int b = 0; b < B; ++b)
 #pragma unroll
@@ -636,10 +664,10 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
                 v.z = silu_f(v.z) * up.z;
                 v.w = silu_f(v.w) * up.w;
             }
-    } else if (fz.pre == kPreRmsNorm) {
-        // The workgroup's threads hold every element of x exactly once
-        // (inactive lanes re-read unit 0, threads past the last piece x[0..3];
-        // both are left out).
+    }
+    if (FUSED && fz.pre == kPreRmsNorm) {
+        // the workgroup's threads hold every element of x once among their
+        // valid steps
         float ss[B];
 #pragma unroll
         for (int b = 0; b < B; ++b) {
@@ -648,12 +676,17 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
             for (int k = 0; k < NST; ++k) {
                 const f4 v = xv[b][k];
                 const float q = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-                ss[b] += !SPREAD || piece(k) < pieces ? q : 0.f;
+                ss[b] += valid(k) ? q : 0.f;
             }
-            float t = SPREAD || active ? ss[b] : 0.f;
+            float t = ss[b];
 #pragma unroll
             for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o);
             if (lane == 0) red[wave][b] = t;
+        }
+        if constexpr (SPREAD) {
+            __builtin_amdgcn_sched_barrier(0);
+            load_group(c0, ra);
+            __builtin_amdgcn_sched_barrier(0);
         }
         lds_barrier();
         const int nw = (int)(blockDim.x >> 6);
@@ -678,60 +711,101 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
         }
     }
 
-    typedef typename std::conditional<TEAMS == 1, XRegs<B, T::kSums>, XLds<B, T::kSums>>::type XA;
+    // Per-unit scale from max|x| over the unit (bit patterns of |x|: unsigned
+    // order is the float order, and a NaN is above every number).
+    constexpr int NCS = PIECES ? NST : 1;   // one scale per held unit
+    ColScale cs[B][NCS];
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+        uint32_t m = 0;
+#pragma unroll
+        for (int k = 0; k < NST; ++k) {
+            const f4 v = xv[b][k];
+            const uint32_t mk = max(max(__float_as_uint(v.x) & 0x7FFFFFFFu, __float_as_uint(v.y) & 0x7FFFFFFFu),
+                                    max(__float_as_uint(v.z) & 0x7FFFFFFFu, __float_as_uint(v.w) & 0x7FFFFFFFu));
+            if constexpr (PIECES) cs[b][PIECES ? k : 0] = col_scale(row16_max_u32(mk));
+            else m = max(m, mk);
+        }
+        if constexpr (!PIECES) cs[b][0] = col_scale(m);
+    }
+    if (SPREAD && !(FUSED && fz.pre == kPreRmsNorm)) {
+        // Wide x shared by several teams of several waves: its loads (16-64
+        // KB per workgroup) have landed once the maxima above read them, so
+        // the first weight row, issued here, does not queue them behind the
+        // weight stream; it is in flight during the conversion.  (With the
+        // RMSNorm prologue it was issued before that prologue's barrier.)
+        __builtin_amdgcn_sched_barrier(0);
+        load_group(c0, ra);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    typedef typename std::conditional<REGS || HOIST, XRegs<B, T::kSums>, XLds<B, T::kSums>>::type XA;
     XA xa;
-    if constexpr (TEAMS == 1) {
+    if constexpr (REGS) {
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            uint32_t img[32];
+            uint32_t img[3][16];
 #pragma unroll
             for (int k = 0; k < T::kSums; ++k) xa.s[b][k] = 0.f;
 #pragma unroll
             for (int s = 0; s < 16; ++s) {
-                const Step st = T::step(u, s);
-                xa.s[b][st.slot] += convert_step(xv[b][s], st.div16, img[st.d0], img[st.d0 + 1]);
+                convert_step(xv[b][s], cs[b][0].s, img[0][s], img[1][s], img[2][s]);
+                xa.s[b][T::step(u, s).slot] += sum4(xv[b][s]);
             }
 #pragma unroll
-            for (int i = 0; i < 8; ++i) xa.g[b][i] = u4{img[4 * i], img[4 * i + 1], img[4 * i + 2], img[4 * i + 3]};
+            for (int k = 0; k < T::kSums; ++k) xa.s[b][k] *= cs[b][0].s;
+            xa.iv[b] = cs[b][0].inv_s;
+#pragma unroll
+            for (int l = 0; l < 3; ++l)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    xa.g[b][l][i] = u4{img[l][4 * i], img[l][4 * i + 1], img[l][4 * i + 2], img[l][4 * i + 3]};
         }
     } else {
-        // uint32 view of the group array and float view of the sum array
-        // (rows of tp entries: the team's units and the pad)
+        // uint32 view of the limb groups, float views of the step sums and
+        // of the per-unit inverse scales (rows of tp entries: the team's
+        // units and the pad)
         const int tp = team_threads + kLdsPad;
         uint32_t *gw = xs;
-        float *sums = reinterpret_cast<float *>(xs + (size_t)B * 8 * 4 * tp);
+        float *sums = reinterpret_cast<float *>(xs + (size_t)B * 3 * 4 * 4 * tp);
+        float *uinv = sums + (size_t)B * 16 * tp;
 #pragma unroll
         for (int k = 0; k < NST; ++k) {
-            int pu = ut, ps = team * NST + k;
-            if constexpr (SPREAD) {
-                if (piece(k) >= pieces) continue;
-                T::inv(piece(k), pu, ps);
-            }
-            const Step st = T::step(SPREAD ? pu : u, ps);
+            if (!valid(k)) continue;
+            const int pu = unit_of(k), ps = step_of(k);
 #pragma unroll
             for (int b = 0; b < B; ++b) {
-                uint32_t p0, p1;
-                const float sum = convert_step(xv[b][k], st.div16, p0, p1);
-                uint32_t *e = gw + ((size_t)(b * 8 + st.d0 / 4) * tp + pu) * 4 + st.d0 % 4;
-                e[0] = p0;
-                e[1] = p1;
-                sums[(b * 16 + ps) * tp + pu] = sum;
+                uint32_t w[3];
+                const ColScale c = cs[b][PIECES ? k : 0];
+                convert_step(xv[b][k], c.s, w[0], w[1], w[2]);
+#pragma unroll
+                for (int l = 0; l < 3; ++l) gw[((size_t)((b * 3 + l) * 4 + ps / 4) * tp + pu) * 4 + ps % 4] = w[l];
+                sums[(b * 16 + ps) * tp + pu] = sum4(xv[b][k]) * c.s;
+                if (ps == 0) uinv[b * tp + pu] = c.inv_s;
             }
         }
-        if constexpr (SPREAD) {
-            // the first row, in flight during the barrier and the sums below
-            load_group(c0, ra);
-            __builtin_amdgcn_sched_barrier(0);
-        }
         lds_barrier();
-        xa.grp = reinterpret_cast<const u4 *>(xs) + ut;
-        xa.tt = tp;
+        if constexpr (HOIST) {
+            // one column: the lane's 12 limb groups stay in registers for
+            // the whole row loop
+            const u4 *grp = reinterpret_cast<const u4 *>(xs) + ut;
+#pragma unroll
+            for (int b = 0; b < B; ++b)
+#pragma unroll
+                for (int l = 0; l < 3; ++l)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) xa.g[b][l][i] = grp[((b * 3 + l) * 4 + i) * tp];
+        } else {
+            xa.grp = reinterpret_cast<const u4 *>(xs) + ut;
+            xa.tt = tp;
+        }
 #pragma unroll
         for (int b = 0; b < B; ++b) {
 #pragma unroll
             for (int k = 0; k < T::kSums; ++k) xa.s[b][k] = 0.f;
 #pragma unroll
             for (int q = 0; q < 16; ++q) xa.s[b][T::step(u, q).slot] += sums[(b * 16 + q) * tp + ut];
+            xa.iv[b] = uinv[b * tp + ut];
         }
     }
 
@@ -855,7 +929,12 @@ int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t row_bytes, Geom ge
     if (fused && B != 1) return AIH_E_INVALID;
     if (fz.post == kPostSiluPairs && (TEAMS % 2 != 0 || N % TEAMS != 0)) return AIH_E_LIMIT;
     const int threads = TEAMS * geo.wr * 64;
-    const size_t lds = TEAMS > 1 ? (size_t)B * kLdsBytesPerUnit * (geo.wr * 64 + kLdsPad) : 0;
+    // The activation image goes to LDS whenever it fits (always for several
+    // teams); a single team of a very wide row (K above about 32500) keeps
+    // each unit's image in its own registers instead.
+    size_t lds = (size_t)B * kLdsBytesPerUnit * (geo.wr * 64 + kLdsPad);
+    const bool regs = TEAMS == 1 && lds > kLdsMax;
+    if (regs) lds = 0;
     const int64_t cap = ctx->cu_count > 0 ? ctx->cu_count : 256;
     // A workgroup computes at most 64 row groups per launch (its results are
     // held in one register per lane); taller matrices take several launches.
@@ -874,12 +953,20 @@ int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t row_bytes, Geom ge
         const int64_t grid = ng < cap ? ng : cap;
         // gate/up pairs write one value per two rows (r0 is a multiple of TEAMS)
         float *ys = Y + (fz.post == kPostSiluPairs ? r0 / 2 : r0);
-        if (fused)
-            hipLaunchKernelGGL((qmatvec_kernel<T, B, TEAMS, ONEWAVE, MAXT, B == 1>), dim3((unsigned)grid),
+        if (fused && regs)
+            hipLaunchKernelGGL((qmatvec_kernel<T, B, TEAMS, ONEWAVE, MAXT, B == 1, TEAMS == 1>), dim3((unsigned)grid),
+                               dim3(threads), lds, ctx->stream, W + r0 * row_bytes, nr, row_bytes, geo, X, ldx,
+                               ys, ldy, fz);
+        else if (fused)
+            hipLaunchKernelGGL((qmatvec_kernel<T, B, TEAMS, ONEWAVE, MAXT, B == 1, false>), dim3((unsigned)grid),
+                               dim3(threads), lds, ctx->stream, W + r0 * row_bytes, nr, row_bytes, geo, X, ldx,
+                               ys, ldy, fz);
+        else if (regs)
+            hipLaunchKernelGGL((qmatvec_kernel<T, B, TEAMS, ONEWAVE, MAXT, false, TEAMS == 1>), dim3((unsigned)grid),
                                dim3(threads), lds, ctx->stream, W + r0 * row_bytes, nr, row_bytes, geo, X, ldx,
                                ys, ldy, fz);
         else
-            hipLaunchKernelGGL((qmatvec_kernel<T, B, TEAMS, ONEWAVE, MAXT, false>), dim3((unsigned)grid),
+            hipLaunchKernelGGL((qmatvec_kernel<T, B, TEAMS, ONEWAVE, MAXT, false, false>), dim3((unsigned)grid),
                                dim3(threads), lds, ctx->stream, W + r0 * row_bytes, nr, row_bytes, geo, X, ldx,
                                ys, ldy, fz);
         const int rc = aih_launch_status();
@@ -911,8 +998,20 @@ int launch_pass(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t row_bytes, Ge
                        : launch<T, 1, 8, true, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, fz);
     case 4: return two ? launch<T, 2, 4, false, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, fz)
                        : launch<T, 1, 4, false, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, fz);
-    case 2: return two ? launch<T, 2, 2, false, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, fz)
-                       : launch<T, 1, 2, false, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, fz);
+    case 2:
+        // two columns of the widest two-team image (K up to 16384) exceed the
+        // LDS of a workgroup: one column per pass there
+        if (two && (size_t)2 * kLdsBytesPerUnit * (geo.wr * 64 + kLdsPad) > kLdsMax) {
+            int rc = launch<T, 1, 2, false, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, fz);
+            if (!rc) {
+                Fuse f1 = fz;
+                if (f1.pre == kPreSiluMul) f1.x2 += ldx;
+                rc = launch<T, 1, 2, false, 512>(ctx, W, N, row_bytes, geo, X + ldx, ldx, Y + ldy, ldy, f1);
+            }
+            return rc;
+        }
+        return two ? launch<T, 2, 2, false, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, fz)
+                   : launch<T, 1, 2, false, 512>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, fz);
     default: {  // one team of up to 16 waves: one column per pass within 128 VGPRs
         int rc = launch<T, 1, 1, false, 1024>(ctx, W, N, row_bytes, geo, X, ldx, Y, ldy, fz);
         if (!rc && two) {

@@ -1,5 +1,13 @@
 """Fused decode matvec vs the oracle (fp32 sequential accumulation over the
-reference-decoded weights): normwise and max relative error <= 1e-3.
+reference-decoded weights): normwise and max relative error <= 2e-5.
+
+Both matvec kernels compute with fp32-equivalent precision (exact integer
+or fp16 x fp16 products of the codes and a power-of-two-scaled fixed-point
+or hi/lo split of x; fp32 sums; the reference's scale formulas in fp32).
+Measured against an fp64 product over the same dequantized weights they
+are within 2e-6; the oracle's own sequential fp32 sum is 1e-6 (K = 4096) to
+5e-6 (K = 65536) away from that, so 2e-5 leaves a margin of about 4 over
+the largest combined error.
 
 Covers the benchmark shapes (Q8_0 4096x4096; Q4_0 and Q4_K 14336x4096; Q6_K
 4096x14336 at batch 1, 2, 4, 8), odd row counts (partial row groups), small K,
@@ -17,7 +25,7 @@ from gpu_util import assert_close, qmatvec, synth_weight, upload
 
 pytestmark = pytest.mark.gpu
 
-TOL = 1e-3  # relative 1e-3 with fp32 accumulation
+TOL = 2e-5  # fp32-equivalent: see the module docstring
 
 
 def x_of(k, batch, seed=43):
@@ -193,9 +201,13 @@ def test_linearity_at_full_size(device, batch_path):
     # the results bit for bit
     assert np.array_equal(ya[0], yb[1]) and np.array_equal(ya[1], yb[0])
     y12 = qmatvec(device, nat.Q4_K, w, n, k, np.vstack([x1 + x2, x1] + extra))
-    assert_close(y12[0], ya[0] + ya[1], 1e-3)       # linearity
+    assert_close(y12[0], ya[0] + ya[1], TOL)         # linearity
     y1 = qmatvec(device, nat.Q4_K, w, n, k, x1)      # single-column kernel
-    assert_close(ya[0], y1[0], 5e-4)                 # the two kernels agree
+    if batch_path == 2:
+        # one column of the two-column pass is the single-column result, bit for bit
+        assert np.array_equal(ya[0], y1[0])
+    else:
+        assert_close(ya[0], y1[0], 1e-5)             # matrix-core and dot-product kernels agree
 
 
 def test_compute_ops_mirror(device, orc):

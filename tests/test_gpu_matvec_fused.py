@@ -4,14 +4,13 @@ separate operators run through the C ABI.
 
 The SiLU-pairs epilogue (gate/up rows interleaved, Y = SiLU(gate)*up) is
 bit-exact to aih_qmatvec + aih_silu_mul_pairs without a prologue, within
-2e-4 of them behind the RMSNorm prologue, and within 2e-3 of the oracle
-(two products, each within 1e-3).
+1e-5 of them behind the RMSNorm prologue, and within 2e-5 of the oracle.
 
 Bars: SiLU*up and the accumulate are bit-exact to aih_silu_mul + aih_qmatvec
 and to y0 + aih_qmatvec (the same fp32 formulas ahead of the same product);
-RMSNorm within 1e-4 normwise of aih_rmsnorm + aih_qmatvec (its sum of squares
-is reduced in another order, which can move an activation across an fp16
-rounding boundary) and within 1e-3 of the oracle.  Shapes cover the
+RMSNorm within 1e-5 normwise of aih_rmsnorm + aih_qmatvec (its sum of squares
+is reduced in another order, which moves the rms by an ulp or so) and within
+2e-5 of the oracle (the matvec's own bound; see test_gpu_matvec.py).  Shapes cover the
 single-wave-team kernel (K 4096), multi-wave teams (K 14336), the
 single-team kernel (K 65536) and a ragged row count (remainder launch).
 """
@@ -76,7 +75,7 @@ def test_silu_mul_prologue_and_accumulate_exact(device, orc, qtype, n, k):
     got = _run(device, qtype, w, n, k, g, u, nat.PRE_SILU_MUL, 1, y0)
     assert np.array_equal(got, y0 + plain)
     ref = orc.matvec(qtype, w, n, k, ol.silu_mul(g, u).reshape(1, k))[0]
-    assert np.linalg.norm(plain - ref) / np.linalg.norm(ref) < 1e-3
+    assert np.linalg.norm(plain - ref) / np.linalg.norm(ref) < 2e-5
 
 
 @pytest.mark.parametrize("qtype,n,k", SHAPES)
@@ -88,9 +87,9 @@ def test_rmsnorm_prologue(device, orc, qtype, n, k):
                  n=k)
     plain = _plain(device, qtype, w, n, k, xn)
     got = _run(device, qtype, w, n, k, x, gw, nat.PRE_RMSNORM, 0, np.zeros(n, np.float32))
-    assert np.linalg.norm(got - plain) / np.linalg.norm(plain) < 1e-4
+    assert np.linalg.norm(got - plain) / np.linalg.norm(plain) < 1e-5
     ref = orc.matvec(qtype, w, n, k, ol.rmsnorm(x.reshape(1, k), gw).reshape(1, k))[0]
-    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-3
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 2e-5
 
 
 def test_plain_and_accumulate_without_prologue(device):
@@ -134,10 +133,10 @@ def test_silu_pairs_epilogue(device, orc, qtype, f, k, pre):
     if pre == nat.PRE_NONE:
         assert np.array_equal(got, two_step)
     else:
-        assert np.linalg.norm(got - two_step) / np.linalg.norm(two_step) < 2e-4
+        assert np.linalg.norm(got - two_step) / np.linalg.norm(two_step) < 1e-5
     xr = x.reshape(1, k) if pre == nat.PRE_NONE else ol.rmsnorm(x.reshape(1, k), gw).reshape(1, k)
     ref = ol.silu_mul(orc.matvec(qtype, gate, f, k, xr)[0], orc.matvec(qtype, up, f, k, xr)[0])
-    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 2e-3
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 2e-5
 
 
 def test_fused_argument_errors(device):

@@ -60,6 +60,8 @@ SIGNATURES = {
     "aih_memcpy_d2d": (_i, [_vp, _vp, _vp, _sz]),
     "aih_upload_tensor": (_i, [_vp, _vp, _vp, _sz]),
     "aih_row_bytes": (_i64, [_i, _i64]),
+    "aih_datatype_from_type": (_i, [_i]),
+    "aih_type_from_datatype": (_i, [_i]),
     "aih_dequantize": (_i, [_vp, _i, _vp, _vp, _u64, _i]),
     "aih_qmatvec": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i]),
     "aih_qmatvec_fused": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _vp, _f, _i, _i, _vp]),

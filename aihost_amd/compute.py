@@ -6,6 +6,8 @@ Names, argument meaning and error behaviour follow the reference so that code
   HipComputeDevice   IComputeDevice   AIHost/AIHost/ICompute/IComputeDevice.cs:27-72
   HipComputeBuffer   IComputeBuffer   AIHost/AIHost/ICompute/IComputeBuffer.cs:6-42
   Tensor             Tensor           AIHost/AIHost/Compute/Tensor.cs:8-150
+  DataType           DataType         AIHost/AIHost/ICompute/IComputeBuffer.cs:57-75
+  map_type           MapType          AIHost/AIHost/Compute/TransformerBase.cs:558-575
   ComputeOps         ComputeOps       AIHost/AIHost/Compute/ComputeOps.cs
       dequantize        Dequantize      :733-745
       dequantize_into   DequantizeInto  :761-861
@@ -23,8 +25,10 @@ import numpy as np
 from . import _native as nat
 
 
-class DataType(enum.IntEnum):
-    """GGUF tensor types handled here (GGUFTensorType, GGUF/GGUFValueType.cs:26-56)."""
+class GGUFTensorType(enum.IntEnum):
+    """ggml tensor type ids of the GGUF file (GGUFTensorType,
+    AIHost/AIHost/GGUF/GGUFValueType.cs:26-56): the type argument of the
+    library's operators.  The four block types of this path and F32."""
     F32 = nat.F32
     Q4_0 = nat.Q4_0
     Q8_0 = nat.Q8_0
@@ -32,8 +36,54 @@ class DataType(enum.IntEnum):
     Q6_K = nat.Q6_K
 
 
-BLOCK_ELEMS = {DataType.F32: 1, DataType.Q4_0: 32, DataType.Q8_0: 32, DataType.Q4_K: 256, DataType.Q6_K: 256}
-BLOCK_BYTES = {DataType.F32: 4, DataType.Q4_0: 18, DataType.Q8_0: 34, DataType.Q4_K: 144, DataType.Q6_K: 210}
+class DataType(enum.IntEnum):
+    """The reference Tensor's type (DataType, AIHost/AIHost/ICompute/
+    IComputeBuffer.cs:57-75), numbered as its declaration order.  Not the
+    ggml numbering: DataType.Q6_K (12) is the ggml id of Q4_K."""
+    F32 = 0
+    F16 = 1
+    Q4_0 = 2
+    Q4_1 = 3
+    Q5_0 = 4
+    Q5_1 = 5
+    Q8_0 = 6
+    Q8_1 = 7
+    Q2_K = 8
+    Q3_K = 9
+    Q4_K = 10
+    Q5_K = 11
+    Q6_K = 12
+    Q8_K = 13
+    I8 = 14
+    I16 = 15
+    I32 = 16
+
+
+def map_type(ggml_type):
+    """TransformerBase.MapType (TransformerBase.cs:558-575): GGUF tensor type ->
+    DataType, through the library; NotImplementedError where MapType throws
+    NotSupportedException."""
+    dt = nat.lib().aih_datatype_from_type(int(ggml_type))
+    if dt < 0:
+        raise NotImplementedError("Unsupported tensor type: %d" % int(ggml_type))
+    return DataType(dt)
+
+
+def gguf_type(dtype):
+    """The ggml id the operators take for a type: a DataType is translated
+    by the library (aih_type_from_datatype); a GGUFTensorType or a plain int
+    is already one."""
+    if isinstance(dtype, DataType):
+        t = nat.lib().aih_type_from_datatype(int(dtype))
+        if t < 0:
+            raise NotImplementedError("DataType %s has no GGUF tensor type" % dtype.name)
+        return t
+    return int(dtype)
+
+
+def data_type(dtype):
+    """A DataType for a DataType or a ggml id (GGUFTensorType or int)."""
+    return dtype if isinstance(dtype, DataType) else map_type(dtype)
 
 
 class InsufficientVramException(MemoryError):
@@ -41,9 +91,11 @@ class InsufficientVramException(MemoryError):
 
 
 def row_bytes(dtype, k):
-    rb = int(nat.lib().aih_row_bytes(int(dtype), int(k)))
+    """GGUFTensorInfo.SizeInBytes of one row of k elements (dtype: a DataType
+    or a ggml id)."""
+    rb = int(nat.lib().aih_row_bytes(gguf_type(dtype), int(k)))
     if rb < 0:
-        raise ValueError("K=%d is not a whole number of %s blocks" % (k, DataType(dtype).name))
+        raise ValueError("K=%d is not a whole number of %s blocks" % (k, data_type(dtype).name))
     return rb
 
 
@@ -63,7 +115,7 @@ class HipComputeBuffer:
     def __init__(self, device, size, element_type=DataType.F32):
         self.device = device
         self.size = int(size)
-        self.element_type = DataType(element_type)
+        self.element_type = data_type(element_type)
         ptr = ctypes.c_void_p()
         st = nat.lib().aih_malloc(device.handle, ctypes.c_size_t(self.size), ctypes.byref(ptr))
         if st == nat.HIP_ERROR_OUT_OF_MEMORY:
@@ -147,10 +199,13 @@ class HipComputeDevice:
 
 
 class Tensor:
-    """Buffer + shape + data type.  Quantized weights use GGUF dims [K, N]."""
+    """Buffer + shape + DataType (the reference's numbering; a ggml id given
+    here is mapped as TransformerBase.MapType does).  Quantized weights use
+    GGUF dims [K, N]."""
 
     def __init__(self, buffer, shape, dtype, name=None):
-        self.buffer, self.shape, self.dtype, self.name = buffer, tuple(int(s) for s in shape), DataType(dtype), name
+        self.buffer, self.shape, self.name = buffer, tuple(int(s) for s in shape), name
+        self.dtype = data_type(dtype)
 
     @property
     def total_elements(self):
@@ -164,7 +219,7 @@ class Tensor:
         n = 1
         for s in shape:
             n *= int(s)
-        dtype = DataType(dtype)
+        dtype = data_type(dtype)
         if dtype != DataType.F32:
             # Tensor.GetDataTypeSize throws for block types (Tensor.cs:138-149)
             raise NotImplementedError("Tensor.create supports F32 only; wrap quantized buffers instead")
@@ -179,8 +234,10 @@ class Tensor:
 
     @staticmethod
     def from_quantized(device, packed, k, n, dtype, name=None):
-        """Upload packed GGUF blocks verbatim as a [K, N] weight (row n = K/QK blocks)."""
+        """Upload packed GGUF blocks verbatim as a [K, N] weight (row n = K/QK
+        blocks); dtype is a DataType or a ggml id."""
         packed = np.ascontiguousarray(packed, dtype=np.uint8)
+        dtype = data_type(dtype)
         if packed.nbytes != n * row_bytes(dtype, k):
             raise ValueError("packed size %d != N*row_bytes = %d" % (packed.nbytes, n * row_bytes(dtype, k)))
         buf = device.create_buffer(packed.nbytes, dtype)
@@ -217,7 +274,7 @@ class ComputeOps:
             raise NotImplementedError("DequantizeInto not supported for F32")
         if target.total_elements < quantized.total_elements:
             raise ValueError("target too small")
-        nat.check(nat.lib().aih_dequantize(self.device.handle, int(quantized.dtype),
+        nat.check(nat.lib().aih_dequantize(self.device.handle, gguf_type(quantized.dtype),
                                            quantized.buffer.get_pointer(), target.buffer.get_pointer(),
                                            ctypes.c_uint64(quantized.total_elements), int(f16_mode)),
                   "aih_dequantize")
@@ -233,7 +290,7 @@ class ComputeOps:
         if b.dtype == DataType.F32:
             raise NotImplementedError("F32 weights are not on the HIP quantized path")
         result = Tensor.create(self.device, (m, n), DataType.F32, name)
-        nat.check(nat.lib().aih_matmul_weights_q(self.device.handle, int(b.dtype), b.buffer.get_pointer(),
+        nat.check(nat.lib().aih_matmul_weights_q(self.device.handle, gguf_type(b.dtype), b.buffer.get_pointer(),
                                                  n, k, a.buffer.get_pointer(), m, result.buffer.get_pointer()),
                   "aih_matmul_weights_q")
         return result
@@ -248,11 +305,12 @@ def fill_normal(seed, n, mean=0.0, std=1.0):
 
 
 def quantize(dtype, values, n_rows, k):
-    """Quantize n_rows x k float32 values into packed GGUF blocks (uint8)."""
+    """Quantize n_rows x k float32 values into packed GGUF blocks (uint8);
+    dtype is a DataType or a ggml id."""
     v = np.ascontiguousarray(values, dtype=np.float32).reshape(-1)
     if v.size != n_rows * k:
         raise ValueError("expected %d values" % (n_rows * k))
     out = np.empty(int(n_rows) * row_bytes(dtype, k), dtype=np.uint8)
-    nat.check(nat.lib().aih_host_quantize(int(dtype), v.ctypes.data, out.ctypes.data, int(n_rows), int(k)),
+    nat.check(nat.lib().aih_host_quantize(gguf_type(dtype), v.ctypes.data, out.ctypes.data, int(n_rows), int(k)),
               "aih_host_quantize")
     return out

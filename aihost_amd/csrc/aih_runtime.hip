@@ -354,6 +354,32 @@ const char *aih_strerror(int status)
     return "unknown aihost_hip status";
 }
 
+// GGUFTensorType -> DataType as TransformerBase.MapType does
+// (TransformerBase.cs:558-575); the DataType ordinals are the declaration
+// order of IComputeBuffer.cs:57-75.
+namespace {
+struct TypePair { int ggml, dt; };
+constexpr TypePair kTypeMap[] = {
+    {0, AIH_DT_F32},   {1, AIH_DT_F16},   {2, AIH_DT_Q4_0},  {3, AIH_DT_Q4_1},  {6, AIH_DT_Q5_0},
+    {7, AIH_DT_Q5_1},  {8, AIH_DT_Q8_0},  {9, AIH_DT_Q8_1},  {10, AIH_DT_Q2_K}, {11, AIH_DT_Q3_K},
+    {12, AIH_DT_Q4_K}, {13, AIH_DT_Q5_K}, {14, AIH_DT_Q6_K}, {15, AIH_DT_Q8_K},
+};
+}  // namespace
+
+int aih_datatype_from_type(int ggml_type)
+{
+    for (const TypePair &p : kTypeMap)
+        if (p.ggml == ggml_type) return p.dt;
+    return AIH_E_UNSUPPORTED;
+}
+
+int aih_type_from_datatype(int datatype)
+{
+    for (const TypePair &p : kTypeMap)
+        if (p.dt == datatype) return p.ggml;
+    return AIH_E_UNSUPPORTED;
+}
+
 int64_t aih_row_bytes(int type, int64_t k)
 {
     aih_block_geom g = aih_geom(type);

@@ -46,11 +46,38 @@ extern "C" {
 #define AIH_E_NO_DEVICE     -6  /* no HIP device at that index                */
 
 /* ---- ggml tensor types handled on this path ---------------------------- */
+/* The operators take GGUFTensorType / ggml ids (GGUFValueType.cs:26-56), the
+ * numbering of the file's tensor infos. */
 #define AIH_TYPE_F32   0
 #define AIH_TYPE_Q4_0  2
 #define AIH_TYPE_Q8_0  8
 #define AIH_TYPE_Q4_K 12
 #define AIH_TYPE_Q6_K 14
+
+/* ---- the reference's operator-level type: DataType --------------------- */
+/* A reference Tensor carries DataType (Tensor.cs:12), whose ordinals
+ * (AIHost/AIHost/ICompute/IComputeBuffer.cs:57-75) are NOT the ggml ids:
+ * DataType.Q8_0 = 6, Q4_K = 10, Q6_K = 12 while the ggml ids 8, 10, 12 are
+ * Q8_0, Q2_K, Q4_K.  Translate with aih_type_from_datatype before calling an
+ * operator; passing a DataType ordinal as a type would read Q6_K blocks as
+ * Q4_K. */
+#define AIH_DT_F32   0
+#define AIH_DT_F16   1
+#define AIH_DT_Q4_0  2
+#define AIH_DT_Q4_1  3
+#define AIH_DT_Q5_0  4
+#define AIH_DT_Q5_1  5
+#define AIH_DT_Q8_0  6
+#define AIH_DT_Q8_1  7
+#define AIH_DT_Q2_K  8
+#define AIH_DT_Q3_K  9
+#define AIH_DT_Q4_K 10
+#define AIH_DT_Q5_K 11
+#define AIH_DT_Q6_K 12
+#define AIH_DT_Q8_K 13
+#define AIH_DT_I8   14
+#define AIH_DT_I16  15
+#define AIH_DT_I32  16
 
 /* ---- fp16 scale decoding modes for aih_dequantize ---------------------- */
 /* IEEE: the reference's GPU decoder, QuantizationFormats.cs:147-152
@@ -130,6 +157,19 @@ int aih_memcpy_d2d(aih_ctx *ctx, void *dst, const void *src, size_t bytes);
 int aih_upload_tensor(aih_ctx *ctx, void *dst, const void *host_src, size_t bytes);
 
 /* ---- operators (ComputeOps, AIHost/AIHost/Compute/ComputeOps.cs) ------- */
+
+/* TransformerBase.MapType (AIHost/AIHost/Compute/TransformerBase.cs:558-575):
+ * the DataType ordinal of a GGUF tensor type, for the fourteen types MapType
+ * maps (F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q8_1, Q2_K .. Q8_K);
+ * AIH_E_UNSUPPORTED for any other value (where MapType throws
+ * NotSupportedException).  Needs no context and no device. */
+int aih_datatype_from_type(int ggml_type);
+
+/* The inverse: the ggml id that the operators take for a reference DataType
+ * ordinal; AIH_E_UNSUPPORTED for I8/I16/I32 and out-of-range values.  The
+ * operators themselves then reject the types this path does not compute on.
+ * Needs no context and no device. */
+int aih_type_from_datatype(int datatype);
 
 /* Bytes of one row of k elements of `type`, or a negative status.
  * (GGUFTensorInfo.SizeInBytes, AIHost/AIHost/GGUF/GGUFTensorInfo.cs:51-78.) */

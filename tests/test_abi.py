@@ -87,3 +87,46 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(nat, "LIB_PATH", str(tmp_path / "nope.so"))
     with pytest.raises(OSError):
         nat.lib()
+
+
+# TransformerBase.MapType (TransformerBase.cs:558-575), written out by name:
+# GGUFTensorType ids (GGUFValueType.cs:26-56) and the DataType members
+# (IComputeBuffer.cs:57-75) in their declaration order.
+DATATYPE_ORDER = ["F32", "F16", "Q4_0", "Q4_1", "Q5_0", "Q5_1", "Q8_0", "Q8_1", "Q2_K", "Q3_K", "Q4_K", "Q5_K",
+                  "Q6_K", "Q8_K", "I8", "I16", "I32"]
+GGUF_IDS = {"F32": 0, "F16": 1, "Q4_0": 2, "Q4_1": 3, "Q5_0": 6, "Q5_1": 7, "Q8_0": 8, "Q8_1": 9, "Q2_K": 10,
+            "Q3_K": 11, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "Q8_K": 15}
+
+
+def test_datatype_mapping_is_maptype():
+    L = nat.lib()
+    for name, gid in GGUF_IDS.items():
+        dt = DATATYPE_ORDER.index(name)
+        assert L.aih_datatype_from_type(gid) == dt, name
+        assert L.aih_type_from_datatype(dt) == gid, name
+    # MapType throws for every other GGUF type; DataType I8/I16/I32 have no GGUF tensor type here
+    for gid in [4, 5] + list(range(16, 40)) + [-1]:
+        assert L.aih_datatype_from_type(gid) == nat.AIH_E_UNSUPPORTED, gid
+    for dt in (14, 15, 16, 17, -1):
+        assert L.aih_type_from_datatype(dt) == nat.AIH_E_UNSUPPORTED, dt
+
+
+def test_reference_datatypes_reach_the_right_format():
+    # The ordinals a reference Tensor carries for this path's formats are
+    # ggml ids of other formats (8 = Q8_0 but DataType Q2_K; 12 = Q4_K but
+    # DataType Q6_K).  Through the mapping they select the right block
+    # geometry: a Q6_K row is never sized (and so never read) as Q4_K.
+    from aihost_amd import compute as C
+    L = nat.lib()
+    assert [C.DataType.Q4_0, C.DataType.Q8_0, C.DataType.Q4_K, C.DataType.Q6_K] == [2, 6, 10, 12]
+    for dt, gid, rb in ((C.DataType.Q8_0, nat.Q8_0, 272), (C.DataType.Q4_K, nat.Q4_K, 144),
+                        (C.DataType.Q6_K, nat.Q6_K, 210), (C.DataType.Q4_0, nat.Q4_0, 144)):
+        assert L.aih_type_from_datatype(int(dt)) == gid
+        assert C.row_bytes(dt, 256) == rb
+        assert C.gguf_type(dt) == gid
+        assert C.map_type(gid) == dt
+    assert L.aih_row_bytes(int(C.DataType.Q6_K), 256) == 144   # the raw ordinal would be read as Q4_K
+    with pytest.raises(NotImplementedError):
+        C.gguf_type(C.DataType.I8)
+    with pytest.raises(NotImplementedError):
+        C.map_type(23)   # IQ4_XS

@@ -210,21 +210,32 @@ def test_linearity_at_full_size(device, batch_path):
         assert_close(ya[0], y1[0], 1e-5)             # matrix-core and dot-product kernels agree
 
 
-def test_compute_ops_mirror(device, orc):
+@pytest.mark.parametrize("dt", ["Q4_0", "Q8_0", "Q4_K", "Q6_K"])
+def test_compute_ops_mirror(device, orc, dt):
+    # Tensors carry the reference's DataType numbering (Q8_0 = 6, Q4_K = 10,
+    # Q6_K = 12); ComputeOps translates it through aih_type_from_datatype, so
+    # every format reaches its own kernels (a raw DataType.Q6_K would be read
+    # as Q4_K blocks).
     ops = C.ComputeOps(device)
+    dtype = C.DataType[dt]
+    qtype = C.gguf_type(dtype)
     n, k = 300, 2048
-    wq = synth_weight(nat.Q4_K, n, k)
-    w = C.Tensor.from_quantized(device, wq, k, n, C.DataType.Q4_K)
-    x = x_of(k, 2)
-    a = C.Tensor.from_data(device, x)
-    y = ops.matmul_weights(a, w)
-    assert y.shape == (2, n)
-    assert_close(y.read(), orc.matvec(nat.Q4_K, wq, n, k, x), TOL)
+    wq = synth_weight(qtype, n, k)
+    w = C.Tensor.from_quantized(device, wq, k, n, dtype)
+    assert w.dtype == dtype
+    for m in (2, 12):     # the matvec (M <= 8) and the GEMM (M > 8)
+        x = x_of(k, m)
+        a = C.Tensor.from_data(device, x)
+        y = ops.matmul_weights(a, w)
+        assert y.shape == (m, n)
+        assert_close(y.read(), orc.matvec(qtype, wq, n, k, x), TOL if m <= 8 else 1e-3)
+        for t in (a, y):
+            t.dispose()
     f = ops.dequantize(w)
-    assert np.array_equal(f.read().reshape(-1), orc.dequantize(nat.Q4_K, wq, n * k))
+    assert np.array_equal(f.read().reshape(-1), orc.dequantize(qtype, wq, n * k))
     with pytest.raises(ValueError):
         ops.matmul_weights(C.Tensor.from_data(device, x_of(k // 2, 1)), w)
-    for t in (w, a, y, f):
+    for t in (w, f):
         t.dispose()
 
 

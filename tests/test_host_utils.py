@@ -40,8 +40,8 @@ def test_fill_normal_definition_and_stats():
     assert not np.array_equal(C.fill_normal(1, 16), C.fill_normal(2, 16))
 
 
-@pytest.mark.parametrize("dtype,rel_rms", [(C.DataType.Q8_0, 0.01), (C.DataType.Q4_0, 0.15),
-                                           (C.DataType.Q4_K, 0.12), (C.DataType.Q6_K, 0.03)])
+@pytest.mark.parametrize("dtype,rel_rms", [(C.GGUFTensorType.Q8_0, 0.01), (C.GGUFTensorType.Q4_0, 0.15),
+                                           (C.GGUFTensorType.Q4_K, 0.12), (C.GGUFTensorType.Q6_K, 0.03)])
 def test_quantize_round_trip(orc, dtype, rel_rms):
     n, k = 32, 512
     x = C.fill_normal(5, n * k, 0.0, 0.02)
@@ -55,7 +55,7 @@ def test_quantize_round_trip(orc, dtype, rel_rms):
 def test_q8_0_error_bound_and_scale_rounding(orc):
     n, k = 16, 256
     x = C.fill_normal(9, n * k, 0.0, 1.0)
-    q = C.quantize(C.DataType.Q8_0, x, n, k).reshape(-1, 34)
+    q = C.quantize(C.GGUFTensorType.Q8_0, x, n, k).reshape(-1, 34)
     xb = x.reshape(-1, 32)
     d_expect = (np.abs(xb).max(1) / np.float32(127)).astype(np.float32).astype(np.float16)
     assert np.array_equal(q[:, 0:2].copy().view(np.uint16)[:, 0], d_expect.view(np.uint16))
@@ -68,14 +68,14 @@ def test_q8_0_error_bound_and_scale_rounding(orc):
 def test_q6_k_scales_are_subnormal_at_small_sigma():
     # N(0, 0.02) weights give Q6_K super-scales below 2^-14 (fp16 subnormal)
     x = C.fill_normal(42, 64 * 256, 0.0, 0.02)
-    q = C.quantize(C.DataType.Q6_K, x, 64, 256).reshape(-1, 210)
+    q = C.quantize(C.GGUFTensorType.Q6_K, x, 64, 256).reshape(-1, 210)
     d = q[:, 208:210].copy().view(np.uint16)[:, 0]
     assert np.all((d & 0x7C00) == 0) and np.all((d & 0x3FF) != 0)
 
 
 def test_quantize_rejects_bad_shapes():
     with pytest.raises(ValueError):
-        C.quantize(C.DataType.Q4_K, np.zeros(100, np.float32), 1, 100)
+        C.quantize(C.GGUFTensorType.Q4_K, np.zeros(100, np.float32), 1, 100)
     with pytest.raises(ValueError):
-        C.row_bytes(C.DataType.Q6_K, 300)
-    assert C.row_bytes(C.DataType.Q4_K, 4096) == 2304
+        C.row_bytes(C.GGUFTensorType.Q6_K, 300)
+    assert C.row_bytes(C.GGUFTensorType.Q4_K, 4096) == 2304

@@ -115,7 +115,7 @@ def test_argmax_first_index_and_nan():
 def test_embed_rows_are_dequantized_rows():
     from aihost_amd import compute as C
     vocab, dim = 7, 256
-    q = C.quantize(C.DataType.Q4_K, C.fill_normal(9, vocab * dim, 0.0, 0.02), vocab, dim)
+    q = C.quantize(C.GGUFTensorType.Q4_K, C.fill_normal(9, vocab * dim, 0.0, 0.02), vocab, dim)
     e = ol.embed(orc.Q4_K, q, vocab, dim, [3, 0, 6, 9, -1])
     full = orc.dequantize(orc.Q4_K, q, vocab * dim).reshape(vocab, dim)
     assert np.array_equal(e[:3], full[[3, 0, 6]]) and not e[3:].any()

@@ -248,6 +248,10 @@ class LlamaDecoder:
         self.scale = float(np.float32(1.0) / np.sqrt(np.float32(c.head_dim)))
         nat.check(self.L.aih_rope_table(self.h, self.table, self.max_len, c.head_dim, c.theta), "aih_rope_table")
         self.n_prompt = 0
+        # host mirror of the device position: the next decode step runs at
+        # this position (prefill sets it to the prompt length, every decode
+        # step advances it, as the argmax step advances *pos on the device)
+        self.position = 0
         self.graph = None
         # The SiLU-pairs epilogue pairs the row teams of a workgroup: 8 teams
         # for widths up to 4096, 4 up to 8192, 2 up to 16384; the fused gate|up
@@ -355,6 +359,7 @@ class LlamaDecoder:
         p = np.array([n - 1], dtype=np.int32)
         nat.check(self.L.aih_memcpy_h2d(self.h, self.pos, p.ctypes.data, 4), "pos")
         self.n_prompt = n
+        self.position = n
         self.head(self.x + (n - 1) * c.dim * 4, self.pos, n - 1)
         return self.read_token() if read else None
 
@@ -384,16 +389,23 @@ class LlamaDecoder:
 
     def decode(self, steps, use_graph=True):
         """Run `steps` greedy decode steps on the device; returns nothing (the
-        tokens accumulate in the device history, see tokens())."""
-        if self.n_prompt + steps > self.max_len:
-            raise ValueError("decode past max_len")
+        tokens accumulate in the device history, see tokens()).  Raises
+        ValueError, before anything runs, when the steps would pass max_len,
+        counting the steps already decoded since the last prefill."""
+        if self.n_prompt == 0:
+            raise ValueError("decode before prefill")
+        if steps < 0 or self.position + steps > self.max_len:
+            raise ValueError("decode of %d steps from position %d passes max_len %d"
+                             % (steps, self.position, self.max_len))
         if use_graph:
             g = self.capture()
             for _ in range(steps):
                 nat.check(self.L.aih_graph_launch(self.h, g), "aih_graph_launch")
+                self.position += 1
         else:
             for _ in range(steps):
                 self.decode_step()
+                self.position += 1
 
     def read_token(self):
         t = np.empty(1, dtype=np.int32)

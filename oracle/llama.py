@@ -37,7 +37,16 @@ preservation, composition of rotations and a hand-computed pair rotation,
 attention with one key, equal keys, causality and the GQA head mapping,
 SiLU at known points, argmax ties -- each chosen so that a plausible slip
 (half-split instead of interleaved pairs, a missing scale, a wrong KV head,
-an off-by-one mask) fails one of them.
+an off-by-one mask) fails one of them.  The composition in Model.forward is
+pinned by special cases with closed forms: W_o = W_down = 0 makes every
+layer the identity (logits = head(rmsnorm(embedding))); one token at
+position 0 makes attention return V of the grouped KV head, so a layer is
+written out by hand; zero gate weights remove the FFN exactly; the cached K
+rows of one token at two positions are the same complex pairs turned by the
+position difference, V rows equal; swapping two earlier tokens changes a
+one-layer model's last row only through RoPE.  Planted slips (a dropped
+residual, swapped norm weights, RoPE after the cache store, a rotated V,
+gate and up swapped, no output norm) each fail at least one of them.
 """
 import numpy as np
 
@@ -132,18 +141,24 @@ class Model:
         self._deq = {}
 
     def mat(self, name):
-        """Dequantized [out, in] matrix of a quantized weight (cached)."""
-        if name not in self._deq:
-            qtype, data, n, k = self.w[name]
-            self._deq[name] = orc.dequantize(qtype, data, n * k).reshape(n, k)
-        return self._deq[name]
+        """Dequantized [out, in] matrix of a quantized weight, held as float64
+        (exact: every dequantized value is a float32).  Cached per packed
+        array, so layers that share one array (synthetic models with a few
+        distinct layer sets) share one matrix."""
+        qtype, data, n, k = self.w[name]
+        key = id(data)
+        if key not in self._deq:
+            m = orc.dequantize(qtype, data, n * k).reshape(n, k).astype(np.float64)
+            self._deq[key] = (data, m)          # the array is kept, so its id stays unique
+        return self._deq[key][1]
 
     def vec(self, name):
         """A fp32 weight vector (norm weights)."""
         return np.asarray(self.w[name][1], dtype=f32).reshape(-1)
 
     def matmul(self, name, x):
-        return (np.asarray(x, dtype=np.float64) @ self.mat(name).T.astype(np.float64)).astype(f32)
+        """x @ W^T in float64, rounded once to float32."""
+        return (np.asarray(x, dtype=np.float64) @ self.mat(name).T).astype(f32)
 
     def forward(self, ids, start, kv, table, last_only=True):
         """Embed ids at positions start.., run every layer (appending to the

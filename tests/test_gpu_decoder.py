@@ -119,5 +119,12 @@ def test_limits(device, model):
         dec.prefill(np.zeros(16, np.int32))
         with pytest.raises(ValueError):
             dec.decode(5)
+        dec.decode(2, use_graph=False)        # positions 16, 17
+        with pytest.raises(ValueError):       # steps already decoded count
+            dec.decode(3)
+        dec.decode(2)                         # positions 18, 19: the last cache row
+        with pytest.raises(ValueError):
+            dec.decode(1, use_graph=False)
+        assert dec.position == 20
     finally:
         dec.dispose()

@@ -143,3 +143,163 @@ def test_oracle_forward_incremental_equals_full_prefill():
         step = m.forward([ids[i]], i, kv, table)
     assert np.allclose(step, full, rtol=1e-5, atol=1e-6)
     assert full.shape == (1, cfg.vocab)
+
+
+# -- composition of Model.forward (ComputeOps.TransformerLayer, ComputeOps.cs:
+# 1250-1356, then TransformerBase.ForwardHead, TransformerBase.cs:168-191),
+# pinned by special cases with closed forms.  The expected values below are
+# written from the definitions (mean-square normalisation, the GQA head
+# expansion, the SiLU), not through the oracle's operators.
+
+def _small_model(seed, n_layers=2):
+    from aihost_amd import llama
+    cfg = llama.LlamaConfig(n_layers=n_layers, dim=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=512, vocab=48)
+    w = dict(llama.synth_weights(cfg, seed=seed))
+    # norm weights well away from 1 and different per norm, so that a swapped
+    # or dropped norm weight changes the result
+    rng = np.random.default_rng(seed)
+    for name, (qt, a, r, c) in list(w.items()):
+        if qt == orc.F32:
+            w[name] = (qt, rng.uniform(0.5, 1.5, a.size).astype(np.float32), r, c)
+    return cfg, w
+
+
+def _zeroed(w, names):
+    out = dict(w)
+    for n in names:
+        qt, a, r, c = out[n]
+        out[n] = (qt, np.zeros_like(a), r, c)
+    return out
+
+
+def _run(cfg, w, ids, start=0, max_len=16, kv=None, model=None):
+    m = model or ol.Model(cfg, w)
+    if kv is None:
+        kv = [(np.zeros((max_len, cfg.kv_dim), np.float32), np.zeros((max_len, cfg.kv_dim), np.float32))
+              for _ in range(cfg.n_layers)]
+    return m.forward(list(ids), start, kv, ol.rope_table(max_len, cfg.head_dim, cfg.theta), last_only=False), m
+
+
+def _deq(w, name):
+    qt, a, r, c = w[name]
+    return orc.dequantize(qt, a, r * c).reshape(r, c).astype(np.float64)
+
+
+def _norm(x, g, eps):
+    x = np.asarray(x, np.float64)
+    return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * np.asarray(g, np.float64)
+
+
+def _head(cfg, w, x):
+    return _norm(x, w["output_norm"][1], cfg.eps) @ _deq(w, "output").T
+
+
+def _embed_rows(w, ids):
+    return _deq(w, "token_embd")[list(ids)]
+
+
+def test_forward_zero_output_projections_is_identity_layers():
+    """W_o = W_down = 0: attention and FFN add nothing, so every layer passes
+    x through and the logits are head(rmsnorm(embedding)).  A missing
+    residual (x replaced by the sublayer output) gives zero logits; a
+    missing output norm or the wrong norm weight changes them."""
+    cfg, w = _small_model(21)
+    w = _zeroed(w, ["blk.%d.%s" % (l, s) for l in range(cfg.n_layers) for s in ("attn_output", "ffn_down")])
+    ids = [5, 0, 47, 12]
+    got, _ = _run(cfg, w, ids)
+    want = _head(cfg, w, _embed_rows(w, ids))
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-5 * np.abs(want).max())
+
+
+def test_forward_single_token_attention_returns_v():
+    """One token at position 0: each head's only visible key is its own, the
+    softmax weight is 1, and attention returns the cached V row of the KV
+    head h // (n_heads / n_kv_heads) -- Q, K and RoPE drop out.  With the
+    FFN written out (SiLU(gate) * up, down, residual), one layer has a closed
+    form; two layers apply it twice.  Catches a swapped attn/ffn norm
+    weight, a wrong GQA head, a missing residual and V being rotated."""
+    cfg, w = _small_model(22)
+    x = _embed_rows(w, [7])
+    for l in range(cfg.n_layers):
+        p = "blk.%d." % l
+        v = _norm(x, w[p + "attn_norm"][1], cfg.eps) @ _deq(w, p + "attn_v").T
+        hd, group = cfg.head_dim, cfg.n_heads // cfg.n_kv_heads
+        a = np.concatenate([v[:, (h // group) * hd:(h // group + 1) * hd] for h in range(cfg.n_heads)], axis=1)
+        x = x + a @ _deq(w, p + "attn_output").T
+        xn = _norm(x, w[p + "ffn_norm"][1], cfg.eps)
+        g, u = xn @ _deq(w, p + "ffn_gate").T, xn @ _deq(w, p + "ffn_up").T
+        x = x + (g / (1.0 + np.exp(-g)) * u) @ _deq(w, p + "ffn_down").T
+    want = _head(cfg, w, x)
+    got, _ = _run(cfg, w, [7])
+    assert np.allclose(got, want, rtol=2e-5, atol=2e-5 * np.abs(want).max())
+    # and Q, K truly drop out: zeroing them changes nothing for one token
+    w0 = _zeroed(w, ["blk.%d.%s" % (l, s) for l in range(cfg.n_layers) for s in ("attn_q", "attn_k")])
+    assert np.array_equal(_run(cfg, w0, [7])[0], got)
+
+
+def test_forward_zero_gate_removes_the_ffn():
+    """Zero gate weights: SiLU(0) = 0, so the FFN adds exactly nothing, and
+    the result equals the model with W_down = 0 as well (for any prompt),
+    while W_up cannot matter.  With the attention also removed (W_o = 0) the
+    logits are head(rmsnorm(embedding)) again."""
+    cfg, w = _small_model(23)
+    ids = [3, 9, 9, 30, 1]
+    layers = range(cfg.n_layers)
+    wg = _zeroed(w, ["blk.%d.ffn_gate" % l for l in layers])
+    a, _ = _run(cfg, wg, ids)
+    b, _ = _run(cfg, _zeroed(wg, ["blk.%d.ffn_down" % l for l in layers]), ids)
+    c, _ = _run(cfg, _zeroed(wg, ["blk.%d.ffn_up" % l for l in layers]), ids)
+    assert np.array_equal(a, b) and np.array_equal(a, c)
+    full, _ = _run(cfg, w, ids)
+    assert not np.allclose(full, a, rtol=1e-3)                       # the FFN does contribute normally
+    d, _ = _run(cfg, _zeroed(wg, ["blk.%d.attn_output" % l for l in layers]), ids)
+    want = _head(cfg, w, _embed_rows(w, ids))
+    assert np.allclose(d, want, rtol=1e-5, atol=1e-5 * np.abs(want).max())
+
+
+def test_forward_caches_rotated_keys_and_plain_values():
+    """Layer 0's input for a token is its embedding wherever it stands, so
+    the cached rows of one token at positions 0 and 3 are related in closed
+    form: V rows equal, and each K pair (2i, 2i+1), read as a complex
+    number, turned by the angle 3 * theta^(-2i/head_dim).  Catches K stored
+    before RoPE (rows equal), V rotated, RoPE at the wrong position and
+    half-split pairs."""
+    cfg, w = _small_model(24, n_layers=1)
+    ids = [17, 2, 30, 17]
+    max_len = 8
+    kv = [(np.zeros((max_len, cfg.kv_dim), np.float32), np.zeros((max_len, cfg.kv_dim), np.float32))]
+    ol.Model(cfg, w).forward(ids, 0, kv, ol.rope_table(max_len, cfg.head_dim, cfg.theta))
+    K, V = kv[0]
+    assert np.array_equal(V[0], V[3]) and not np.array_equal(V[0], V[1])
+    assert not np.allclose(K[0], K[3])
+    hd = cfg.head_dim
+    ang = 3.0 * cfg.theta ** (-np.arange(hd // 2) * 2.0 / hd)
+    k0 = K[0].astype(np.float64).reshape(cfg.n_kv_heads, hd // 2, 2)
+    k3 = K[3].astype(np.float64).reshape(cfg.n_kv_heads, hd // 2, 2)
+    z0, z3 = k0[..., 0] + 1j * k0[..., 1], k3[..., 0] + 1j * k3[..., 1]
+    assert np.allclose(z3, z0 * np.exp(1j * ang), atol=2e-6 * np.abs(z0).max())
+    assert not K[4:].any() and not V[4:].any()           # nothing past the prompt is written
+
+
+def test_forward_last_row_sees_key_order_through_rope():
+    """One layer: without RoPE the last query's attention is a function of
+    the set of earlier keys, so swapping the first two tokens could not
+    change the last row.  With RoPE it does."""
+    cfg, w = _small_model(26, n_layers=1)
+    a, m = _run(cfg, w, [4, 40, 11, 2])
+    b, _ = _run(cfg, w, [40, 4, 11, 2], model=m)
+    assert not np.allclose(a[-1], b[-1], rtol=1e-4)
+
+
+def test_forward_prefill_rows_equal_incremental_rows():
+    """Every row of a multi-token forward (last_only=False) equals the
+    logits of the same position decoded one token at a time."""
+    cfg, w = _small_model(25)
+    ids = [8, 1, 44, 20]
+    full, m = _run(cfg, w, ids, max_len=8)
+    kv = [(np.zeros((8, cfg.kv_dim), np.float32), np.zeros((8, cfg.kv_dim), np.float32))
+          for _ in range(cfg.n_layers)]
+    table = ol.rope_table(8, cfg.head_dim, cfg.theta)
+    for i, t in enumerate(ids):
+        row = m.forward([t], i, kv, table)
+        assert np.allclose(row[0], full[i], rtol=1e-5, atol=1e-5 * np.abs(full[i]).max()), i

@@ -18,6 +18,8 @@ AIH_E_NOT_GFX950 = -3
 AIH_E_NOT_ALLOCATED = -4
 AIH_E_LIMIT = -5
 AIH_E_NO_DEVICE = -6
+AIH_E_SCRATCH = -7
+NOALLOC_SCRATCH_BYTES = 16 << 20      # AIH_NOALLOC_SCRATCH_BYTES
 HIP_ERROR_OUT_OF_MEMORY = 2
 
 F32, Q4_0, Q8_0, Q4_K, Q6_K = 0, 2, 8, 12, 14
@@ -67,6 +69,7 @@ SIGNATURES = {
     "aih_qmatvec_fused": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _vp, _f, _i, _i, _vp]),
     "aih_qgemm": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),
     "aih_matmul_weights_q": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),
+    "aih_matmul_weights_q_noalloc": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),
     "aih_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _i64, _i64, _f]),
     "aih_rope_table": (_i, [_vp, _vp, ctypes.c_int32, ctypes.c_int32, _f]),
     "aih_rope": (_i, [_vp, _vp, _i64, _vp, _i64, _i64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _vp, _vp,

@@ -54,6 +54,9 @@ struct aih_ctx {
     void *work = nullptr;
     size_t work_bytes = 0;
     std::vector<void *> work_retired;
+    // Device address of this GPU's static staging buffer (the allocation-free
+    // entry point's), set by aih_init.
+    void *noalloc_scratch = nullptr;
 };
 
 // Device workspace of at least `bytes` on the context's device.  Growing it
@@ -61,6 +64,17 @@ struct aih_ctx {
 // (AIH_E_LIMIT): run the operation once outside the capture first.  Returns
 // AIH_OK or a status.
 int aih_workspace(aih_ctx *ctx, size_t bytes, void **out);
+
+// Staging memory a caller supplies in place of the context workspace (the
+// allocation-free entry point passes its static device buffer).
+struct aih_scratch {
+    void *ptr;
+    size_t bytes;
+};
+
+// Staging memory of at least `bytes`: `ext` when given (AIH_E_SCRATCH when it
+// is smaller; nothing is allocated), else the context workspace.
+int aih_stage(aih_ctx *ctx, const aih_scratch *ext, size_t bytes, void **out);
 
 #define AIH_TRY(expr)                                  \
     do {                                               \
@@ -78,12 +92,15 @@ static inline int aih_launch_status()
 // Kernel launch entry points implemented per source file.
 int aih_launch_dequant(aih_ctx *ctx, int type, const void *q, float *out,
                        uint64_t n_blocks, int f16_mode);
+// `ext`: staging memory to use instead of the context workspace (may be null).
 int aih_launch_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
-                       const float *X, int64_t ldx, float *Y, int64_t ldy, int batch);
+                       const float *X, int64_t ldx, float *Y, int64_t ldy, int batch,
+                       const aih_scratch *ext = nullptr);
 int aih_launch_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
-                     const float *X, int64_t M, float *Y);
+                     const float *X, int64_t M, float *Y, const aih_scratch *ext = nullptr);
 int aih_launch_qmatvec_mfma(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
-                            const float *X, int64_t ldx, float *Y, int64_t ldy, int batch);
+                            const float *X, int64_t ldx, float *Y, int64_t ldy, int batch,
+                            const aih_scratch *ext = nullptr);
 int aih_launch_qmatvec_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *X,
                              const float *X2, float eps, int pre, int post, float *Y);
 int aih_launch_embed(aih_ctx *ctx, int type, const void *table, int64_t vocab, int64_t dim,

@@ -256,14 +256,14 @@ int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t row_byt
 }  // namespace
 
 int aih_launch_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
-                     const float *X, int64_t M, float *Y)
+                     const float *X, int64_t M, float *Y, const aih_scratch *ext)
 {
     // K advances in 64-element steps.
     if (K % BK != 0) return AIH_E_LIMIT;
     if ((reinterpret_cast<uintptr_t>(X) & 15) != 0) return AIH_E_INVALID;
     const int64_t mpad = (M + 31) / 32 * 32;
     void *work = nullptr;
-    int rc = aih_workspace(ctx, (size_t)mpad * (size_t)K * sizeof(_Float16), &work);
+    int rc = aih_stage(ctx, ext, (size_t)mpad * (size_t)K * sizeof(_Float16), &work);
     if (rc) return rc;
     _Float16 *xh = static_cast<_Float16 *>(work);
     const int64_t nslots = mpad * K / 8;

@@ -1076,12 +1076,12 @@ int check_args(int64_t K, const void *W, const float *X, int64_t ldx)
 }  // namespace
 
 int aih_launch_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
-                       const float *X, int64_t ldx, float *Y, int64_t ldy, int batch)
+                       const float *X, int64_t ldx, float *Y, int64_t ldy, int batch, const aih_scratch *ext)
 {
     const int rc = check_args(K, W, X, ldx);
     if (rc) return rc;
     // Three or more columns: the MFMA kernel reads W once for all of them.
-    if (batch >= kMfmaMinBatch) return aih_launch_qmatvec_mfma(ctx, type, W, N, K, X, ldx, Y, ldy, batch);
+    if (batch >= kMfmaMinBatch) return aih_launch_qmatvec_mfma(ctx, type, W, N, K, X, ldx, Y, ldy, batch, ext);
     return dispatch(ctx, type, W, N, K, X, ldx, Y, ldy, batch, Fuse{nullptr, 0.f, kPreNone, kPostStore});
 }
 

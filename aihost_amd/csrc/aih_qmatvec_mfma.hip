@@ -41,7 +41,8 @@
 // (all columns) into LDS as hi/lo fp16 pieces, with the per-group scales and
 // the per-sub-block sums of x, and each lane loads, for its weight row, the
 // 8 codes of every 32-element window that its k-block covers.  Each workgroup
-// writes its 64 x batch partial sums to the context workspace; a second
+// writes its 64 x batch partial sums to the context workspace (or to the
+// staging memory the allocation-free entry point supplies); a second
 // kernel adds the splits in a fixed order (the result does not depend on
 // timing).  With one split the first kernel stores Y itself.
 //
@@ -540,7 +541,7 @@ split_sum_kernel(const float *__restrict__ P, int64_t np, int S, int batch, int6
 
 template <class U, int T>
 int launch_t(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
-             const float *X, int64_t ldx, float *Y, int64_t ldy, int batch)
+             const float *X, int64_t ldx, float *Y, int64_t ldy, int batch, const aih_scratch *ext)
 {
     const int64_t ntiles = (N + RWG - 1) / RWG;
     const int64_t nblk = K / U::kBlockElems;
@@ -557,10 +558,10 @@ int launch_t(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t row_b
     float *P = nullptr;
     if (S > 1) {
         void *ws = nullptr;
-        const int st = aih_workspace(ctx, (size_t)(S * batch * np) * sizeof(float), &ws);
+        const int st = aih_stage(ctx, ext, (size_t)(S * batch * np) * sizeof(float), &ws);
         if (st == AIH_OK) {
             P = static_cast<float *>(ws);
-        } else if (st == AIH_E_LIMIT) {
+        } else if (st == AIH_E_LIMIT && !ext) {
             // the workspace cannot grow during graph capture: one split per row tile
             S = 1;
             per = nunits;
@@ -591,24 +592,24 @@ int launch_t(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t row_b
 // 3..4 columns: four sub-blocks per column in the 16 MFMA rows; 5..8: two
 template <class U>
 int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
-           const float *X, int64_t ldx, float *Y, int64_t ldy, int batch)
+           const float *X, int64_t ldx, float *Y, int64_t ldy, int batch, const aih_scratch *ext)
 {
-    return batch <= 4 ? launch_t<U, 4>(ctx, W, N, K, row_bytes, X, ldx, Y, ldy, batch)
-                      : launch_t<U, 2>(ctx, W, N, K, row_bytes, X, ldx, Y, ldy, batch);
+    return batch <= 4 ? launch_t<U, 4>(ctx, W, N, K, row_bytes, X, ldx, Y, ldy, batch, ext)
+                      : launch_t<U, 2>(ctx, W, N, K, row_bytes, X, ldx, Y, ldy, batch, ext);
 }
 
 }  // namespace
 
 int aih_launch_qmatvec_mfma(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
-                            const float *X, int64_t ldx, float *Y, int64_t ldy, int batch)
+                            const float *X, int64_t ldx, float *Y, int64_t ldy, int batch, const aih_scratch *ext)
 {
     const int64_t rb = aih_row_bytes(type, K);
     const uint8_t *w = static_cast<const uint8_t *>(W);
     switch (type) {
-    case AIH_TYPE_Q4_K: return launch<UQ4K>(ctx, w, N, K, rb, X, ldx, Y, ldy, batch);
-    case AIH_TYPE_Q6_K: return launch<UQ6K>(ctx, w, N, K, rb, X, ldx, Y, ldy, batch);
-    case AIH_TYPE_Q8_0: return launch<UQ80>(ctx, w, N, K, rb, X, ldx, Y, ldy, batch);
-    case AIH_TYPE_Q4_0: return launch<UQ40>(ctx, w, N, K, rb, X, ldx, Y, ldy, batch);
+    case AIH_TYPE_Q4_K: return launch<UQ4K>(ctx, w, N, K, rb, X, ldx, Y, ldy, batch, ext);
+    case AIH_TYPE_Q6_K: return launch<UQ6K>(ctx, w, N, K, rb, X, ldx, Y, ldy, batch, ext);
+    case AIH_TYPE_Q8_0: return launch<UQ80>(ctx, w, N, K, rb, X, ldx, Y, ldy, batch, ext);
+    case AIH_TYPE_Q4_0: return launch<UQ40>(ctx, w, N, K, rb, X, ldx, Y, ldy, batch, ext);
     default: return AIH_E_UNSUPPORTED;
     }
 }

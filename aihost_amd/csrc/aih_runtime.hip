@@ -5,9 +5,35 @@
 
 #include <cstring>
 #include <cstdio>
+#include <mutex>
 #include <new>
 
 namespace {
+
+// Staging memory of aih_matmul_weights_q_noalloc: one copy per GPU, created
+// with the code object.  Host code never uses this name as an address: each
+// device's copy is looked up once (hipGetSymbolAddress, with that device
+// current, in aih_init) and that pointer is passed to the kernels.
+static __device__ __align__(256) unsigned char scratch[AIH_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on `device` (the current device).
+int scratch_address(int device, void **out)
+{
+    if (device < 0 || device >= kMaxDevices) return AIH_E_LIMIT;
+    std::lock_guard<std::mutex> g(g_scratch_lock);
+    if (!g_scratch_ptr[device]) {
+        void *p = nullptr;
+        AIH_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return AIH_E_INVALID;
+        g_scratch_ptr[device] = p;
+    }
+    *out = g_scratch_ptr[device];
+    return AIH_OK;
+}
 
 int select_device(aih_ctx *ctx)
 {
@@ -74,6 +100,14 @@ int aih_workspace(aih_ctx *ctx, size_t bytes, void **out)
     return AIH_OK;
 }
 
+int aih_stage(aih_ctx *ctx, const aih_scratch *ext, size_t bytes, void **out)
+{
+    if (!ext) return aih_workspace(ctx, bytes, out);
+    if (bytes > ext->bytes || !ext->ptr) return AIH_E_SCRATCH;
+    *out = ext->ptr;
+    return AIH_OK;
+}
+
 extern "C" {
 
 int aih_abi_version(void) { return AIH_ABI_VERSION; }
@@ -95,6 +129,11 @@ int aih_init(int device_index, aih_ctx **out)
     if (!ctx) return (int)hipErrorOutOfMemory;
     ctx->device = device_index;
     ctx->cu_count = prop.multiProcessorCount;
+    const int src = scratch_address(device_index, &ctx->noalloc_scratch);
+    if (src != AIH_OK) {
+        delete ctx;
+        return src;
+    }
     hipError_t err = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     for (int i = 0; err == hipSuccess && i < aih_ctx::kStageSlots; ++i) {
         err = hipHostMalloc(&ctx->stage[i], aih_ctx::kStageBytes, hipHostMallocDefault);
@@ -348,6 +387,9 @@ const char *aih_strerror(int status)
     case AIH_E_NOT_ALLOCATED: return "pointer not allocated by this context (double free?)";
     case AIH_E_LIMIT: return "shape exceeds the kernel limits";
     case AIH_E_NO_DEVICE: return "no HIP device at that index";
+    case AIH_E_SCRATCH:
+        return "the operation needs more staging memory than the allocation-free entry point's static buffer "
+               "(AIH_NOALLOC_SCRATCH_BYTES): use aih_matmul_weights_q, or fewer rows per call";
     default: break;
     }
     if (status > 0) return hipGetErrorString((hipError_t)status);
@@ -421,8 +463,12 @@ int aih_qmatvec_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t 
     return aih_launch_qmatvec_fused(ctx, type, W, N, K, X, X2, eps, pre, post, Y);
 }
 
-int aih_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
-                const float *X, int64_t ldx, float *Y, int64_t ldy, int batch)
+}  // extern "C"
+
+namespace {
+
+int qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *X, int64_t ldx, float *Y,
+            int64_t ldy, int batch, const aih_scratch *ext)
 {
     if (!ctx) return AIH_E_INVALID;
     if (!aih_is_quant(type)) return AIH_E_UNSUPPORTED;
@@ -433,11 +479,11 @@ int aih_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
     if (!W || !X || !Y) return AIH_E_INVALID;
     int rc = select_device(ctx);
     if (rc) return rc;
-    return aih_launch_qmatvec(ctx, type, W, N, K, X, ldx, Y, ldy, batch);
+    return aih_launch_qmatvec(ctx, type, W, N, K, X, ldx, Y, ldy, batch, ext);
 }
 
-int aih_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
-              const float *X, int64_t M, float *Y)
+int qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *X, int64_t M, float *Y,
+          const aih_scratch *ext)
 {
     if (!ctx) return AIH_E_INVALID;
     if (!aih_is_quant(type)) return AIH_E_UNSUPPORTED;
@@ -447,14 +493,45 @@ int aih_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
     if (!W || !X || !Y) return AIH_E_INVALID;
     int rc = select_device(ctx);
     if (rc) return rc;
-    return aih_launch_qgemm(ctx, type, W, N, K, X, M, Y);
+    return aih_launch_qgemm(ctx, type, W, N, K, X, M, Y, ext);
+}
+
+int matmul_weights_q(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *X, int64_t M,
+                     float *Y, const aih_scratch *ext)
+{
+    if (M >= 1 && M <= 8) return qmatvec(ctx, type, W, N, K, X, K, Y, N, (int)M, ext);
+    return qgemm(ctx, type, W, N, K, X, M, Y, ext);
+}
+
+}  // namespace
+
+extern "C" {
+
+int aih_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
+                const float *X, int64_t ldx, float *Y, int64_t ldy, int batch)
+{
+    return qmatvec(ctx, type, W, N, K, X, ldx, Y, ldy, batch, nullptr);
+}
+
+int aih_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
+              const float *X, int64_t M, float *Y)
+{
+    return qgemm(ctx, type, W, N, K, X, M, Y, nullptr);
 }
 
 int aih_matmul_weights_q(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
                          const float *X, int64_t M, float *Y)
 {
-    if (M >= 1 && M <= 8) return aih_qmatvec(ctx, type, W, N, K, X, K, Y, N, (int)M);
-    return aih_qgemm(ctx, type, W, N, K, X, M, Y);
+    return matmul_weights_q(ctx, type, W, N, K, X, M, Y, nullptr);
+}
+
+int aih_matmul_weights_q_noalloc(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
+                                 const float *X, int64_t M, float *Y)
+{
+    if (!ctx) return AIH_E_INVALID;
+    // the device address of this GPU's static buffer, looked up in aih_init
+    const aih_scratch ext = {ctx->noalloc_scratch, AIH_NOALLOC_SCRATCH_BYTES};
+    return matmul_weights_q(ctx, type, W, N, K, X, M, Y, &ext);
 }
 
 }  // extern "C"

@@ -44,6 +44,8 @@ extern "C" {
 #define AIH_E_NOT_ALLOCATED -4  /* pointer not owned by this context (double free) */
 #define AIH_E_LIMIT         -5  /* shape beyond what the kernels support      */
 #define AIH_E_NO_DEVICE     -6  /* no HIP device at that index                */
+#define AIH_E_SCRATCH       -7  /* needs more staging memory than the static
+                                   buffer of aih_matmul_weights_q_noalloc  */
 
 /* ---- ggml tensor types handled on this path ---------------------------- */
 /* The operators take GGUFTensorType / ggml ids (GGUFValueType.cs:26-56), the
@@ -234,6 +236,23 @@ int aih_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
  * aih_qmatvec and larger M to aih_qgemm. */
 int aih_matmul_weights_q(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
                          const float *X, int64_t M, float *Y);
+
+/* aih_matmul_weights_q without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory -- code
+ * being captured into a HIP graph, tight serving loops, harnesses that forbid
+ * hipMalloc.  Same arguments, routing, kernels and results as
+ * aih_matmul_weights_q; the staging memory those kernels need (the partial
+ * sums of the 3..8-column matvec, the GEMM's fp16 copy of X: mpad * K * 2
+ * bytes, mpad = M rounded up to 32) comes from one static device buffer of
+ * AIH_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends, instead of
+ * the context workspace.  A call that needs more returns AIH_E_SCRATCH
+ * before launching anything (at K = 4096 the GEMM takes M up to 2048; at
+ * K = 14336, up to 576).  Every call on one GPU shares that buffer: calls
+ * that overlap on one GPU (two streams, two contexts, two threads) race and
+ * must be serialized by the caller.  Nothing in it has to start at zero. */
+#define AIH_NOALLOC_SCRATCH_BYTES (16u << 20)
+int aih_matmul_weights_q_noalloc(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
+                                 const float *X, int64_t M, float *Y);
 
 /* ---- decoder operators (the rest of a Llama layer around the matmuls) --
  *

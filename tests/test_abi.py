@@ -45,10 +45,12 @@ def test_binding_covers_header():
 def test_abi_version_and_strerror():
     L = nat.lib()
     assert L.aih_abi_version() == 1
-    for code in (0, -1, -2, -3, -4, -5, -6, 2, -99):
+    for code in (0, -1, -2, -3, -4, -5, -6, -7, 2, -99):
         s = nat.strerror(code)
         assert isinstance(s, str) and s
     assert "double free" in nat.strerror(nat.AIH_E_NOT_ALLOCATED)
+    assert "AIH_NOALLOC_SCRATCH_BYTES" in nat.strerror(nat.AIH_E_SCRATCH)
+    assert nat.strerror(-99) == "unknown aihost_hip status"
 
 
 def test_row_bytes():
@@ -65,6 +67,7 @@ def test_null_context_is_rejected():
     L = nat.lib()
     assert L.aih_qmatvec(None, nat.Q4_K, None, 1, 256, None, 256, None, 1, 1) == nat.AIH_E_INVALID
     assert L.aih_qgemm(None, nat.Q4_K, None, 1, 256, None, 16, None) == nat.AIH_E_INVALID
+    assert L.aih_matmul_weights_q_noalloc(None, nat.Q4_K, None, 1, 256, None, 16, None) == nat.AIH_E_INVALID
     assert L.aih_dequantize(None, nat.Q4_K, None, None, 256, 0) == nat.AIH_E_INVALID
     assert L.aih_malloc(None, 16, ctypes.byref(ctypes.c_void_p())) == nat.AIH_E_INVALID
     assert L.aih_free(None, None) == nat.AIH_E_INVALID

@@ -70,6 +70,7 @@ SIGNATURES = {
     "aih_qgemm": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),
     "aih_matmul_weights_q": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),
     "aih_matmul_weights_q_noalloc": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),
+    "aih_probe_stream_read": (_i, [_vp, _vp, _u64, _i, _vp]),
     "aih_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _i64, _i64, _f]),
     "aih_rope_table": (_i, [_vp, _vp, ctypes.c_int32, ctypes.c_int32, _f]),
     "aih_rope": (_i, [_vp, _vp, _i64, _vp, _i64, _i64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _vp, _vp,

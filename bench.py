@@ -6,14 +6,22 @@ Headline workload: Q4_K decode matvec, W = 14336 x 4096 (GGUF dims
 over one weight copy.  Weights are synthetic N(0, 0.02) (seed 42) quantized to
 Q4_K; x is N(0, 1) (seed 43).  Twelve copies of the weight (396 MB, more than
 the 256 MB Infinity Cache) are used in rotation so every step streams its
-weights from HBM.  Launches are captured once in a HIP graph (120 launches,
-ten passes over the copies) and the graph is replayed; the timed region is
-bracketed by stream synchronisation and HIP events on the library's stream.
-Within a graph the kernels run back to back; the gap between two graph
-replays (a few microseconds) is spread over 120 launches.
+weights from HBM.  Launches are captured once in a HIP graph of G launches
+over the copies (G = the largest divisor of --steps up to 120) and the timed
+region is exactly steps / G whole replays, bracketed by stream
+synchronisation and HIP events on the library's stream.  Within a graph the
+kernels run back to back; every launch pays the fixed cost of a kernel
+boundary (reported beside the result: the same grid launched with nothing to
+read).
 
 Algorithmic bytes per step: packed W (14336 * 2304 B) + x (4096 * 4 B) +
-y (14336 * 4 B) = 33,103,872 B.  value = those bytes / wall time per step.
+y (14336 * 4 B) = 33,103,872 B.  value = those bytes / wall time per step;
+roofline.achieved = those bytes / HIP-event time per launch.
+
+Arithmetic: the weight codes are multiplied exactly (v_dot4_i32_i8) with x
+held as three signed-byte limbs of a per-64-element fixed-point form, the
+products summed in int32; block scales, mins and the limb weights are applied
+in fp32 (normwise error against an fp64 product about 1e-6).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -33,8 +41,17 @@ METRIC = "quant matvec GB/s (% HBM peak) + decode tokens/s, Q4_K 4096x14336, 1 G
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK = 2.5e15     # dense fp16 MFMA FLOP/s
 COPIES = 12
-GRAPH_LAUNCHES = 120
+GRAPH_LAUNCHES = 120     # most launches per captured graph
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "qmatvec_q4k_14336x4096_b1_hbm_traffic.md")
+
+
+def graph_size(steps, cap=GRAPH_LAUNCHES):
+    """Launches per graph: the largest divisor of `steps` up to `cap`, so that
+    the timed region is a whole number of replays."""
+    for g in range(max(1, min(cap, steps)), 0, -1):
+        if steps % g == 0:
+            return g
+    return 1
 
 
 def algorithmic_bytes(qtype, n, k, batch):
@@ -43,13 +60,11 @@ def algorithmic_bytes(qtype, n, k, batch):
 
 
 class MatvecBench:
-    """Rotating weight copies + one captured graph of `launches` launches."""
+    """Rotating weight copies + one captured graph of `launches` calls."""
 
     def __init__(self, dev, qtype, n, k, batch, copies=COPIES, launches=GRAPH_LAUNCHES, seed_w=42, seed_x=43):
         from aihost_amd import _native as nat
         from aihost_amd import compute as C
-        if batch >= 3:
-            launches //= 2   # two kernels per call (splits, then their sum): same graph size
         self.nat, self.dev = nat, dev
         self.qtype, self.n, self.k, self.batch = qtype, n, k, batch
         self.packed = C.quantize(qtype, C.fill_normal(seed_w, n * k, 0.0, 0.02), n, k)
@@ -77,17 +92,23 @@ class MatvecBench:
                                         self.x.get_pointer(), self.k, self.y.get_pointer(), self.n, self.batch)
         self.nat.check(st, "aih_qmatvec")
 
-    def run(self, steps):
-        """Launch exactly `steps` matvecs (graph replays + a direct remainder)."""
+    def replay(self, n):
         L, h = self.nat.lib(), self.dev.handle
-        for _ in range(steps // self.launches):
+        for _ in range(n):
             self.nat.check(L.aih_graph_launch(h, self.graph), "aih_graph_launch")
-        for i in range(steps % self.launches):
-            self._launch(self.w[i % self.copies])
+
+    def run(self, steps):
+        """Exactly `steps` calls: steps / launches whole graph replays."""
+        if steps % self.launches:
+            raise ValueError("steps (%d) must be a multiple of the graph size (%d)" % (steps, self.launches))
+        self.replay(steps // self.launches)
 
     def time(self, steps, warmup):
+        """(wall ms, HIP-event ms) per call over `steps` calls, after at
+        least `warmup` untimed calls (whole replays); the events bracket the
+        timed replays on the library's stream."""
         L, h = self.nat.lib(), self.dev.handle
-        self.run(warmup)
+        self.replay(-(-warmup // self.launches))
         self.dev.synchronize()
         t0 = time.perf_counter()
         self.nat.check(L.aih_event_record(h, 0), "event")
@@ -105,6 +126,53 @@ class MatvecBench:
     def close(self):
         self.nat.lib().aih_graph_destroy(self.graph)
         for b in self.w + [self.x, self.y]:
+            b.dispose()
+
+
+class StreamBench:
+    """The read ceiling: aih_probe_stream_read over rotating copies of a
+    buffer (nbytes = 0: launches that read nothing), graphs as MatvecBench."""
+
+    def __init__(self, dev, nbytes, nontemporal, copies=COPIES, launches=GRAPH_LAUNCHES):
+        from aihost_amd import _native as nat
+        self.nat, self.dev, self.nbytes = nat, dev, nbytes
+        self.src = [dev.create_buffer(max(16, nbytes)) for _ in range(copies if nbytes else 1)]
+        for b in self.src:
+            nat.check(nat.lib().aih_memset(dev.handle, b.get_pointer(), 1, max(16, nbytes)), "aih_memset")
+        self.out = dev.create_buffer(8192 * 4)
+        L, h = nat.lib(), dev.handle
+        self._launch(0, nontemporal)
+        dev.synchronize()
+        nat.check(L.aih_capture_begin(h), "aih_capture_begin")
+        for i in range(launches):
+            self._launch(i, nontemporal)
+        g = ctypes.c_void_p()
+        nat.check(L.aih_capture_end(h, ctypes.byref(g)), "aih_capture_end")
+        self.graph, self.launches = g.value, launches
+
+    def _launch(self, i, nontemporal):
+        b = self.src[i % len(self.src)]
+        self.nat.check(self.nat.lib().aih_probe_stream_read(self.dev.handle, b.get_pointer(), self.nbytes,
+                                                            int(nontemporal), self.out.get_pointer()),
+                       "aih_probe_stream_read")
+
+    def time(self, graphs, warmup=2):
+        L, h = self.nat.lib(), self.dev.handle
+        for _ in range(warmup):
+            self.nat.check(L.aih_graph_launch(h, self.graph), "aih_graph_launch")
+        self.dev.synchronize()
+        self.nat.check(L.aih_event_record(h, 0), "event")
+        for _ in range(graphs):
+            self.nat.check(L.aih_graph_launch(h, self.graph), "aih_graph_launch")
+        self.nat.check(L.aih_event_record(h, 1), "event")
+        self.dev.synchronize()
+        ev = ctypes.c_float()
+        self.nat.check(L.aih_event_elapsed(h, 0, 1, ctypes.byref(ev)), "event")
+        return ev.value / (graphs * self.launches)
+
+    def close(self):
+        self.nat.lib().aih_graph_destroy(self.graph)
+        for b in self.src + [self.out]:
             b.dispose()
 
 
@@ -172,6 +240,30 @@ def measured_traffic():
     return None
 
 
+def row_bytes_total(n, k):
+    from aihost_amd import _native as nat
+    from aihost_amd import compute as C
+    return n * C.row_bytes(nat.Q4_K, k)
+
+
+def ceilings(dev, nbytes, steps):
+    """Ceilings for one launch reading `nbytes` (the headline's packed bytes):
+    a plain and a non-temporal 16-byte stream over 12 rotating copies, and the
+    same grid launched with nothing to read (the fixed cost of a launch)."""
+    out = {}
+    for name, nb, ntl in (("stream_read_%dB" % nbytes, nbytes, 0),
+                          ("stream_read_%dB_nontemporal" % nbytes, nbytes, 1),
+                          ("empty_launch_same_grid", 0, 0)):
+        sb = StreamBench(dev, nb, ntl)
+        us = sb.time(max(1, steps // (3 * GRAPH_LAUNCHES))) * 1e3
+        out[name] = {"us_per_launch": round(us, 3)}
+        if nb:
+            out[name]["GB/s"] = round(nb / (us * 1e-6) / 1e9, 1)
+            out[name]["frac_hbm_peak"] = round(nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+        sb.close()
+    return out
+
+
 def cpu_baseline(packed, x, n, k, seconds, threads=1):
     """Time the oracle (the C restatement of the reference CPU path) on the same
     workload: whole passes over the 14336 x 4096 matrix, repeated until at
@@ -189,16 +281,16 @@ def cpu_baseline(packed, x, n, k, seconds, threads=1):
 
 
 def host_threads():
-    """Host threads for the multi-threaded CPU baseline: OMP_NUM_THREADS when
-    set (the share of host cores this process may use), else the CPUs in this
-    process's affinity mask; at most 16."""
+    """(threads, source) for the multi-threaded CPU baseline: OMP_NUM_THREADS
+    when set (the share of the host's cores this process is given), else the
+    CPUs in this process's affinity mask."""
     try:
         n = int(os.environ.get("OMP_NUM_THREADS", "0"))
     except ValueError:
         n = 0
-    if n <= 0:
-        n = len(os.sched_getaffinity(0))
-    return max(1, min(16, n))
+    if n > 0:
+        return n, "OMP_NUM_THREADS"
+    return max(1, len(os.sched_getaffinity(0))), "affinity mask"
 
 
 def decoder_bench(dev, distinct_layers, prompt=512, gen=128, cpu=True):
@@ -294,6 +386,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary workloads")
     ap.add_argument("--no-decoder", action="store_true", help="skip the full-decoder prefill/decode leg")
     ap.add_argument("--decoder-distinct-layers", type=int, default=2)
+    ap.add_argument("--ceilings-only", action="store_true",
+                    help="print only the stream-read ceilings and the launch floor (one JSON line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -302,9 +396,17 @@ def main():
     from aihost_amd import _native as nat
     from aihost_amd import compute as C
 
+    if args.steps < 1:
+        print("--steps must be at least 1", file=sys.stderr)
+        sys.exit(2)
     dev = C.HipComputeDevice(0)
     n, k = 14336, 4096
-    main_b = MatvecBench(dev, nat.Q4_K, n, k, 1)
+    if args.ceilings_only:
+        print(json.dumps(ceilings(dev, row_bytes_total(n, k), args.steps)))
+        dev.dispose()
+        return
+    g_main = graph_size(args.steps)
+    main_b = MatvecBench(dev, nat.Q4_K, n, k, 1, launches=g_main)
     # Untimed copy of one weight copy: a kernel of known traffic, so that a
     # counter run (FETCH_SIZE / WRITE_SIZE) over this script can be scaled by
     # what the counters read for it.
@@ -331,12 +433,13 @@ def main():
                                     ("q6_k_4096x14336_b8", nat.Q6_K, 4096, 14336, 8),
                                     ("q4_k_4096x14336_b1", nat.Q4_K, 4096, 14336, 1)):
             mb = MatvecBench(dev, qt, nn, kk, b)
-            s, kern = mb.time(max(GRAPH_LAUNCHES, args.steps // 3), args.warmup // 3)
+            s, kern = mb.time(GRAPH_LAUNCHES * max(1, args.steps // (3 * GRAPH_LAUNCHES)), args.warmup // 3)
             by = algorithmic_bytes(qt, nn, kk, b)
             extra[name] = {"GB/s": round(by / (s * 1e-3) / 1e9, 1),
                            "us_per_call": round(s * 1e3, 3),
                            "frac_hbm_peak": round(by / (kern * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
             mb.close()
+        extra.update(ceilings(dev, packed.nbytes, args.steps))
         # weight upload (host -> HBM through the pinned staging ring), a load-time
         # rate that crosses PCIe: reported beside the kernels, never as `value`
         ub = dev.create_buffer(packed.nbytes)
@@ -372,11 +475,12 @@ def main():
                "sample": "%d full passes of the 14336x4096 Q4_K batch-1 matvec (row dequant + sequential fp32 dot, "
                          "oracle/oracle.c -O2 -ffp-contract=off) in %.1f s, one thread" % (reps, el)}
         # the same port with its rows split over the host cores (OpenMP, static schedule)
-        nt = host_threads()
+        nt, src = host_threads()
         reps, el = cpu_baseline(packed, x_host.reshape(1, k), n, k, args.cpu_seconds / 2, threads=nt)
         cpu_mt = {"value": round(nbytes * reps / el / 1e9, 3), "unit": "GB/s", "cores": nt, "kind": "port",
-                  "sample": "%d full passes of the same matvec in %.1f s, rows split over %d OpenMP threads"
-                            % (reps, el, nt)}
+                  "host_nproc": os.cpu_count(), "threads_from": src,
+                  "sample": "%d full passes of the same matvec in %.1f s, rows split over %d OpenMP threads "
+                            "(the %s; the host has %d CPUs)" % (reps, el, nt, src, os.cpu_count())}
     dev.dispose()
 
     out = {
@@ -390,15 +494,24 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16xf16+f32",
+        "dtype": "i32+f32",
         "data": "synthetic: W ~ N(0,0.02) seed 42 quantized to Q4_K by the library's GGUF quantizer; x ~ N(0,1) seed 43",
         "config": {"workload": "Q4_K decode matvec, W 14336x4096 (GGUF dims [4096,14336]), batch 1",
                    "N": n, "K": k, "batch": 1, "weight_copies": COPIES,
-                   "launch": "hipGraph of %d launches over the copies, replayed" % GRAPH_LAUNCHES,
+                   "launch": "hipGraph of %d launches over the copies, replayed %d times (steps = %d)"
+                             % (g_main, args.steps // g_main, args.steps),
+                   "arithmetic": "weight codes x three int8 limbs of fixed-point x, v_dot4_i32_i8 (exact int32); "
+                                 "scales, mins and limb weights in fp32",
                    "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "kernel_us": round(ms_kernel * 1e3, 3), "bytes_per_launch": nbytes},
+                     "traffic_source": "committed counter summary %s (FETCH_SIZE + WRITE_SIZE per launch, scaled "
+                                       "by a copy of known size), not this run" % os.path.relpath(TRAFFIC_PROFILE, ROOT),
+                     "kernel_us": round(ms_kernel * 1e3, 3),
+                     "timing": "kernel_us: HIP events around the timed graph replays on the library's stream, per "
+                               "launch: back-to-back kernels, each with its launch's fixed cost, plus the start-up "
+                               "of each replay (one replay at --steps <= 120: about 0.3 us per launch at 20)",
+                     "bytes_per_launch": nbytes},
         "cpu_baseline": cpu,
         "cpu_baseline_threads": cpu_mt,
         "decode": decode,

@@ -391,6 +391,16 @@ int aih_event_record(aih_ctx *ctx, int slot);
 /* Milliseconds between two recorded slots; waits for the later one. */
 int aih_event_elapsed(aih_ctx *ctx, int slot_start, int slot_end, float *ms);
 
+/* ---- measurement (no reference counterpart) ---------------------------
+ * The ceiling the matvec's HBM throughput is judged against: streams `bytes`
+ * (a multiple of 16, 16-byte aligned) from src with 16-byte loads, one
+ * workgroup of 512 threads per CU, and nothing else; nontemporal != 0 adds
+ * the non-temporal hint to the loads.  bytes == 0 launches the same grid
+ * with nothing to read (the fixed cost of a launch).  `out` is a device
+ * buffer of 8192 uint32 that receives an XOR of the data (one word per
+ * wave).  Asynchronous on the context's stream, like the operators. */
+int aih_probe_stream_read(aih_ctx *ctx, const void *src, uint64_t bytes, int nontemporal, uint32_t *out);
+
 /* Human-readable text for any status code.  Never returns NULL. */
 const char *aih_strerror(int status);
 

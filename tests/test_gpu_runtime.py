@@ -91,3 +91,28 @@ def test_second_context_is_independent(device):
     # a pointer owned by one context is not freeable through another
     assert nat.lib().aih_free(device.handle, p) == nat.AIH_E_NOT_ALLOCATED
     d2.dispose()   # frees b as well
+
+
+def test_probe_stream_read_folds_every_byte(device):
+    """The bandwidth probe reads every 16-byte piece once: the XOR of the
+    per-wave words equals the XOR of the whole buffer's 32-bit words."""
+    from aihost_amd import _native as nat
+    L = nat.lib()
+    data = np.random.default_rng(5).integers(0, 2**32, (1 << 20) // 4, dtype=np.uint32)
+    src = device.create_buffer(data.nbytes)
+    out = device.create_buffer(8192 * 4)
+    try:
+        src.write(data)
+        for nt in (0, 1):
+            nat.check(L.aih_memset(device.handle, out.get_pointer(), 0, 8192 * 4), "memset")
+            nat.check(L.aih_probe_stream_read(device.handle, src.get_pointer(), data.nbytes, nt, out.get_pointer()),
+                      "probe")
+            device.synchronize()
+            words = out.read_range(0, 8192, np.uint32)
+            assert np.bitwise_xor.reduce(words) == np.bitwise_xor.reduce(data)
+        nat.check(L.aih_probe_stream_read(device.handle, None, 0, 0, out.get_pointer()), "empty launch")
+        assert L.aih_probe_stream_read(device.handle, src.get_pointer(), 17, 0, out.get_pointer()) == nat.AIH_E_INVALID
+        assert L.aih_probe_stream_read(device.handle, src.get_pointer(), 16, 0, None) == nat.AIH_E_INVALID
+    finally:
+        src.dispose()
+        out.dispose()

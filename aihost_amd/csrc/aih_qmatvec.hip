@@ -21,41 +21,31 @@
 // DPP inside a wave and through LDS across the waves of a team; row results
 // stay in registers until the end of the launch.
 //
-// Arithmetic (fp32-equivalent).  A 4-bit (or 6-bit, or biased 8-bit) code q
-// masked out of its packed word, two codes per 32-bit register, IS the fp16
-// subnormal q * 2^-24: the exponent field stays zero, so the code needs no
-// conversion and carries no bias.  Codes in a high nibble are used in place
-// (value 16q * 2^-24) against activations stored pre-divided by 16.  Each
-// activation is held as two fp16 numbers, hi = fp16(x') and lo =
-// fp16((x' - hi) * 2^11), which together carry 22 significant bits, and every
-// code pair is contracted with both by v_dot2_f32_f16 (the products of two
-// fp16 numbers are exact in fp32; the sums accumulate in fp32).  x' is x times
-// a power of two chosen per column from max|x| (every workgroup reduces it
-// over the x it loads anyway), so that the largest activation lands in
-// [2^13, 2^14): no activation overflows fp16, and every one within 2^-27 of
-// the largest keeps all 22 bits.  Accumulators therefore hold
-// R * sum(q * x) with R = 2^-24 * (the power of two); the format offsets
-// (-8 for Q4_0, -32 for Q6_K, +128 for the biased Q8_0 code) enter as
-// -offset * R * sum(x), with sum(x) taken in fp32 from x itself.  Sub-block
-// scales and mins are applied once per sub-block in fp32:
+// Arithmetic (fp32-equivalent).  Each workgroup turns x, per 64-element unit,
+// into integers: X = round(x * S) with a power of two S = 2^(148 - e) chosen
+// from the unit's max|x| (biased exponent e), so that |X| < 2^22, and writes X
+// as three balanced signed-byte limbs (X = d0 + 2^8 d1 + 2^16 d2).  A weight
+// code (4-bit, 6-bit, or the int8 of Q8_0) masked out of its packed word
+// multiplies each limb exactly with v_dot4_i32_i8, four code/limb pairs per
+// instruction, the products summed exactly in int32 per sub-block.  The limb
+// sums are combined in fp32 (A0 + 2^8 A1 + 2^16 A2), the format's offset
+// (-8 for Q4_0, -32 for Q6_K) enters as offset * sum(x) (sum of the scaled
+// x, in fp32), the sub-block scales and mins are applied in fp32:
 //   Q4_K: d*sc*S - dmin*mn*X      (S = sum q*x, X = sum x over the sub-block)
 //   Q6_K: d*sc*sum((q-32)*x)      Q8_0: d*sum(q*x)      Q4_0: d*sum((q-8)*x)
-// and each row's total is divided by R once, after the wave reduction.  The
-// measured normwise error against the reference's sequential fp32 product is
-// about 1e-6 (the earlier fp16-activation form: 2e-4).
+// and each unit's contribution is multiplied by 1/S.  The fused
+// multiply-adds are written out (the file is compiled with
+// -ffp-contract=off), so every column is computed by the same instructions.
+// The normwise error against an fp64 product is about 1e-6, against the
+// reference's sequential fp32 product 1e-6 to 5e-6 (that product's own
+// error).
 #include "aih_internal.h"
 
 namespace {
 
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
-__device__ __forceinline__ float dot2(uint32_t p, uint32_t x, float acc)
-{
-    return __builtin_amdgcn_fdot2(as_h2(p), as_h2(x), acc, false);
-}
 // (a & mask) | b as one v_and_or_b32.  Written out because VOP3 encodings on
 // this architecture take no literal operand and read at most one scalar
 // register, so with a literal mask the compiler emits a v_and_b32 + v_or_b32
@@ -68,13 +58,6 @@ __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t b
 }
 __device__ __forceinline__ float f16lo(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xFFFFu)); }
 __device__ __forceinline__ float f16hi(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16)); }
-__device__ __forceinline__ h2 pack2(float a, float b)
-{
-    h2 r;
-    r.x = (_Float16)a;  // round to nearest even
-    r.y = (_Float16)b;
-    return r;
-}
 
 template <class T>
 __device__ __forceinline__ T ldg(const void *p)

@@ -240,6 +240,19 @@ def measured_traffic():
     return None
 
 
+def gemm_leg(dev):
+    """Prefill GEMM: Q4_K W 4096x4096, X 512x4096 (MFMA-bound; fp16 operands,
+    fp32 accumulation), graph replays of 20 calls."""
+    from aihost_amd import _native as nat
+    gb = GemmBench(dev, nat.Q4_K, 4096, 4096, 512)
+    ms = gb.time(10)
+    gb.close()
+    flops = 2.0 * 512 * 4096 * 4096
+    return {"q4_k_gemm_4096x4096_m512": {"TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
+                                         "us_per_call": round(ms * 1e3, 2),
+                                         "frac_mfma_peak": round(flops / (ms * 1e-3) / MFMA_F16_PEAK, 4)}}
+
+
 def row_bytes_total(n, k):
     from aihost_amd import _native as nat
     from aihost_amd import compute as C
@@ -293,7 +306,7 @@ def host_threads():
     return max(1, len(os.sched_getaffinity(0))), "affinity mask"
 
 
-def decoder_bench(dev, distinct_layers, prompt=512, gen=128, cpu=True):
+def decoder_bench(dev, distinct_layers, prompt=512, gen=128, cpu=True, graph=True):
     """Full Llama decoder of the 8B shape (32 layers, hidden 4096, 32/8 heads
     of 128, FFN 14336, vocab 32000), Q4_K weights with a Q6_K head: prefill of
     a `prompt`-token random prompt, then `gen` greedy decode steps replayed
@@ -312,12 +325,12 @@ def decoder_bench(dev, distinct_layers, prompt=512, gen=128, cpu=True):
     ids = np.random.default_rng(43).integers(0, cfg.vocab, prompt).astype(np.int32)
     try:
         first = dec.prefill(ids)          # warm-up (GEMM workspace, code paths)
-        dec.decode(4)                     # captures the decode graph
+        dec.decode(4, use_graph=graph)    # captures the decode graph
         dev.synchronize()
         nat.check(L.aih_event_record(h, 2), "event")
         dec.prefill(ids, read=False)
         nat.check(L.aih_event_record(h, 3), "event")
-        dec.decode(gen)
+        dec.decode(gen, use_graph=graph)
         nat.check(L.aih_event_record(h, 4), "event")
         dev.synchronize()
         ms = ctypes.c_float()
@@ -342,7 +355,8 @@ def decoder_bench(dev, distinct_layers, prompt=512, gen=128, cpu=True):
         "prefill_tokens": prompt, "prefill_ms": round(t_pre * 1e3, 2),
         "prefill_tokens_per_s": round(prompt / t_pre, 1),
         "prefill_layer_matmul_TFLOP/s": round(flops_pre / t_pre / 1e12, 1),
-        "decode_tokens": gen, "decode_ms_per_token": round(per_tok * 1e3, 4),
+        "decode_tokens": gen, "decode_steps": "graph replays" if graph else "eager launches",
+        "decode_ms_per_token": round(per_tok * 1e3, 4),
         "decode_tokens_per_s": round(gen / t_dec, 1),
         "decode_GB/s": round((wbytes + kv_bytes) / per_tok / 1e9, 1),
         "decode_frac_hbm_peak": round((wbytes + kv_bytes) / per_tok / 1e9 / HBM_PEAK_GBS, 4),
@@ -386,8 +400,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary workloads")
     ap.add_argument("--no-decoder", action="store_true", help="skip the full-decoder prefill/decode leg")
     ap.add_argument("--decoder-distinct-layers", type=int, default=2)
-    ap.add_argument("--ceilings-only", action="store_true",
-                    help="print only the stream-read ceilings and the launch floor (one JSON line)")
+    ap.add_argument("--only", choices=("ceilings", "gemm", "decoder-eager"),
+                    help="one leg alone, for profiling (one JSON line): the stream-read ceilings and the launch "
+                         "floor; the prefill GEMM; the decoder with eager decode steps (no graph)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -401,8 +416,16 @@ def main():
         sys.exit(2)
     dev = C.HipComputeDevice(0)
     n, k = 14336, 4096
-    if args.ceilings_only:
+    if args.only == "ceilings":
         print(json.dumps(ceilings(dev, row_bytes_total(n, k), args.steps)))
+        dev.dispose()
+        return
+    if args.only == "gemm":
+        print(json.dumps(gemm_leg(dev)))
+        dev.dispose()
+        return
+    if args.only == "decoder-eager":
+        print(json.dumps(decoder_bench(dev, args.decoder_distinct_layers, gen=32, cpu=False, graph=False)))
         dev.dispose()
         return
     g_main = graph_size(args.steps)
@@ -455,14 +478,7 @@ def main():
         extra["upload_q4_k_14336x4096"] = {"GB/s": round(5 * src.nbytes / el / 1e9, 2),
                                            "ms_per_call": round(el / 5 * 1e3, 3)}
         ub.dispose()
-        # prefill GEMM: Q4_K W 4096x4096, X 512x4096 (MFMA-bound; fp16 operands, fp32 accumulation)
-        gb = GemmBench(dev, nat.Q4_K, 4096, 4096, 512)
-        ms = gb.time(10)
-        flops = 2.0 * 512 * 4096 * 4096
-        extra["q4_k_gemm_4096x4096_m512"] = {"TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1),
-                                             "us_per_call": round(ms * 1e3, 2),
-                                             "frac_mfma_peak": round(flops / (ms * 1e-3) / MFMA_F16_PEAK, 4)}
-        gb.close()
+        extra.update(gemm_leg(dev))
 
     decode = None
     if not args.no_decoder:

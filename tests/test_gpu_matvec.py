@@ -72,6 +72,9 @@ def test_benchmark_shapes(device, orc, qtype, n, k, batch):
     (nat.Q4_K, 40, 8192, 3), (nat.Q4_K, 40, 8704, 4), (nat.Q4_K, 33, 7680, 8), (nat.Q4_K, 24, 8960, 3),
     (nat.Q6_K, 48, 6144, 3), (nat.Q6_K, 48, 6656, 8), (nat.Q6_K, 17, 5632, 5),
     (nat.Q8_0, 20, 8192, 6), (nat.Q4_0, 20, 8704, 7),
+    # a partial last unit (Q8_0: 130 blocks = 16 units + 2 blocks; Q4_0: 34
+    # blocks), a unit of two blocks, a single unit
+    (nat.Q8_0, 9, 4160, 3), (nat.Q4_0, 30, 1088, 6), (nat.Q8_0, 40, 64, 4), (nat.Q4_K, 16, 512, 8),
     # batch 3..8 with K split over workgroups (sizes for 256 CUs): splits of
     # several rounds with a partial last unit (Q4_0, 17 units of which the
     # last holds 2 blocks, 3 splits of 6/6/5 units); rounds of 2 + 1 units

@@ -76,6 +76,15 @@ __device__ __forceinline__ uint64_t bld8(Rsrc r, uint32_t vo, uint32_t so)
     const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, 0);
     return (uint64_t)v[0] | ((uint64_t)v[1] << 32);
 }
+// The 8 bytes at vo + 2 for a 4-byte-aligned vo (Q8_0/Q4_0 code pieces that
+// start at 2 mod 4): one aligned 12-byte load and two funnel shifts; an
+// 8-byte load at 2 mod 4 takes the slow unaligned path.
+__device__ __forceinline__ uint64_t bld8_at2(Rsrc r, uint32_t vo, uint32_t so)
+{
+    const auto v = __builtin_amdgcn_raw_buffer_load_b96(r, vo, so, 0);
+    const uint32_t lo = __builtin_amdgcn_alignbit(v[1], v[0], 16), hi = __builtin_amdgcn_alignbit(v[2], v[1], 16);
+    return (uint64_t)lo | ((uint64_t)hi << 32);
+}
 __device__ __forceinline__ uint32_t bld2(Rsrc r, uint32_t vo, uint32_t so)
 {
     return __builtin_amdgcn_raw_buffer_load_b16(r, vo, so, 0);
@@ -170,11 +179,23 @@ struct UQ6K {
     struct Raw { uint64_t ql[4], qh[2]; u4 sc; uint32_t d; };
     __device__ static void load(Rsrc r, uint32_t rowoff, int q, uint32_t so, int, Raw &w)
     {
+        // Units are 210 bytes: an odd unit starts at 2 mod 4 (rows at
+        // multiples of 4).  Its pieces come from aligned loads 2 bytes lower,
+        // funnel-shifted by 16 bits (by 0 for an even unit).
+        const uint32_t sa = so & ~3u, sh = (so & 3u) * 8;
+        auto piece = [&](uint32_t vo) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b96(r, vo, sa, 0);
+            return (uint64_t)__builtin_amdgcn_alignbit(v[1], v[0], sh) |
+                   ((uint64_t)__builtin_amdgcn_alignbit(v[2], v[1], sh) << 32);
+        };
 #pragma unroll
-        for (int i = 0; i < 4; ++i) w.ql[i] = bld8(r, rowoff + 64 * (i >> 1) + 32 * (i & 1) + 8 * q, so);
+        for (int i = 0; i < 4; ++i) w.ql[i] = piece(rowoff + 64 * (i >> 1) + 32 * (i & 1) + 8 * q);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) w.qh[h] = bld8(r, rowoff + 128 + 32 * h + 8 * q, so);
-        w.sc = bld16(r, rowoff + 192, so);
+        for (int h = 0; h < 2; ++h) w.qh[h] = piece(rowoff + 128 + 32 * h + 8 * q);
+        const u4 s4 = bld16(r, rowoff + 192, sa);
+        const uint32_t s5 = __builtin_amdgcn_raw_buffer_load_b32(r, rowoff + 208, sa, 0);
+        w.sc = u4{__builtin_amdgcn_alignbit(s4.y, s4.x, sh), __builtin_amdgcn_alignbit(s4.z, s4.y, sh),
+                  __builtin_amdgcn_alignbit(s4.w, s4.z, sh), __builtin_amdgcn_alignbit(s5, s4.w, sh)};
         w.d = bld2(r, rowoff + 208, so);
     }
     __device__ static void coef(const Raw &r, float *k, float *)
@@ -210,11 +231,15 @@ struct UQ80 {
     __device__ static void load(Rsrc r, uint32_t rowoff, int q, uint32_t so, int nb, Raw &w)
     {
         // a block past the row's end (only in a last, partial unit) re-reads
-        // block 0 of the unit, so no read leaves the row, and gets scale 0
+        // the start of the unit, so no read leaves the row, and gets scale 0.
+        // Rows and units start at multiples of 4 bytes (K is a multiple of
+        // 64): the pieces of even blocks lie at 2 mod 4, those of odd ones
+        // are aligned.
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
             const uint32_t o = b < nb ? rowoff + 34 * b : rowoff;
-            w.qs[b] = bld8(r, o + 2 + 8 * q, so);
+            if (b % 2 == 0) w.qs[b] = bld8_at2(r, o + 8 * q, so);
+            else w.qs[b] = bld8(r, b < nb ? o + 2 + 8 * q : o + 8 * q, so);
             w.d[b] = b < nb ? bld2(r, o, so) : 0u;
         }
     }
@@ -240,10 +265,12 @@ struct UQ40 {
     struct Raw { uint64_t qs[8]; uint32_t d[8]; };
     __device__ static void load(Rsrc r, uint32_t rowoff, int q, uint32_t so, int nb, Raw &w)
     {
+        // as Q8_0: even blocks' pieces at 2 mod 4, odd ones aligned
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
             const uint32_t o = b < nb ? rowoff + 18 * b : rowoff;
-            w.qs[b] = bld8(r, o + 2 + 8 * (q & 1), so);
+            if (b % 2 == 0) w.qs[b] = bld8_at2(r, o + 8 * (q & 1), so);
+            else w.qs[b] = bld8(r, b < nb ? o + 2 + 8 * (q & 1) : o + 8 * (q & 1), so);
             w.d[b] = b < nb ? bld2(r, o, so) : 0u;
         }
     }

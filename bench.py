@@ -253,6 +253,22 @@ def gemm_leg(dev):
                                          "frac_mfma_peak": round(flops / (ms * 1e-3) / MFMA_F16_PEAK, 4)}}
 
 
+def small_batch_leg(dev, steps=600):
+    """Q6_K 4096x14336 at 4 and 8 activation columns (the matrix-core kernel
+    and its sum of the K splits), graphs of 60 calls: 120 kernel nodes, a size
+    the kernel tracer handles."""
+    from aihost_amd import _native as nat
+    out = {}
+    for b in (4, 8):
+        mb = MatvecBench(dev, nat.Q6_K, 4096, 14336, b, launches=60)
+        s, kern = mb.time(steps, 60)
+        by = algorithmic_bytes(nat.Q6_K, 4096, 14336, b)
+        out["q6_k_4096x14336_b%d" % b] = {"GB/s": round(by / (s * 1e-3) / 1e9, 1), "us_per_call": round(s * 1e3, 3),
+                                          "launch": "hipGraph of 60 calls, replayed"}
+        mb.close()
+    return out
+
+
 def row_bytes_total(n, k):
     from aihost_amd import _native as nat
     from aihost_amd import compute as C
@@ -400,9 +416,10 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary workloads")
     ap.add_argument("--no-decoder", action="store_true", help="skip the full-decoder prefill/decode leg")
     ap.add_argument("--decoder-distinct-layers", type=int, default=2)
-    ap.add_argument("--only", choices=("ceilings", "gemm", "decoder-eager"),
+    ap.add_argument("--only", choices=("ceilings", "gemm", "decoder-eager", "small-batch"),
                     help="one leg alone, for profiling (one JSON line): the stream-read ceilings and the launch "
-                         "floor; the prefill GEMM; the decoder with eager decode steps (no graph)")
+                         "floor; the prefill GEMM; the decoder with eager decode steps (no graph); the Q6_K "
+                         "4096x14336 matvec at 4 and 8 columns")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -422,6 +439,10 @@ def main():
         return
     if args.only == "gemm":
         print(json.dumps(gemm_leg(dev)))
+        dev.dispose()
+        return
+    if args.only == "small-batch":
+        print(json.dumps(small_batch_leg(dev)))
         dev.dispose()
         return
     if args.only == "decoder-eager":

@@ -48,6 +48,23 @@ __device__ __forceinline__ float xor2(float v)   // lane ^ 2 (quad_perm [2,3,0,1
     return __builtin_amdgcn_update_dpp(0.0f, v, 0x4E, 0xF, 0xF, false);
 }
 
+// Maximum / sum over the aligned 16 lanes of a row, returned to every lane
+// of the row: pairs, quads, half rows (row_half_mirror), rows (row_mirror).
+__device__ __forceinline__ float row16_max(float v)
+{
+    v = fmaxf(v, xor1(v));
+    v = fmaxf(v, xor2(v));
+    v = fmaxf(v, __builtin_amdgcn_update_dpp(0.0f, v, 0x141, 0xF, 0xF, false));
+    return fmaxf(v, __builtin_amdgcn_update_dpp(0.0f, v, 0x140, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_sum(float v)
+{
+    v += xor1(v);
+    v += xor2(v);
+    v += __builtin_amdgcn_update_dpp(0.0f, v, 0x141, 0xF, 0xF, false);
+    return v + __builtin_amdgcn_update_dpp(0.0f, v, 0x140, 0xF, 0xF, false);
+}
+
 // Sum over the 64 lanes of a wave, returned to every lane: pairs, quads,
 // half rows and rows of 16 by DPP, then rows 0+1, 2+3 and 0..3 into lane 63
 // (row_bcast), read back with readlane.
@@ -640,79 +657,180 @@ attn_decode_combine(const float *__restrict__ part, float *__restrict__ O, int32
     O[(int64_t)h * kHD + t] = lsum > 0.f ? a / lsum : 0.f;
 }
 
-// Prefill: workgroup (h, tile) of 256 threads handles kQTile query rows;
-// thread t: query t/4, dims 32*(t%4) .. +31, with an online softmax over key
-// tiles of 64 rows staged in LDS.
+// Prefill on the matrix cores: v_mfma_f32_16x16x4_f32 takes fp32 operands
+// and accumulates in fp32, as the reference's scalar loops do (only the
+// order of the additions differs).  Workgroup (h, tile) of 256 threads owns
+// kQTile = 64 query rows; wave w the 16 rows 16w .. 16w+15.  Per tile of 64
+// keys, staged in LDS: S = Q K^T (16 x 64 per wave), an online softmax per
+// query row, O += P V (16 x 128 per wave).
+//
+// MFMA 16x16x4 layouts (lane l, g = l/16, c = l%16): A[i][k] is lane
+// i + 16k, B[k][j] lane j + 16k, D[i][j] lane j + 16(i/4), register i%4.
+//   S: A = Q (lane holds query c, dims 4s + g for the 32 k-steps s),
+//      B = K^T (key c of a 16-key block, dim 4s + g): D row 4g + r = query,
+//      column c = key.
+//   O: A = P (query c, key 4s + g), B = V (key 4s + g, dim c of a 16-dim
+//      block): D row 4g + r = query, column c = dim.
+// So every lane keeps the running max and sum of its four D rows 4g + r,
+// and P goes through LDS to change from the D to the A layout.  The LDS
+// images are permuted so that one 16-byte read gives a lane four k-steps:
+//   K tile: key j, dim d at [j][(d%4) * 32 + d/4]        (row stride kRK)
+//   V tile: dim d, key j at [d][(j%4) * 16 + j/4]        (row stride kRV)
+//   P:      query q, key j at [q][(j%4) * 16 + j/4]      (row stride kRP)
+constexpr int kKT = 64;       // keys per tile
+constexpr int kRK = 132;      // strides in floats: 16-byte rows, 4 banks apart
+constexpr int kRV = 68;
+constexpr int kRP = 68;
+
 __global__ void __launch_bounds__(256)
 attn_prefill_kernel(const float *__restrict__ Q, const float *__restrict__ Kc, const float *__restrict__ Vc,
                     float *__restrict__ O, int64_t n_q, int32_t n_heads, int32_t n_kv_heads, int32_t start,
                     const int32_t *pos, int32_t max_len, float scale)
 {
-    __shared__ f4 ks[64][kHD / 4];
-    __shared__ f4 vs[64][kHD / 4];
-    const int h = blockIdx.x, t = threadIdx.x;
+    __shared__ __align__(16) float ks[kKT * kRK];
+    __shared__ __align__(16) float vt[kHD * kRV];
+    __shared__ __align__(16) float ps[4][16 * kRP];
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int g = lane >> 4, c = lane & 15;
     const int kvh = h / (n_heads / n_kv_heads);
     const int64_t kv_stride = (int64_t)n_kv_heads * kHD, q_stride = (int64_t)n_heads * kHD;
     const int32_t p0 = dev_pos(start, pos);
     const int64_t i0 = (int64_t)blockIdx.y * kQTile;
-    const int qi = t >> 2, part4 = t & 3;
-    const int64_t i = i0 + qi;
-    const bool valid = i < n_q;
-    const int64_t p_i = p0 + (valid ? i : n_q - 1);            // last key of this query
     // keys beyond the cache (a position past max_len) are never read
     const int64_t p_last = min<int64_t>(p0 + min<int64_t>(i0 + kQTile, n_q) - 1, (int64_t)max_len - 1);
 
-    f4 q[8], acc[8];
-    const f4 *q4 = reinterpret_cast<const f4 *>(Q + (valid ? i : 0) * q_stride + (int64_t)h * kHD + part4 * 32);
+    // Q fragments: query 16w + c, dims 4s + g (rows past n_q read the last row, never stored)
+    float qf[32];
+    {
+        const float *qrow = Q + min<int64_t>(i0 + 16 * w + c, n_q - 1) * q_stride + (int64_t)h * kHD;
 #pragma unroll
-    for (int d = 0; d < 8; ++d) {
-        q[d] = q4[d];
-        acc[d] = f4{0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < 32; ++s) qf[s] = qrow[4 * s + g];
     }
-    float m = -INFINITY, l = 0.f;
-    for (int64_t j0 = 0; j0 <= p_last; j0 += 64) {
-        __syncthreads();   // previous tile consumed
-        for (int e = t; e < 64 * (kHD / 4); e += 256) {
-            const int r = e / (kHD / 4), c = e % (kHD / 4);
-            const int64_t j = j0 + r;
-            const bool in = j <= p_last;
-            ks[r][c] = in ? reinterpret_cast<const f4 *>(Kc + j * kv_stride + kvh * kHD)[c] : f4{0.f, 0.f, 0.f, 0.f};
-            vs[r][c] = in ? reinterpret_cast<const f4 *>(Vc + j * kv_stride + kvh * kHD)[c] : f4{0.f, 0.f, 0.f, 0.f};
+    // the position of each of this lane's four D rows (last key it attends to)
+    int64_t qp[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) qp[r] = p0 + min<int64_t>(i0 + 16 * w + 4 * g + r, n_q - 1);
+    float m[4], l[4];
+    f4 o[8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        m[r] = -INFINITY;
+        l[r] = 0.f;
+    }
+#pragma unroll
+    for (int db = 0; db < 8; ++db) o[db] = f4{0.f, 0.f, 0.f, 0.f};
+
+    // staging: K thread (key kr_j + 8i, dims kr_d .. +3), V thread (key
+    // vr_j, dims vr_d + 4i .. +3), so that each layout's LDS writes are
+    // spread over the banks
+    const int kr_j = tid >> 5, kr_d = 4 * (tid & 31);
+    const int vr_j = tid & 63, vr_d = 32 * (tid >> 6);
+    f4 kr[8], vr[8];
+    auto gload = [&](int64_t j0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int64_t jk = j0 + kr_j + 8 * i, jv = j0 + vr_j;
+            kr[i] = jk <= p_last ? *reinterpret_cast<const f4 *>(Kc + jk * kv_stride + kvh * kHD + kr_d)
+                                 : f4{0.f, 0.f, 0.f, 0.f};
+            vr[i] = jv <= p_last ? *reinterpret_cast<const f4 *>(Vc + jv * kv_stride + kvh * kHD + vr_d + 4 * i)
+                                 : f4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    gload(0);
+    float *pw = ps[w];
+    for (int64_t j0 = 0; j0 <= p_last; j0 += kKT) {
+        __syncthreads();   // the previous tile is consumed
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float *kd = ks + (kr_j + 8 * i) * kRK + kr_d / 4;
+            kd[0] = kr[i].x;
+            kd[32] = kr[i].y;
+            kd[64] = kr[i].z;
+            kd[96] = kr[i].w;
+            float *vd = vt + (vr_d + 4 * i) * kRV + (vr_j % 4) * 16 + vr_j / 4;
+            vd[0] = vr[i].x;
+            vd[kRV] = vr[i].y;
+            vd[2 * kRV] = vr[i].z;
+            vd[3 * kRV] = vr[i].w;
         }
         __syncthreads();
-        const int64_t jn = min<int64_t>(64, p_last - j0 + 1);
-        for (int jj = 0; jj < jn; ++jj) {
-            float a = 0.f;
+        gload(j0 + kKT);   // the next tile's rows in flight (zeros past p_last)
+
+        // S = Q K^T, four blocks of 16 keys
+        f4 sc[4];
 #pragma unroll
-            for (int d = 0; d < 8; ++d) {
-                const f4 k = ks[jj][part4 * 8 + d];
-                a = fmaf(q[d].x, k.x, a);
-                a = fmaf(q[d].y, k.y, a);
-                a = fmaf(q[d].z, k.z, a);
-                a = fmaf(q[d].w, k.w, a);
-            }
-            a += xor1(a);
-            a += xor2(a);
-            if (j0 + jj > p_i) continue;            // causal: key after the query
-            const float s = a * scale;
-            const float mn = fmaxf(m, s);
-            const float corr = expf(m - mn), pj = expf(s - mn);
-            l = l * corr + pj;
+        for (int kb = 0; kb < 4; ++kb) {
+            f4 acc = {0.f, 0.f, 0.f, 0.f};
+            const float *kp = ks + (16 * kb + c) * kRK + 32 * g;
 #pragma unroll
-            for (int d = 0; d < 8; ++d) {
-                const f4 v = vs[jj][part4 * 8 + d];
-                acc[d].x = fmaf(pj, v.x, acc[d].x * corr);
-                acc[d].y = fmaf(pj, v.y, acc[d].y * corr);
-                acc[d].z = fmaf(pj, v.z, acc[d].z * corr);
-                acc[d].w = fmaf(pj, v.w, acc[d].w * corr);
+            for (int s4 = 0; s4 < 8; ++s4) {
+                const f4 kf = *reinterpret_cast<const f4 *>(kp + 4 * s4);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[4 * s4 + 0], kf.x, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[4 * s4 + 1], kf.y, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[4 * s4 + 2], kf.z, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[4 * s4 + 3], kf.w, acc, 0, 0, 0);
             }
-            m = mn;
+            sc[kb] = acc;
+        }
+        // scale, causal mask, online softmax of rows 4g + r (16 lanes each)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                const float v = j0 + 16 * kb + c > qp[r] ? -INFINITY : sc[kb][r] * scale;
+                sc[kb][r] = v;
+                mx = fmaxf(mx, v);
+            }
+            mx = row16_max(mx);
+            // key 0 lies in the first tile of every row: mn is finite from then on
+            const float mn = fmaxf(m[r], mx), corr = expf(m[r] - mn);
+            float sum = 0.f;
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                const float pj = expf(sc[kb][r] - mn);
+                sc[kb][r] = pj;
+                sum += pj;
+            }
+            sum = row16_sum(sum);
+            l[r] = l[r] * corr + sum;
+            m[r] = mn;
+#pragma unroll
+            for (int db = 0; db < 8; ++db) o[db][r] *= corr;
+        }
+        // P from the D layout (row 4g + r, key 16kb + c) to the A layout through LDS
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) pw[(4 * g + r) * kRP + (c % 4) * 16 + 4 * kb + c / 4] = sc[kb][r];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        f4 pa[4];
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) pa[s4] = *reinterpret_cast<const f4 *>(pw + c * kRP + 16 * g + 4 * s4);
+        // O += P V, eight blocks of 16 dims
+#pragma unroll
+        for (int db = 0; db < 8; ++db) {
+            const float *vp = vt + (16 * db + c) * kRV + 16 * g;
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4) {
+                const f4 vf = *reinterpret_cast<const f4 *>(vp + 4 * s4);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[s4].x, vf.x, o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[s4].y, vf.y, o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[s4].z, vf.z, o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[s4].w, vf.w, o[db], 0, 0, 0);
+            }
         }
     }
-    if (valid) {
-        f4 *o4 = reinterpret_cast<f4 *>(O + i * q_stride + (int64_t)h * kHD + part4 * 32);
 #pragma unroll
-        for (int d = 0; d < 8; ++d) o4[d] = acc[d] / l;
+    for (int r = 0; r < 4; ++r) {
+        const int64_t i = i0 + 16 * w + 4 * g + r;
+        if (i < n_q) {
+            float *orow = O + i * q_stride + (int64_t)h * kHD + c;
+#pragma unroll
+            for (int db = 0; db < 8; ++db) orow[16 * db] = o[db][r] / l[r];
+        }
     }
 }
 

@@ -216,9 +216,15 @@ def test_attention_decode_scratch_reused(device, bufs):
         assert np.linalg.norm(o - ref) / np.linalg.norm(ref) < 1e-5
 
 
-@pytest.mark.parametrize("n_q,start", [(512, 0), (100, 0), (65, 40), (2, 7)])
+@pytest.mark.parametrize("n_q,start", [(512, 0), (100, 0), (65, 40), (2, 7), (128, 512), (17, 600)])
 def test_attention_prefill(device, bufs, n_q, start):
+    # query tiles of 64 and key tiles of 64: full and partial tiles of both,
+    # rows that end at the cache's last row (start + n_q = 640)
     _attn(device, bufs, n_q, start, 640)
+
+
+def test_attention_prefill_at_device_position(device, bufs):
+    _attn(device, bufs, 70, 3, 640, pos_dev=20)
 
 
 def test_attention_gqa_small(device, bufs):

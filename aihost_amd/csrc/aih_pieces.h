@@ -129,6 +129,48 @@ struct G4K {
     }
 };
 
+// Q4_K in 32-weight pieces: half ph of the 32 code bytes of group g = c % 4
+// holds elements 16 ph .. 16 ph + 15 of sub-block 2g (low nibbles, chunk
+// columns 16 ph ..) and of sub-block 2g + 1 (high nibbles, columns 32 + 16 ph
+// ..).  One header and one 16-byte code load give 32 weights, and the two
+// scale/min pairs come from the same shifted header words: for g < 2 they are
+// plain 6-bit fields, for g >= 2 (sub-blocks 4..7) the low four bits sit in
+// the last header word and the top two in the first two (get_scale_min_k4,
+// QuantizationFormats.cs:157-165), selected here by per-lane masks rather
+// than branches.
+struct G4K32 {
+    typedef G4K::Raw Raw;
+    __device__ static void load(const uint8_t *row, int c, int ph, Raw &r)
+    {
+        const uint8_t *b = row + (c >> 2) * 144;
+        r.hdr = ldg<u4>(b);
+        r.qs = ldg<u4>(b + 16 + 32 * (c & 3) + 16 * ph);
+    }
+    __device__ static void piece(const Raw &r, int c, int, h8 out[4])
+    {
+        const int g = c & 3;
+        const int sh = 16 * (g & 1);
+        const bool upper = g >= 2;
+        const uint32_t sA = upper ? 2u : 0u, mA = upper ? 0x30u : 0x3Fu, mW = upper ? 0xFu : 0u;
+        const uint32_t a = r.hdr.y >> sh, b = r.hdr.z >> sh, w = r.hdr.w >> sh;
+        const uint32_t sc0 = ((a >> sA) & mA) | (w & mW);
+        const uint32_t sc1 = ((a >> (8u + sA)) & mA) | ((w >> 8) & mW);
+        const uint32_t mn0 = ((b >> sA) & mA) | ((w >> 4) & mW);
+        const uint32_t mn1 = ((b >> (8u + sA)) & mA) | ((w >> 12) & mW);
+        const float d = f16_bits(r.hdr.x), dmin = f16_bits(r.hdr.x >> 16);
+        // high nibbles stay in place (16 q under the exponent byte): scale / 16
+        const float D0 = d * (float)sc0, D1 = d * (float)sc1 * 0.0625f;
+        const float C0 = 1024.f * D0 + dmin * (float)mn0, C1 = 1024.f * D1 + dmin * (float)mn1;
+        const uint32_t lo = 0x0F0F0F0Fu, hi = 0xF0F0F0F0u;
+        out[0] = weights8(r.qs.x & lo, r.qs.y & lo, D0, C0);
+        out[1] = weights8(r.qs.z & lo, r.qs.w & lo, D0, C0);
+        out[2] = weights8(r.qs.x & hi, r.qs.y & hi, D1, C1);
+        out[3] = weights8(r.qs.z & hi, r.qs.w & hi, D1, C1);
+    }
+    // chunk column of out[q] for half ph
+    __device__ static constexpr int col(int ph, int q) { return 16 * ph + 8 * (q & 1) + 32 * (q >> 1); }
+};
+
 // Q6_K: chunk c covers half h = (c % 4) / 2 of block c / 4, quarters
 // Q0 = 2 * (c % 2) and Q0 + 1; piece s is quarter Q = Q0 + s / 2, columns
 // 16 * (s % 2) .. +15 (ComputeOps.cs:1748-1771).
@@ -260,12 +302,37 @@ struct HasPieceH {
     static constexpr bool value = sizeof(test<T>(0)) == 1;
 };
 
+// 32-weight pieces for formats without a dedicated form: half ph of chunk c
+// is pieces 2 ph and 2 ph + 1, columns 32 ph .. 32 ph + 31.
+template <class T>
+struct Pair32 {
+    struct Raw { typename T::Raw a, b; };
+    __device__ static void load(const uint8_t *row, int c, int ph, Raw &r)
+    {
+        T::load(row, c, 2 * ph, r.a);
+        T::load(row, c, 2 * ph + 1, r.b);
+    }
+    __device__ static void piece(const Raw &r, int c, int ph, h8 out[4]);
+    __device__ static constexpr int col(int ph, int q) { return 32 * ph + 8 * q; }
+};
+
+// The GEMM producers' piece type for format T.
+template <class T> struct Piece32 { typedef Pair32<T> type; };
+template <> struct Piece32<G4K> { typedef G4K32 type; };
+
 // The 16 weights of piece s of chunk c as two fp16 vectors.
 template <class T>
 __device__ __forceinline__ void piece16h(const typename T::Raw &r, int c, int s, h8 &lo, h8 &hi)
 {
     if constexpr (HasPieceH<T>::value) T::piece_h(r, c, s, lo, hi);
     else piece_h_of<T>(r, c, s, lo, hi);
+}
+
+template <class T>
+__device__ void Pair32<T>::piece(const Raw &r, int c, int ph, h8 out[4])
+{
+    piece16h<T>(r.a, c, 2 * ph, out[0], out[1]);
+    piece16h<T>(r.b, c, 2 * ph + 1, out[2], out[3]);
 }
 
 }  // namespace aih_pieces

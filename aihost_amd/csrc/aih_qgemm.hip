@@ -242,14 +242,170 @@ qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
     }
 }
 
+// Wide tiles for large products: a workgroup of eight waves owns a 256 (M) x
+// 64 (N) tile, so each dequantized weight feeds twice as many outputs as in
+// qgemm_kernel.  Every wave takes both roles in each super-step s:
+//   - it dequantizes its 8 of the 64 weight rows (row 8w + lane / 8) for
+//     super-step s+1 into the other LDS buffer, 32 weights per lane
+//     (Piece32), from packed loads PR256 super-steps ahead;
+//   - it multiplies super-step s: wave w owns rows 32w .. 32w+31 of the M tile
+//     and all 64 columns (two 32x32 accumulators sharing each A fragment), A
+//     fragments from the tiled X one super-step ahead, B fragments from LDS.
+// The two waves of a SIMD (w and w + 4) run the two halves in opposite
+// orders, so that one dequantizes while the other multiplies.  On MI355X a
+// workgroup takes about 1.25 times as long as a 128-row one, for twice the
+// outputs.
+constexpr int BM2 = 256;
+constexpr int PR256 = 2;
+
+template <class T>
+__global__ void __launch_bounds__(512)
+qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
+                const _Float16 *__restrict__ Xt, int64_t M, float *__restrict__ Y)
+{
+    constexpr int PR = PR256;
+    typedef typename Piece32<T>::type P;
+    typedef typename P::Raw Raw;
+    __shared__ __align__(16) _Float16 wsh[2][BN][LD2];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t m0 = (int64_t)blockIdx.y * BM2, n0 = (int64_t)blockIdx.x * BN;
+    const int nch = (int)(K / 64);
+    const int nss = (nch + SC - 1) / SC;
+
+    // dequantization share: row 8 wave + rl, 32 weights per lane (chunk pc, half ph)
+    const int rl = lane >> 3, p = lane & 7, pc = p >> 1, ph = p & 1;
+    const int64_t wn = n0 + 8 * wave + rl;
+    const uint8_t *wrow = W + (wn < N ? wn : N - 1) * row_bytes;
+    auto gload = [&](int ss, Raw *r) {
+        int c = ss * SC + pc;
+        c = c < nch ? c : nch - 1;
+        P::load(wrow, c, ph, r[0]);
+    };
+    // chunks past K exist only in a last, partial super-step, staged as zeros
+    auto stage = [&](auto tail, int ss, int buf, const Raw *r) {
+        const int c = ss * SC + pc;
+        h8 o[4];
+        P::piece(r[0], c, ph, o);
+        _Float16 *d = &wsh[buf][8 * wave + rl][64 * pc];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<h8 *>(d + P::col(ph, q)) = decltype(tail)::value && c >= nch ? h8{} : o[q];
+    };
+
+    // multiplication share: rows 32 wave .. +31 of the M tile
+    const int fr = lane & 31, fk = 8 * (lane >> 5);
+    const int64_t kc = K / 16, mblocks = (M + 31) / 32;
+    int64_t mb = (m0 + 32 * wave) / 32;
+    mb = mb < mblocks ? mb : mblocks - 1;
+    const _Float16 *xa = Xt + (mb * kc * 64 + lane) * 8;
+    struct AF { h8 a[4]; };
+    auto aload = [&](int kb, AF &f) {
+        kb = kb < nch ? kb : nch - 1;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) f.a[kk] = ldg<h8>(xa + ((int64_t)kb * 4 + kk) * 512);
+    };
+    f16v acc0 = {}, acc1 = {};
+    struct BF { h8 b0[4], b1[4]; };
+    auto bload = [&](int buf, int t, BF &b) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            b.b0[kk] = *reinterpret_cast<const h8 *>(&wsh[buf][fr][64 * t + 16 * kk + fk]);
+            b.b1[kk] = *reinterpret_cast<const h8 *>(&wsh[buf][32 + fr][64 * t + 16 * kk + fk]);
+        }
+    };
+    auto mm = [&](const AF &f, const BF &b) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[kk], b.b0[kk], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[kk], b.b1[kk], acc1, 0, 0, 0);
+        }
+    };
+
+    // Iteration it: products of super-step it from buffer it & 1, and, if
+    // `more`, the dequantization of super-step it + 1 into the other buffer
+    // from ring slot r, whose loads are then reissued for super-step
+    // it + 1 + PR when `reload`.
+    Raw ring[PR][1];
+    AF f[SC];
+    BF bb[2];
+    // The two waves of a SIMD (w and w + 4) take the two halves in opposite
+    // orders, so that one dequantizes while the other multiplies.
+    const bool valu_first = wave < 4;
+    auto body = [&](auto tail, int it, Raw *r, bool more, bool reload) {
+        const int buf = it & 1;
+        auto deq = [&] {
+            if (more) {
+                stage(tail, it + 1, buf ^ 1, r);
+                if (reload) gload(it + 1 + PR, r);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        bload(buf, 0, bb[0]);
+        if (valu_first) deq();
+#pragma unroll
+        for (int t = 0; t < SC; ++t) {
+            if (t + 1 < SC) bload(buf, t + 1, bb[(t + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+            mm(f[t], bb[t & 1]);
+            aload(SC * (it + 1) + t, f[t]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (!valu_first) deq();
+        __builtin_amdgcn_sched_barrier(0);
+        lds_barrier();
+    };
+
+#pragma unroll
+    for (int j = 0; j < PR; ++j) gload(j, ring[j]);
+#pragma unroll
+    for (int t = 0; t < SC; ++t) aload(t, f[t]);
+    stage(std::true_type{}, 0, 0, ring[0]);
+    gload(PR, ring[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+    // iteration it stages super-step it + 1 from ring slot (it + 1) % PR; the
+    // main loop's stages are all full super-steps before the last
+    int ss = 0;
+    for (; ss + PR + 1 < nss; ss += PR) {
+#pragma unroll
+        for (int j = 0; j < PR; ++j) body(std::false_type{}, ss + j, ring[(j + 1) % PR], true, true);
+    }
+#pragma unroll
+    for (int j = 0; j <= PR; ++j) {
+        const int it = ss + j;
+        if (it < nss) body(std::true_type{}, it, ring[(j + 1) % PR], it + 1 < nss, it + 1 + PR < nss);
+    }
+
+    const int64_t na = n0 + fr, nb = n0 + 32 + fr;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int i = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int64_t m = m0 + 32 * wave + i;
+        if (m < M) {
+            if (na < N) Y[m * N + na] = acc0[r];
+            if (nb < N) Y[m * N + nb] = acc1[r];
+        }
+    }
+}
+
 template <class T>
 int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
            const _Float16 *Xh, int64_t M, float *Y)
 {
-    const int64_t gx = (N + BN - 1) / BN, gy = (M + BM - 1) / BM;
+    const int64_t gx = (N + BN - 1) / BN, gy = (M + BM - 1) / BM, gy2 = (M + BM2 - 1) / BM2;
     if (gy > 65535 || gx > 0x7FFFFFFF) return AIH_E_LIMIT;
-    hipLaunchKernelGGL((qgemm_kernel<T>), dim3((unsigned)gx, (unsigned)gy), dim3(512), 0, ctx->stream,
-                       W, N, K, row_bytes, Xh, M, Y);
+    // 256-row tiles halve the dequantization per output, and a workgroup of
+    // them takes about 1.25 times as long as one of 128 rows (measured on
+    // MI355X); they are taken when that wins on rounds of workgroups over the
+    // device's CUs
+    const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+    const int64_t rounds = (gx * gy + cus - 1) / cus, rounds2 = (gx * gy2 + cus - 1) / cus;
+    if (5 * rounds2 < 4 * rounds)
+        hipLaunchKernelGGL((qgemm256_kernel<T>), dim3((unsigned)gx, (unsigned)gy2), dim3(512), 0, ctx->stream,
+                           W, N, K, row_bytes, Xh, M, Y);
+    else
+        hipLaunchKernelGGL((qgemm_kernel<T>), dim3((unsigned)gx, (unsigned)gy), dim3(512), 0, ctx->stream,
+                           W, N, K, row_bytes, Xh, M, Y);
     return aih_launch_status();
 }
 

@@ -47,6 +47,20 @@ def test_shapes(device, orc, qtype, n, k, m):
     assert_close(y, orc.matvec(qtype, w, n, k, x, nthreads=8), TOL, "type %d %dx%d M=%d" % (qtype, n, k, m))
 
 
+# Grids large enough for the 256-row tiles on a 256-CU device (fewer rounds of
+# workgroups than the 128-row tiles): partial tiles in M and N, and for Q8_0 a
+# partial last super-step.
+@pytest.mark.parametrize("qtype,n,k,m", [
+    (nat.Q4_K, 6377, 1536, 300), (nat.Q6_K, 6400, 1024, 384),
+    (nat.Q8_0, 6377, 1600, 300), (nat.Q4_0, 6400, 1600, 257),
+])
+def test_wide_tiles(device, orc, qtype, n, k, m):
+    w = synth_weight(qtype, n, k, seed=n + k)
+    x = x_of(m, k, seed=m * 3 + k)
+    y = qgemm(device, qtype, w, n, k, x)
+    assert_close(y, orc.matvec(qtype, w, n, k, x, nthreads=16), TOL, "type %d %dx%d M=%d" % (qtype, n, k, m))
+
+
 def test_subnormal_scales(device, orc):
     rng = np.random.default_rng(9)
     n, k, m = 70, 512, 33

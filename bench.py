@@ -253,6 +253,68 @@ def gemm_leg(dev):
                                          "frac_mfma_peak": round(flops / (ms * 1e-3) / MFMA_F16_PEAK, 4)}}
 
 
+_VENDOR_GEMM = r"""
+import json, sys, torch
+out = {}
+for m, n, k in json.loads(sys.argv[1]):
+    a = torch.randn(m, k, device="cuda", dtype=torch.float16)
+    w = torch.randn(n, k, device="cuda", dtype=torch.float16)
+    for _ in range(10):
+        torch.nn.functional.linear(a, w)
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(50):
+        torch.nn.functional.linear(a, w)
+    e.record()
+    torch.cuda.synchronize()
+    out["%dx%d_m%d" % (n, k, m)] = s.elapsed_time(e) * 1e3 / 50
+    del a, w
+print(json.dumps(out))
+"""
+
+
+GEMM_SHAPES = ((4096, 4096), (6144, 4096), (28672, 4096), (4096, 14336))
+
+
+def vendor_gemm(m=512):
+    """Microseconds per call of the vendor fp16 GEMM at GEMM_SHAPES, from a
+    child process; started before this process touches the GPU."""
+    import subprocess
+    child = subprocess.run([sys.executable, "-c", _VENDOR_GEMM, json.dumps([[m, n, k] for n, k in GEMM_SHAPES])],
+                           capture_output=True, text=True, timeout=600)
+    if child.returncode != 0:
+        return {"vendor_error": (child.stderr.strip().splitlines() or ["exit %d" % child.returncode])[-1]}
+    return json.loads(child.stdout.strip().splitlines()[-1])
+
+
+def gemm_shapes_leg(dev, vendor):
+    """The fused Q4_K GEMM at the Llama-8B prefill shapes (M = 512: Q|K|V
+    6144x4096, W_o 4096x4096, gate|up 28672x4096, down 4096x14336) beside the
+    vendor library's fp16 GEMM on fp16 weights with no dequantization
+    (torch.nn.functional.linear, which calls hipBLASLt; `vendor` from
+    vendor_gemm, a child process, since torch brings its own HIP runtime): a
+    practical ceiling for the matrix cores at these shapes."""
+    from aihost_amd import _native as nat
+    m = 512
+    out = {}
+    for n, k in GEMM_SHAPES:
+        flops = 2.0 * m * n * k
+        gb = GemmBench(dev, nat.Q4_K, n, k, m)
+        ms = gb.time(10)
+        gb.close()
+        key = "%dx%d_m%d" % (n, k, m)
+        r = {"q4_k_fused_us_per_call": round(ms * 1e3, 1),
+             "q4_k_fused_TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1)}
+        if key in vendor:
+            r["vendor_fp16_us_per_call"] = round(vendor[key], 1)
+            r["vendor_fp16_TFLOP/s"] = round(flops / (vendor[key] * 1e-6) / 1e12, 1)
+        out[key] = r
+    if "vendor_error" in vendor:
+        out["vendor_error"] = vendor["vendor_error"]
+    return out
+
+
 def small_batch_leg(dev, steps=600):
     """Q6_K 4096x14336 at 4 and 8 activation columns (the matrix-core kernel
     and its sum of the K splits), graphs of 60 calls: 120 kernel nodes, a size
@@ -416,10 +478,13 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary workloads")
     ap.add_argument("--no-decoder", action="store_true", help="skip the full-decoder prefill/decode leg")
     ap.add_argument("--decoder-distinct-layers", type=int, default=2)
-    ap.add_argument("--only", choices=("ceilings", "gemm", "decoder-eager", "small-batch"),
+    ap.add_argument("--only", choices=("ceilings", "gemm", "gemm-shapes", "decoder-eager", "small-batch"),
                     help="one leg alone, for profiling (one JSON line): the stream-read ceilings and the launch "
-                         "floor; the prefill GEMM; the decoder with eager decode steps (no graph); the Q6_K "
-                         "4096x14336 matvec at 4 and 8 columns")
+                         "floor; the prefill GEMM; the GEMM at the prefill shapes beside the vendor fp16 GEMM; "
+                         "the decoder with eager decode steps (no graph); the Q6_K 4096x14336 matvec at 4 and "
+                         "8 columns")
+    ap.add_argument("--no-vendor", action="store_true",
+                    help="with --only gemm-shapes: skip the vendor GEMM's child process (for profiler runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -431,6 +496,7 @@ def main():
     if args.steps < 1:
         print("--steps must be at least 1", file=sys.stderr)
         sys.exit(2)
+    vendor = vendor_gemm() if args.only == "gemm-shapes" and not args.no_vendor else {}
     dev = C.HipComputeDevice(0)
     n, k = 14336, 4096
     if args.only == "ceilings":
@@ -439,6 +505,10 @@ def main():
         return
     if args.only == "gemm":
         print(json.dumps(gemm_leg(dev)))
+        dev.dispose()
+        return
+    if args.only == "gemm-shapes":
+        print(json.dumps(gemm_shapes_leg(dev, vendor)))
         dev.dispose()
         return
     if args.only == "small-batch":

@@ -24,7 +24,7 @@ HIP_ERROR_OUT_OF_MEMORY = 2
 
 F32, Q4_0, Q8_0, Q4_K, Q6_K = 0, 2, 8, 12, 14
 F16_IEEE, F16_REFCPU = 0, 1
-PRE_NONE, PRE_RMSNORM, PRE_SILU_MUL = 0, 1, 2
+PRE_NONE, PRE_RMSNORM, PRE_SILU_MUL, PRE_SILU_PAIRS = 0, 1, 2, 3
 POST_STORE, POST_ACCUMULATE, POST_SILU_PAIRS = 0, 1, 2
 
 
@@ -68,6 +68,7 @@ SIGNATURES = {
     "aih_qmatvec": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _i]),
     "aih_qmatvec_fused": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _vp, _f, _i, _i, _vp]),
     "aih_qgemm": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),
+    "aih_qgemm_fused": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _vp, _f, _i64, _i, _i, _vp]),
     "aih_matmul_weights_q": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),
     "aih_matmul_weights_q_noalloc": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),
     "aih_probe_stream_read": (_i, [_vp, _vp, _u64, _i, _vp]),
@@ -84,6 +85,8 @@ SIGNATURES = {
     "aih_attention_scratch_floats": (_i64, [ctypes.c_int32, ctypes.c_int32]),
     "aih_attention": (_i, [_vp, _vp, _vp, _vp, _vp, _i64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                            ctypes.c_int32, _vp, ctypes.c_int32, _f, _vp, _i64]),
+    "aih_attention_strided": (_i, [_vp, _vp, _i64, _vp, _vp, _vp, _i64, ctypes.c_int32, ctypes.c_int32,
+                                   ctypes.c_int32, ctypes.c_int32, _vp, ctypes.c_int32, _f, _vp, _i64]),
     "aih_attention_decode_qkv": (_i, [_vp, _vp, _vp, _vp, _vp, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                       ctypes.c_int32, _vp, _vp, ctypes.c_int32, ctypes.c_int32, _f, _vp, _i64]),
     "aih_embed_q": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),

@@ -683,9 +683,9 @@ constexpr int kRV = 68;
 constexpr int kRP = 68;
 
 __global__ void __launch_bounds__(256)
-attn_prefill_kernel(const float *__restrict__ Q, const float *__restrict__ Kc, const float *__restrict__ Vc,
-                    float *__restrict__ O, int64_t n_q, int32_t n_heads, int32_t n_kv_heads, int32_t start,
-                    const int32_t *pos, int32_t max_len, float scale)
+attn_prefill_kernel(const float *__restrict__ Q, int64_t ldq, const float *__restrict__ Kc,
+                    const float *__restrict__ Vc, float *__restrict__ O, int64_t n_q, int32_t n_heads,
+                    int32_t n_kv_heads, int32_t start, const int32_t *pos, int32_t max_len, float scale)
 {
     __shared__ __align__(16) float ks[kKT * kRK];
     __shared__ __align__(16) float vt[kHD * kRV];
@@ -702,7 +702,7 @@ attn_prefill_kernel(const float *__restrict__ Q, const float *__restrict__ Kc, c
     // Q fragments: query 16w + c, dims 4s + g (rows past n_q read the last row, never stored)
     float qf[32];
     {
-        const float *qrow = Q + min<int64_t>(i0 + 16 * w + c, n_q - 1) * q_stride + (int64_t)h * kHD;
+        const float *qrow = Q + min<int64_t>(i0 + 16 * w + c, n_q - 1) * ldq + (int64_t)h * kHD;
 #pragma unroll
         for (int s = 0; s < 32; ++s) qf[s] = qrow[4 * s + g];
     }
@@ -915,6 +915,88 @@ argmax_kernel(const float *__restrict__ X, int64_t n, int32_t *token, int32_t *p
     }
 }
 
+// ---------------------------------------------------------------- GEMM operand
+// The activation operand of the prefill GEMM computed by the element-wise step
+// before it and written straight in the GEMM's fp16 fragment order
+// (aih_qgemm.hip: the A operand of v_mfma_f32_32x32x16_f16 for rows
+// 32 mb .. +31 and k 16 kk .. +15 is the 1 KB block mb * K/16 + kk, lane
+// l = row % 32 + 32 * (k / 8 % 2) at 16 bytes * l).  One workgroup per row;
+// rows M .. mpad-1 (mpad = M rounded up to 32) are zero.  The arithmetic is
+// that of rmsnorm_kernel, silu_mul_kernel and silu_mul_pairs_kernel, rounded
+// to fp16 as the GEMM's own conversion does, so the operand is the one the
+// separate operator and aih_qgemm would have built.
+//   PRE = AIH_PRE_RMSNORM     x = (X / sqrt(mean(X^2) + eps)) * X2   (X2: K weights)
+//   PRE = AIH_PRE_SILU_MUL    x = SiLU(X) * X2                        (X2: M x K)
+//   PRE = AIH_PRE_SILU_PAIRS  x[k] = SiLU(X[2k]) * X[2k+1]            (X: M x 2K)
+template <int PRE>
+__global__ void __launch_bounds__(256)
+x_tile_pre_kernel(const float *__restrict__ X, const float *__restrict__ X2, float eps, int64_t M, int64_t K,
+                  _Float16 *__restrict__ Xt)
+{
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    __shared__ float red[4];
+    const int64_t m = blockIdx.x;
+    _Float16 *base = Xt + (((m >> 5) * (K / 16)) * 64 + (m & 31)) * 8;
+    auto slot = [&](int64_t k) { return reinterpret_cast<h8 *>(base + ((k >> 4) * 64 + ((k >> 3) & 1) * 32) * 8); };
+    if (m >= M) {
+        for (int64_t k = 8 * (int64_t)threadIdx.x; k < K; k += 8 * 256) *slot(k) = h8{};
+        return;
+    }
+    const f4 *x4 = reinterpret_cast<const f4 *>(X + m * (PRE == AIH_PRE_SILU_PAIRS ? 2 * K : K));
+    float rms = 1.f;
+    if (PRE == AIH_PRE_RMSNORM) {
+        float ss = 0.f;
+        for (int64_t i = threadIdx.x; i < K / 4; i += 256) {
+            const f4 v = x4[i];
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+        ss = block_sum<256>(ss, red);
+        rms = sqrtf(ss / (float)K + eps);
+    }
+    for (int64_t k = 8 * (int64_t)threadIdx.x; k < K; k += 8 * 256) {
+        float o[8];
+        if (PRE == AIH_PRE_RMSNORM) {
+            const f4 *w4 = reinterpret_cast<const f4 *>(X2);
+            const f4 v[2] = {x4[k / 4], x4[k / 4 + 1]}, w[2] = {w4[k / 4], w4[k / 4 + 1]};
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                o[4 * j] = (v[j].x / rms) * w[j].x;
+                o[4 * j + 1] = (v[j].y / rms) * w[j].y;
+                o[4 * j + 2] = (v[j].z / rms) * w[j].z;
+                o[4 * j + 3] = (v[j].w / rms) * w[j].w;
+            }
+        } else {
+            float g[8], u[8];
+            if (PRE == AIH_PRE_SILU_MUL) {
+                const f4 *u4 = reinterpret_cast<const f4 *>(X2 + m * K);
+                const f4 a = x4[k / 4], b = x4[k / 4 + 1], c = u4[k / 4], d = u4[k / 4 + 1];
+                const float gg[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+                const float uu[8] = {c.x, c.y, c.z, c.w, d.x, d.y, d.z, d.w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) { g[j] = gg[j]; u[j] = uu[j]; }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const f4 p = x4[k / 2 + j];
+                    g[2 * j] = p.x;
+                    u[2 * j] = p.y;
+                    g[2 * j + 1] = p.z;
+                    u[2 * j + 1] = p.w;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float sig = 1.0f / (1.0f + expf(-g[j]));
+                o[j] = (g[j] * sig) * u[j];
+            }
+        }
+        h8 r;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r[j] = (_Float16)o[j];
+        *slot(k) = r;
+    }
+}
+
 unsigned grid_for(aih_ctx *ctx, int64_t work, int per_block = 256)
 {
     const int64_t want = (work + per_block - 1) / per_block;
@@ -950,6 +1032,30 @@ int launch_gqa(aih_ctx *ctx, int group, dim3 grid, const float *Qsrc, float *Kc,
 }
 
 }  // namespace
+
+int aih_launch_x_tile_pre(aih_ctx *ctx, int pre, const float *X, const float *X2, float eps, int64_t M, int64_t K,
+                          void *Xt)
+{
+    const int64_t mpad = (M + 31) / 32 * 32;
+    if (mpad > 0x7FFFFFFF) return AIH_E_LIMIT;
+    _Float16 *xt = static_cast<_Float16 *>(Xt);
+    switch (pre) {
+    case AIH_PRE_RMSNORM:
+        hipLaunchKernelGGL(x_tile_pre_kernel<AIH_PRE_RMSNORM>, dim3((unsigned)mpad), dim3(256), 0, ctx->stream, X, X2,
+                           eps, M, K, xt);
+        break;
+    case AIH_PRE_SILU_MUL:
+        hipLaunchKernelGGL(x_tile_pre_kernel<AIH_PRE_SILU_MUL>, dim3((unsigned)mpad), dim3(256), 0, ctx->stream, X, X2,
+                           eps, M, K, xt);
+        break;
+    case AIH_PRE_SILU_PAIRS:
+        hipLaunchKernelGGL(x_tile_pre_kernel<AIH_PRE_SILU_PAIRS>, dim3((unsigned)mpad), dim3(256), 0, ctx->stream, X,
+                           X2, eps, M, K, xt);
+        break;
+    default: return AIH_E_INVALID;
+    }
+    return aih_launch_status();
+}
 
 extern "C" {
 
@@ -1051,8 +1157,18 @@ int aih_attention(aih_ctx *ctx, const float *Q, const float *Kc, const float *Vc
                   int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t start, const int32_t *pos,
                   int32_t max_len, float scale, float *scratch, int64_t scratch_floats)
 {
+    return aih_attention_strided(ctx, Q, (int64_t)n_heads * head_dim, Kc, Vc, O, n_q, n_heads, n_kv_heads, head_dim,
+                                 start, pos, max_len, scale, scratch, scratch_floats);
+}
+
+int aih_attention_strided(aih_ctx *ctx, const float *Q, int64_t ldq, const float *Kc, const float *Vc, float *O,
+                          int64_t n_q, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t start,
+                          const int32_t *pos, int32_t max_len, float scale, float *scratch,
+                          int64_t scratch_floats)
+{
     if (!ctx || !Q || !Kc || !Vc || !O || n_q < 0 || n_heads <= 0 || n_kv_heads <= 0 || max_len <= 0)
         return AIH_E_INVALID;
+    if (ldq < (int64_t)n_heads * head_dim || ldq % 4) return AIH_E_INVALID;
     if (n_heads % n_kv_heads) return AIH_E_INVALID;
     if (head_dim != kHD) return AIH_E_UNSUPPORTED;
     if (!aligned16(Q) || !aligned16(Kc) || !aligned16(Vc) || !aligned16(O)) return AIH_E_INVALID;
@@ -1078,8 +1194,8 @@ int aih_attention(aih_ctx *ctx, const float *Q, const float *Kc, const float *Vc
     }
     const int64_t tiles = (n_q + kQTile - 1) / kQTile;
     if (tiles > 65535) return AIH_E_LIMIT;
-    hipLaunchKernelGGL(attn_prefill_kernel, dim3(n_heads, (unsigned)tiles), dim3(256), 0, ctx->stream, Q, Kc, Vc, O,
-                       n_q, n_heads, n_kv_heads, start, pos, max_len, scale);
+    hipLaunchKernelGGL(attn_prefill_kernel, dim3(n_heads, (unsigned)tiles), dim3(256), 0, ctx->stream, Q, ldq, Kc, Vc,
+                       O, n_q, n_heads, n_kv_heads, start, pos, max_len, scale);
     return aih_launch_status();
 }
 

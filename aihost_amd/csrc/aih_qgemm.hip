@@ -98,7 +98,7 @@ template <> struct GRing<G6K> { static constexpr int PR = 2; };
 template <class T>
 __global__ void __launch_bounds__(512)
 qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
-             const _Float16 *__restrict__ Xt, int64_t M, float *__restrict__ Y)
+             const _Float16 *__restrict__ Xt, int64_t M, float *__restrict__ Y, int accumulate)
 {
     constexpr int PR = GRing<T>::PR;
     __shared__ __align__(16) _Float16 wsh[2][BN][LD2];
@@ -236,8 +236,8 @@ qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
         const int i = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         const int64_t m = m0 + 32 * wave + i;
         if (m < M) {
-            if (na < N) Y[m * N + na] = acc0[r];
-            if (nb < N) Y[m * N + nb] = acc1[r];
+            if (na < N) Y[m * N + na] = accumulate ? Y[m * N + na] + acc0[r] : acc0[r];
+            if (nb < N) Y[m * N + nb] = accumulate ? Y[m * N + nb] + acc1[r] : acc1[r];
         }
     }
 }
@@ -261,7 +261,7 @@ constexpr int PR256 = 2;
 template <class T>
 __global__ void __launch_bounds__(512)
 qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
-                const _Float16 *__restrict__ Xt, int64_t M, float *__restrict__ Y)
+                const _Float16 *__restrict__ Xt, int64_t M, float *__restrict__ Y, int accumulate)
 {
     constexpr int PR = PR256;
     typedef typename Piece32<T>::type P;
@@ -382,15 +382,15 @@ qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
         const int i = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         const int64_t m = m0 + 32 * wave + i;
         if (m < M) {
-            if (na < N) Y[m * N + na] = acc0[r];
-            if (nb < N) Y[m * N + nb] = acc1[r];
+            if (na < N) Y[m * N + na] = accumulate ? Y[m * N + na] + acc0[r] : acc0[r];
+            if (nb < N) Y[m * N + nb] = accumulate ? Y[m * N + nb] + acc1[r] : acc1[r];
         }
     }
 }
 
 template <class T>
 int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
-           const _Float16 *Xh, int64_t M, float *Y)
+           const _Float16 *Xh, int64_t M, float *Y, int accumulate)
 {
     const int64_t gx = (N + BN - 1) / BN, gy = (M + BM - 1) / BM, gy2 = (M + BM2 - 1) / BM2;
     if (gy > 65535 || gx > 0x7FFFFFFF) return AIH_E_LIMIT;
@@ -402,14 +402,41 @@ int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t row_byt
     const int64_t rounds = (gx * gy + cus - 1) / cus, rounds2 = (gx * gy2 + cus - 1) / cus;
     if (5 * rounds2 < 4 * rounds)
         hipLaunchKernelGGL((qgemm256_kernel<T>), dim3((unsigned)gx, (unsigned)gy2), dim3(512), 0, ctx->stream,
-                           W, N, K, row_bytes, Xh, M, Y);
+                           W, N, K, row_bytes, Xh, M, Y, accumulate);
     else
         hipLaunchKernelGGL((qgemm_kernel<T>), dim3((unsigned)gx, (unsigned)gy), dim3(512), 0, ctx->stream,
-                           W, N, K, row_bytes, Xh, M, Y);
+                           W, N, K, row_bytes, Xh, M, Y, accumulate);
     return aih_launch_status();
 }
 
 }  // namespace
+
+int aih_launch_qgemm_tiled(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const void *Xtv,
+                           int64_t M, float *Y, int accumulate)
+{
+    if (K % BK != 0) return AIH_E_LIMIT;
+    const int64_t rb = aih_row_bytes(type, K);
+    const uint8_t *w = static_cast<const uint8_t *>(W);
+    const _Float16 *Xt = static_cast<const _Float16 *>(Xtv);
+    switch (type) {
+    case AIH_TYPE_Q4_K: return launch<G4K>(ctx, w, N, K, rb, Xt, M, Y, accumulate);
+    case AIH_TYPE_Q6_K: return launch<G6K>(ctx, w, N, K, rb, Xt, M, Y, accumulate);
+    case AIH_TYPE_Q8_0: return launch<G80>(ctx, w, N, K, rb, Xt, M, Y, accumulate);
+    case AIH_TYPE_Q4_0: return launch<G40>(ctx, w, N, K, rb, Xt, M, Y, accumulate);
+    default: return AIH_E_UNSUPPORTED;
+    }
+}
+
+int aih_launch_x_tile(aih_ctx *ctx, const float *X, int64_t M, int64_t K, void *Xt)
+{
+    const int64_t mpad = (M + 31) / 32 * 32;
+    const int64_t nslots = mpad * K / 8;
+    const int64_t blocks = (nslots + 255) / 256;
+    const unsigned grid = (unsigned)(blocks < 8192 ? blocks : 8192);
+    hipLaunchKernelGGL(x_tile_kernel, dim3(grid), dim3(256), 0, ctx->stream, X, M, K, static_cast<_Float16 *>(Xt),
+                       nslots);
+    return aih_launch_status();
+}
 
 int aih_launch_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
                      const float *X, int64_t M, float *Y, const aih_scratch *ext)
@@ -421,20 +448,7 @@ int aih_launch_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K
     void *work = nullptr;
     int rc = aih_stage(ctx, ext, (size_t)mpad * (size_t)K * sizeof(_Float16), &work);
     if (rc) return rc;
-    _Float16 *xh = static_cast<_Float16 *>(work);
-    const int64_t nslots = mpad * K / 8;
-    const int64_t blocks = (nslots + 255) / 256;
-    const unsigned grid = (unsigned)(blocks < 8192 ? blocks : 8192);
-    hipLaunchKernelGGL(x_tile_kernel, dim3(grid), dim3(256), 0, ctx->stream, X, M, K, xh, nslots);
-    rc = aih_launch_status();
+    rc = aih_launch_x_tile(ctx, X, M, K, work);
     if (rc) return rc;
-    const int64_t rb = aih_row_bytes(type, K);
-    const uint8_t *w = static_cast<const uint8_t *>(W);
-    switch (type) {
-    case AIH_TYPE_Q4_K: return launch<G4K>(ctx, w, N, K, rb, xh, M, Y);
-    case AIH_TYPE_Q6_K: return launch<G6K>(ctx, w, N, K, rb, xh, M, Y);
-    case AIH_TYPE_Q8_0: return launch<G80>(ctx, w, N, K, rb, xh, M, Y);
-    case AIH_TYPE_Q4_0: return launch<G40>(ctx, w, N, K, rb, xh, M, Y);
-    default: return AIH_E_UNSUPPORTED;
-    }
+    return aih_launch_qgemm_tiled(ctx, type, W, N, K, work, M, Y, 0);
 }

@@ -230,8 +230,10 @@ class LlamaDecoder:
         # prefill: gate and up (interleaved with a fused gate|up buffer), then
         # SiLU(gate) * up in self.up
         self.gate, self.up = buf(P * 2 * c.ffn * 4), buf(P * c.ffn * 4)
-        # decode: outputs of the fused Q|K|V and gate|up (SiLU-pairs) matvecs
-        self.qkv = buf((qd + 2 * c.kv_dim) * 4)
+        # outputs of the fused Q|K|V projection (one row in decode, up to
+        # max_prefill rows in the fused prefill) and of the decode gate|up
+        # (SiLU-pairs) matvec
+        self.qkv = buf(P * (qd + 2 * c.kv_dim) * 4)
         self.gu = buf(c.ffn * 4)
         self.logits = buf(c.vocab * 4)
         self.kc = [buf(self.max_len * c.kv_dim * 4) for _ in range(c.n_layers)]
@@ -260,6 +262,9 @@ class LlamaDecoder:
         self.pairs_epilogue = teams > 0 and (2 * c.ffn) % teams == 0
         # the fused decode attention serves query groups of 1, 2, 4 or 8 heads
         self.fused_attention = c.n_heads // c.n_kv_heads in (1, 2, 4, 8)
+        # prompts of more than 8 rows (the GEMM's range) run the fused prefill
+        # layer (_prefill_layer_fused); False selects the separate operators
+        self.fused_prefill = True
 
     # -- operators (thin checked wrappers)
     def _mm(self, name, X, M, Y):
@@ -277,6 +282,42 @@ class LlamaDecoder:
         nat.check(self.L.aih_qmatvec_fused(self.h, qt, ptr, n, k, X, X2, self.cfg.eps, pre, post, Y),
                   "fused matvec %s" % name)
 
+    def _mmx(self, name, X, X2, pre, post, M, Y):
+        """Prefill GEMM with a fused prologue (RMSNorm, SiLU*up, SiLU of
+        gate/up pairs) and epilogue (residual add), aih_qgemm_fused."""
+        qt, ptr, n, k = self.w[name]
+        nat.check(self.L.aih_qgemm_fused(self.h, qt, ptr, n, k, X, X2, self.cfg.eps, M, pre, post, Y),
+                  "fused GEMM %s" % name)
+
+    def _prefill_layer_fused(self, l, rows, start, pos):
+        """One layer over `rows` > 8 prompt rows in six GEMM-centred steps: the
+        Q|K|V GEMM with the attention RMSNorm computed into its operand, RoPE
+        and the cache store, attention reading the query block in place, the
+        W_o GEMM adding into x, the gate|up GEMM with the FFN RMSNorm in its
+        operand, the down GEMM with SiLU(gate)*up in its operand adding into x.
+        Bit for bit the result of the separate operators (layer())."""
+        c, L, h, p = self.cfg, self.L, self.h, "blk.%d." % l
+        qd = c.n_heads * c.head_dim
+        ld = qd + 2 * c.kv_dim
+        self._mmx(p + "attn_qkv", self.x, self.w.ptr(p + "attn_norm"), nat.PRE_RMSNORM, nat.POST_STORE, rows,
+                  self.qkv)
+        q, k, v = self.qkv, self.qkv + qd * 4, self.qkv + (qd + c.kv_dim) * 4
+        nat.check(L.aih_rope_qkv(h, q, ld, k, ld, v, ld, self.kc[l], self.vc[l], rows, c.n_heads, c.n_kv_heads,
+                                 c.head_dim, start, pos, self.table, self.max_len, self.max_len),
+                  "rope q, k -> cache, v -> cache")
+        nat.check(L.aih_attention_strided(h, q, ld, self.kc[l], self.vc[l], self.att, rows, c.n_heads,
+                                          c.n_kv_heads, c.head_dim, start, pos, self.max_len, self.scale,
+                                          self.scratch, self.scratch_floats), "attention")
+        self._mmx(p + "attn_output", self.att, None, nat.PRE_NONE, nat.POST_ACCUMULATE, rows, self.x)
+        norm = self.w.ptr(p + "ffn_norm")
+        if p + "ffn_gate_up" in self.w:
+            self._mmx(p + "ffn_gate_up", self.x, norm, nat.PRE_RMSNORM, nat.POST_STORE, rows, self.gate)
+            self._mmx(p + "ffn_down", self.gate, None, nat.PRE_SILU_PAIRS, nat.POST_ACCUMULATE, rows, self.x)
+        else:
+            self._mmx(p + "ffn_gate", self.x, norm, nat.PRE_RMSNORM, nat.POST_STORE, rows, self.gate)
+            self._mmx(p + "ffn_up", self.x, norm, nat.PRE_RMSNORM, nat.POST_STORE, rows, self.up)
+            self._mmx(p + "ffn_down", self.gate, self.up, nat.PRE_SILU_MUL, nat.POST_ACCUMULATE, rows, self.x)
+
     def layer(self, l, rows, start, pos):
         """One decoder layer over `rows` activation rows at positions start..
         (+*pos when pos is a device pointer).  A single row (decode) runs as
@@ -284,9 +325,14 @@ class LlamaDecoder:
         attention with RoPE and the KV cache store fused in (two kernels),
         W_o matvec adding into x, gate|up matvec with the FFN RMSNorm fused in
         and SiLU(gate)*up as its epilogue, down matvec adding into x.
-        Several rows (prefill) use the GEMM and the separate operators."""
+        More than 8 rows (prefill) run _prefill_layer_fused; with
+        fused_prefill off, or up to 8 rows, the matmuls and the separate
+        operators."""
         c, L, h, p = self.cfg, self.L, self.h, "blk.%d." % l
         qd = c.n_heads * c.head_dim
+        if self.fused_prefill and rows > 8 and p + "attn_qkv" in self.w:
+            self._prefill_layer_fused(l, rows, start, pos)
+            return
         decode = rows == 1 and p + "attn_qkv" in self.w
         if decode:
             self._mmf(p + "attn_qkv", self.x, self.w.ptr(p + "attn_norm"), nat.PRE_RMSNORM, nat.POST_STORE,

@@ -218,6 +218,9 @@ int aih_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
 #define AIH_POST_STORE      0
 #define AIH_POST_ACCUMULATE 1
 #define AIH_POST_SILU_PAIRS 2
+/* aih_qgemm_fused only:  x[k] = SiLU(X[2k]) * X[2k+1]  (X rows of 2K floats:
+ * the output of a GEMM over gate/up rows interleaved; X2 unused). */
+#define AIH_PRE_SILU_PAIRS  3
 int aih_qmatvec_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *X,
                       const float *X2, float eps, int pre, int post, float *Y);
 
@@ -236,6 +239,26 @@ int aih_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
  * aih_qmatvec and larger M to aih_qgemm. */
 int aih_matmul_weights_q(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
                          const float *X, int64_t M, float *Y);
+
+/* Prefill GEMM with the neighbouring element-wise steps of a Llama layer
+ * fused in:  y[m, n] = sum_k x[m, k] W[n, k] for M rows, with
+ *   pre = AIH_PRE_NONE        x = X
+ *   pre = AIH_PRE_RMSNORM     x[m] = (X[m] / sqrt(mean(X[m]^2) + eps)) * X2   (X2: K norm weights)
+ *   pre = AIH_PRE_SILU_MUL    x = SiLU(X) * X2                               (X2: M x K)
+ *   pre = AIH_PRE_SILU_PAIRS  x[m, k] = SiLU(X[m, 2k]) * X[m, 2k+1]           (X: M x 2K)
+ * and
+ *   post = AIH_POST_STORE       Y[m, n] = y[m, n]
+ *   post = AIH_POST_ACCUMULATE  Y[m, n] += y[m, n]      (the residual add)
+ * The element-wise step writes the GEMM's fp16 operand directly (no fp32
+ * intermediate, no separate conversion) with the formulas of aih_rmsnorm,
+ * aih_silu_mul, aih_silu_mul_pairs and aih_add, so the result is bit for bit
+ * that of the separate operator, then aih_qgemm (and aih_add).  Workspace,
+ * K and alignment rules as aih_qgemm; X, X2 16-byte aligned; Y must not
+ * alias X or X2.  Replaces, for a prompt, the LayerNorm / SiLU+Multiply /
+ * Add around MatMulWeights in ComputeOps.TransformerLayer
+ * (ComputeOps.cs:1250-1356) and FeedForward (ComputeOps.cs:1218-1241). */
+int aih_qgemm_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *X,
+                    const float *X2, float eps, int64_t M, int pre, int post, float *Y);
 
 /* aih_matmul_weights_q without any allocation.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory -- code
@@ -330,6 +353,15 @@ int64_t aih_attention_scratch_floats(int32_t n_heads, int32_t max_len);
 int aih_attention(aih_ctx *ctx, const float *Q, const float *Kc, const float *Vc, float *O, int64_t n_q,
                   int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t start, const int32_t *pos,
                   int32_t max_len, float scale, float *scratch, int64_t scratch_floats);
+
+/* aih_attention with query rows ldq floats apart (ldq >= n_heads*head_dim,
+ * a multiple of 4): the query block of a fused Q|K|V projection output read
+ * in place.  O rows stay n_heads*head_dim floats apart.  Same results as
+ * aih_attention on the same query values. */
+int aih_attention_strided(aih_ctx *ctx, const float *Q, int64_t ldq, const float *Kc, const float *Vc, float *O,
+                          int64_t n_q, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t start,
+                          const int32_t *pos, int32_t max_len, float scale, float *scratch,
+                          int64_t scratch_floats);
 
 /* One decode step's attention with the position steps before it fused in:
  * for the projection output QKV of one row at position p = start + *pos

@@ -1,0 +1,199 @@
+"""Fused prefill steps against the separate operators they replace, bit for bit:
+
+- aih_qgemm_fused with each prologue (RMSNorm, SiLU*up, SiLU of gate/up pairs)
+  and epilogue (residual add) vs aih_rmsnorm / aih_silu_mul / aih_silu_mul_pairs,
+  aih_qgemm and aih_add, on the 128-row and the 256-row GEMM tiles, with a
+  partial last row block (rows past M are zero in the operand);
+- aih_attention_strided reading the query block of a Q|K|V row in place vs
+  aih_attention on a contiguous copy;
+- a decoder prefill through the fused layer vs the same prompt through the
+  separate operators: logits and K/V caches identical.
+"""
+import numpy as np
+import pytest
+
+from aihost_amd import _native as nat
+from aihost_amd import llama
+from gpu_util import synth_weight, upload
+
+pytestmark = pytest.mark.gpu
+
+EPS = 1e-5
+
+
+def _read(buf, n):
+    return buf.read_range(0, n, np.float32)
+
+
+def _check(st, what):
+    nat.check(st, what)
+
+
+def _read_ptr(device, ptr, n):
+    out = np.empty(n, np.float32)
+    nat.check(nat.lib().aih_memcpy_d2h(device.handle, out.ctypes.data, ptr, out.nbytes), "aih_memcpy_d2h")
+    return out
+
+
+def _separate(device, qtype, wb, n, k, m, pre, post, xb, x2b, y0):
+    """The operators aih_qgemm_fused replaces, one after the other."""
+    L, h = nat.lib(), device.handle
+    opb = device.create_buffer(m * k * 4)
+    yb = upload(device, y0)
+    tmp = device.create_buffer(m * n * 4)
+    try:
+        if pre == nat.PRE_NONE:
+            src = xb
+        elif pre == nat.PRE_RMSNORM:
+            _check(L.aih_rmsnorm(h, xb.get_pointer(), x2b.get_pointer(), opb.get_pointer(), m, k, EPS), "rmsnorm")
+            src = opb
+        elif pre == nat.PRE_SILU_MUL:
+            _check(L.aih_silu_mul(h, xb.get_pointer(), x2b.get_pointer(), opb.get_pointer(), m * k), "silu_mul")
+            src = opb
+        else:
+            _check(L.aih_silu_mul_pairs(h, xb.get_pointer(), opb.get_pointer(), m, k), "silu_mul_pairs")
+            src = opb
+        if post == nat.POST_STORE:
+            _check(L.aih_qgemm(h, qtype, wb.get_pointer(), n, k, src.get_pointer(), m, yb.get_pointer()), "qgemm")
+        else:
+            _check(L.aih_qgemm(h, qtype, wb.get_pointer(), n, k, src.get_pointer(), m, tmp.get_pointer()), "qgemm")
+            _check(L.aih_add(h, yb.get_pointer(), tmp.get_pointer(), yb.get_pointer(), m * n), "add")
+        return _read(yb, m * n)
+    finally:
+        for b in (opb, yb, tmp):
+            b.dispose()
+
+
+def _fused(device, qtype, wb, n, k, m, pre, post, xb, x2b, y0):
+    yb = upload(device, y0)
+    try:
+        _check(nat.lib().aih_qgemm_fused(device.handle, qtype, wb.get_pointer(), n, k, xb.get_pointer(),
+                                         x2b.get_pointer() if x2b is not None else None, EPS, m, pre, post,
+                                         yb.get_pointer()), "aih_qgemm_fused")
+        return _read(yb, m * n)
+    finally:
+        yb.dispose()
+
+
+MODES = [(nat.PRE_RMSNORM, nat.POST_STORE), (nat.PRE_NONE, nat.POST_ACCUMULATE),
+         (nat.PRE_SILU_PAIRS, nat.POST_ACCUMULATE), (nat.PRE_SILU_MUL, nat.POST_STORE),
+         (nat.PRE_RMSNORM, nat.POST_ACCUMULATE), (nat.PRE_NONE, nat.POST_STORE)]
+
+
+# (Q4_K, 6400, 1024, 300) takes the 256-row tiles on a 256-CU device
+@pytest.mark.parametrize("qtype,n,k,m", [(nat.Q4_K, 192, 512, 40), (nat.Q6_K, 100, 768, 77),
+                                         (nat.Q8_0, 70, 320, 9), (nat.Q4_K, 6400, 1024, 300)])
+def test_qgemm_fused_equals_separate_operators(device, qtype, n, k, m):
+    rng = np.random.default_rng(n + k + m)
+    w = synth_weight(qtype, n, k, seed=k)
+    wb = upload(device, w)
+    try:
+        for pre, post in MODES:
+            xw = 2 * k if pre == nat.PRE_SILU_PAIRS else k
+            x = rng.standard_normal((m, xw)).astype(np.float32)
+            x2 = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32) if pre == nat.PRE_RMSNORM else \
+                rng.standard_normal((m, k)).astype(np.float32)
+            y0 = rng.standard_normal((m, n)).astype(np.float32)
+            xb, x2b = upload(device, x), upload(device, x2)
+            try:
+                x2_arg = x2b if pre in (nat.PRE_RMSNORM, nat.PRE_SILU_MUL) else None
+                ref = _separate(device, qtype, wb, n, k, m, pre, post, xb, x2b, y0)
+                got = _fused(device, qtype, wb, n, k, m, pre, post, xb, x2_arg, y0)
+                assert np.isfinite(ref).all()
+                assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), \
+                    "type %d %dx%d M=%d pre %d post %d: %d of %d differ" % (
+                        qtype, n, k, m, pre, post, int(np.sum(got != ref)), got.size)
+            finally:
+                xb.dispose()
+                x2b.dispose()
+    finally:
+        wb.dispose()
+
+
+def test_qgemm_fused_argument_errors(device):
+    L, h = nat.lib(), device.handle
+    n, k, m = 64, 256, 16
+    wb = upload(device, synth_weight(nat.Q4_K, n, k))
+    xb = device.create_buffer(m * 2 * k * 4)
+    yb = device.create_buffer(m * n * 4)
+    try:
+        w, x, y = wb.get_pointer(), xb.get_pointer(), yb.get_pointer()
+        assert L.aih_qgemm_fused(h, nat.Q4_K, w, n, k, x, None, EPS, m, nat.PRE_RMSNORM, 0, y) == nat.AIH_E_INVALID
+        assert L.aih_qgemm_fused(h, nat.Q4_K, w, n, k, x, None, EPS, m, nat.PRE_SILU_MUL, 0, y) == nat.AIH_E_INVALID
+        assert L.aih_qgemm_fused(h, nat.Q4_K, w, n, k, x, None, EPS, m, 4, 0, y) == nat.AIH_E_INVALID
+        assert L.aih_qgemm_fused(h, nat.Q4_K, w, n, k, x, None, EPS, m, 0, nat.POST_SILU_PAIRS, y) == \
+            nat.AIH_E_INVALID
+        assert L.aih_qgemm_fused(h, nat.Q4_K, w, n, k, x + 4, None, EPS, m, 0, 0, y) == nat.AIH_E_INVALID
+        assert L.aih_qgemm_fused(h, nat.F32, w, n, k, x, None, EPS, m, 0, 0, y) == nat.AIH_E_UNSUPPORTED
+        # K a whole number of Q8_0 blocks but not of 64-element GEMM steps
+        assert L.aih_qgemm_fused(h, nat.Q8_0, w, n, 96, x, None, EPS, m, 0, 0, y) == nat.AIH_E_LIMIT
+        assert L.aih_qgemm_fused(h, nat.Q4_K, w, n, k, x, None, EPS, 0, nat.PRE_SILU_PAIRS, 0, y) == nat.AIH_OK
+    finally:
+        for b in (wb, xb, yb):
+            b.dispose()
+
+
+@pytest.mark.parametrize("n_q,start", [(100, 0), (70, 30)])
+def test_attention_strided_equals_contiguous(device, n_q, start):
+    L, h = nat.lib(), device.handle
+    n_heads, n_kv, hd, max_len = 8, 2, 128, 160
+    qd, kvd = n_heads * hd, n_kv * hd
+    ld = qd + 2 * kvd
+    rng = np.random.default_rng(n_q + start)
+    qkv = rng.standard_normal((n_q, ld)).astype(np.float32)
+    kc = rng.standard_normal((max_len, kvd)).astype(np.float32)
+    vc = rng.standard_normal((max_len, kvd)).astype(np.float32)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    bufs = [upload(device, a) for a in (qkv, np.ascontiguousarray(qkv[:, :qd]), kc, vc)]
+    o1, o2 = device.create_buffer(n_q * qd * 4), device.create_buffer(n_q * qd * 4)
+    sf = int(L.aih_attention_scratch_floats(n_heads, max_len))
+    sb = device.create_buffer(sf * 4)
+    try:
+        qs, qc, kb, vb = bufs
+        _check(L.aih_attention_strided(h, qs.get_pointer(), ld, kb.get_pointer(), vb.get_pointer(), o1.get_pointer(),
+                                       n_q, n_heads, n_kv, hd, start, None, max_len, scale, sb.get_pointer(), sf),
+               "strided")
+        _check(L.aih_attention(h, qc.get_pointer(), kb.get_pointer(), vb.get_pointer(), o2.get_pointer(), n_q,
+                               n_heads, n_kv, hd, start, None, max_len, scale, sb.get_pointer(), sf), "contiguous")
+        a, b = _read(o1, n_q * qd), _read(o2, n_q * qd)
+        assert np.isfinite(b).all()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        assert L.aih_attention_strided(h, qs.get_pointer(), qd - 4, kb.get_pointer(), vb.get_pointer(),
+                                       o1.get_pointer(), n_q, n_heads, n_kv, hd, start, None, max_len, scale,
+                                       sb.get_pointer(), sf) == nat.AIH_E_INVALID
+        assert L.aih_attention_strided(h, qs.get_pointer(), ld + 2, kb.get_pointer(), vb.get_pointer(),
+                                       o1.get_pointer(), n_q, n_heads, n_kv, hd, start, None, max_len, scale,
+                                       sb.get_pointer(), sf) == nat.AIH_E_INVALID
+    finally:
+        for x in bufs + [o1, o2, sb]:
+            x.dispose()
+
+
+CFG = llama.LlamaConfig(n_layers=2, dim=512, n_heads=4, n_kv_heads=2, head_dim=128, ffn=1024, vocab=1000)
+
+
+def test_fused_prefill_layer_equals_separate_operators(device):
+    w = llama.synth_weights(CFG, seed=11)
+    dw = llama.DeviceWeights(device, w)
+    ids = np.random.default_rng(4).integers(0, CFG.vocab, 45).astype(np.int32)
+    out = []
+    try:
+        for fused in (True, False):
+            dec = llama.LlamaDecoder(device, CFG, dw, 96, 48)
+            try:
+                dec.fused_prefill = fused
+                tok = dec.prefill(ids)
+                logits = dec.read_logits()
+                caches = [np.concatenate([_read_ptr(device, b, 96 * CFG.kv_dim) for b in (dec.kc[l], dec.vc[l])])
+                          for l in range(CFG.n_layers)]
+                out.append((tok, logits, caches))
+            finally:
+                dec.dispose()
+    finally:
+        dw.dispose()
+    (t1, l1, c1), (t2, l2, c2) = out
+    assert t1 == t2
+    assert np.isfinite(l2).all()
+    assert np.array_equal(l1.view(np.uint32), l2.view(np.uint32))
+    for a, b in zip(c1, c2):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))

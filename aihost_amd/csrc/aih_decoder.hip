@@ -682,10 +682,28 @@ constexpr int kRK = 132;      // strides in floats: 16-byte rows, 4 banks apart
 constexpr int kRV = 68;
 constexpr int kRP = 68;
 
+// Causal balance: query tiles are dispatched longest first, and a tile whose
+// keys span at least kSplitKT key tiles is done by two workgroups, dispatched
+// one after the other, over its first n_kt / 2 and its last n_kt - n_kt / 2
+// key tiles.  Part 0
+// leaves its unnormalised output in O and part 1 in part_o, with each row's
+// running max and sum in part_ml; attn_prefill_merge combines them.  Every
+// row of such a tile attends to the first key of part 1's range (its
+// positions are at least p_last - 63 >= 64 (n_kt / 2) when n_kt >= 3, since
+// p_last >= 64 (n_kt - 1)), so both parts' softmax states start finite.
+constexpr int kSplitKT = 3;
+
+__device__ __forceinline__ int64_t prefill_key_tiles(int64_t i0, int64_t n_q, int32_t p0, int32_t max_len)
+{
+    const int64_t p_last = min<int64_t>(p0 + min<int64_t>(i0 + kQTile, n_q) - 1, (int64_t)max_len - 1);
+    return p_last < 0 ? 0 : p_last / kKT + 1;
+}
+
 __global__ void __launch_bounds__(256)
 attn_prefill_kernel(const float *__restrict__ Q, int64_t ldq, const float *__restrict__ Kc,
                     const float *__restrict__ Vc, float *__restrict__ O, int64_t n_q, int32_t n_heads,
-                    int32_t n_kv_heads, int32_t start, const int32_t *pos, int32_t max_len, float scale)
+                    int32_t n_kv_heads, int32_t start, const int32_t *pos, int32_t max_len, float scale,
+                    float *__restrict__ part_o, float *__restrict__ part_ml)
 {
     __shared__ __align__(16) float ks[kKT * kRK];
     __shared__ __align__(16) float vt[kHD * kRV];
@@ -695,9 +713,18 @@ attn_prefill_kernel(const float *__restrict__ Q, int64_t ldq, const float *__res
     const int kvh = h / (n_heads / n_kv_heads);
     const int64_t kv_stride = (int64_t)n_kv_heads * kHD, q_stride = (int64_t)n_heads * kHD;
     const int32_t p0 = dev_pos(start, pos);
-    const int64_t i0 = (int64_t)blockIdx.y * kQTile;
+    // blockIdx.y = 2 * rank + part, tiles longest first (two parts per tile
+    // with part_o, else one)
+    const int parts = part_o ? 2 : 1;
+    const int part = (int)blockIdx.y % parts;
+    const int64_t i0 = (int64_t)(gridDim.y / parts - 1 - blockIdx.y / parts) * kQTile;
     // keys beyond the cache (a position past max_len) are never read
     const int64_t p_last = min<int64_t>(p0 + min<int64_t>(i0 + kQTile, n_q) - 1, (int64_t)max_len - 1);
+    const int64_t n_kt = prefill_key_tiles(i0, n_q, p0, max_len);
+    const bool split = part_o && n_kt >= kSplitKT;
+    if (part == 1 && !split) return;
+    const int64_t j_begin = split && part == 1 ? kKT * (n_kt / 2) : 0;
+    const int64_t j_end = split && part == 0 ? kKT * (n_kt / 2) : p_last + 1;
 
     // Q fragments: query 16w + c, dims 4s + g (rows past n_q read the last row, never stored)
     float qf[32];
@@ -736,9 +763,9 @@ attn_prefill_kernel(const float *__restrict__ Q, int64_t ldq, const float *__res
                                  : f4{0.f, 0.f, 0.f, 0.f};
         }
     };
-    gload(0);
+    gload(j_begin);
     float *pw = ps[w];
-    for (int64_t j0 = 0; j0 <= p_last; j0 += kKT) {
+    for (int64_t j0 = j_begin; j0 < j_end; j0 += kKT) {
         __syncthreads();   // the previous tile is consumed
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -827,11 +854,45 @@ attn_prefill_kernel(const float *__restrict__ Q, int64_t ldq, const float *__res
     for (int r = 0; r < 4; ++r) {
         const int64_t i = i0 + 16 * w + 4 * g + r;
         if (i < n_q) {
-            float *orow = O + i * q_stride + (int64_t)h * kHD + c;
+            if (split) {
+                float *orow = (part == 0 ? O + i * q_stride : part_o + i * q_stride) + (int64_t)h * kHD + c;
 #pragma unroll
-            for (int db = 0; db < 8; ++db) orow[16 * db] = o[db][r] / l[r];
+                for (int db = 0; db < 8; ++db) orow[16 * db] = o[db][r];
+                if (c == 0) {
+                    float *ml = part_ml + ((int64_t)part * n_heads * n_q + (int64_t)h * n_q + i) * 2;
+                    ml[0] = m[r];
+                    ml[1] = l[r];
+                }
+            } else {
+                float *orow = O + i * q_stride + (int64_t)h * kHD + c;
+#pragma unroll
+                for (int db = 0; db < 8; ++db) orow[16 * db] = o[db][r] / l[r];
+            }
         }
     }
+}
+
+// The two parts of each split tile: workgroup (h, tile, z) merges rows
+// 2z, 2z + 1 of query tile `tile` (attn_prefill_kernel's longest-first
+// order; workgroups of other tiles exit), one element per thread:
+//   O = (e^(m0 - M) o0 + e^(m1 - M) o1) / (e^(m0 - M) l0 + e^(m1 - M) l1),  M = max(m0, m1).
+__global__ void __launch_bounds__(256)
+attn_prefill_merge(float *__restrict__ O, const float *__restrict__ part_o, const float *__restrict__ part_ml,
+                   int64_t n_q, int32_t n_heads, int32_t start, const int32_t *pos, int32_t max_len)
+{
+    const int h = blockIdx.x;
+    const int64_t i0 = (int64_t)(gridDim.y - 1 - blockIdx.y) * kQTile;
+    if (prefill_key_tiles(i0, n_q, dev_pos(start, pos), max_len) < kSplitKT) return;
+    const int64_t i = i0 + 2 * blockIdx.z + (threadIdx.x >> 7);
+    if (i >= n_q) return;
+    const int64_t q_stride = (int64_t)n_heads * kHD;
+    const int64_t e = i * q_stride + (int64_t)h * kHD + (threadIdx.x & (kHD - 1));
+    const float *ml0 = part_ml + ((int64_t)h * n_q + i) * 2;
+    const float *ml1 = part_ml + ((int64_t)n_heads * n_q + (int64_t)h * n_q + i) * 2;
+    const float m0 = ml0[0], l0 = ml0[1], m1 = ml1[0], l1 = ml1[1];
+    const float o0 = O[e], o1 = part_o[e];
+    const float mm = fmaxf(m0, m1), a0 = expf(m0 - mm), a1 = expf(m1 - mm);
+    O[e] = (a0 * o0 + a1 * o1) / (a0 * l0 + a1 * l1);
 }
 
 // ---------------------------------------------------------------- argmax
@@ -1193,9 +1254,26 @@ int aih_attention_strided(aih_ctx *ctx, const float *Q, int64_t ldq, const float
         return aih_launch_status();
     }
     const int64_t tiles = (n_q + kQTile - 1) / kQTile;
-    if (tiles > 65535) return AIH_E_LIMIT;
-    hipLaunchKernelGGL(attn_prefill_kernel, dim3(n_heads, (unsigned)tiles), dim3(256), 0, ctx->stream, Q, ldq, Kc, Vc,
-                       O, n_q, n_heads, n_kv_heads, start, pos, max_len, scale);
+    if (2 * tiles > 65535) return AIH_E_LIMIT;
+    // split tiles need one more output image and two floats per row and part,
+    // from the context workspace; without it (a capture that would have to
+    // grow it) every tile runs whole
+    float *part_o = nullptr, *part_ml = nullptr;
+    {
+        void *work = nullptr;
+        const size_t need = (size_t)n_q * (size_t)n_heads * (kHD + 4) * sizeof(float);
+        if (aih_stage(ctx, nullptr, need, &work) == AIH_OK) {
+            part_o = static_cast<float *>(work);
+            part_ml = part_o + (size_t)n_q * n_heads * kHD;
+        }
+    }
+    hipLaunchKernelGGL(attn_prefill_kernel, dim3(n_heads, (unsigned)(tiles * (part_o ? 2 : 1))), dim3(256), 0,
+                       ctx->stream, Q, ldq, Kc, Vc, O, n_q, n_heads, n_kv_heads, start, pos, max_len, scale, part_o,
+                       part_ml);
+    int rc = aih_launch_status();
+    if (rc || !part_o) return rc;
+    hipLaunchKernelGGL(attn_prefill_merge, dim3(n_heads, (unsigned)tiles, kQTile / 2), dim3(256), 0, ctx->stream, O,
+                       part_o, part_ml, n_q, n_heads, start, pos, max_len);
     return aih_launch_status();
 }
 

@@ -347,7 +347,10 @@ int64_t aih_attention_scratch_floats(int32_t n_heads, int32_t max_len);
  * the query positions must already be in the cache.  head_dim must be 128.
  * One query row uses a split-over-keys kernel and a combine kernel, with
  * `scratch` (aih_attention_scratch_floats floats); more rows use a tiled
- * kernel with an online softmax.  Calls sharing a scratch must not overlap.  Replaces ComputeOps.MultiHeadAttention and FusedMHAGenerate
+ * kernel with an online softmax, whose query tiles with long key ranges run
+ * as two halves merged afterwards, staged in the context workspace
+ * (n_q * n_heads * (head_dim + 4) floats; grown on demand, and where it
+ * cannot grow -- inside a capture -- the tiles run whole).  Calls sharing a scratch must not overlap.  Replaces ComputeOps.MultiHeadAttention and FusedMHAGenerate
  * (ComputeOps.cs:1015-1102, shaders ComputeShaders.cs:656-733), without the
  * latter's 4096-key limit. */
 int aih_attention(aih_ctx *ctx, const float *Q, const float *Kc, const float *Vc, float *O, int64_t n_q,

@@ -10,10 +10,14 @@
 // cores (v_mfma_f32_32x32x16_f16, fp32 accumulation).
 //
 // Tiling.  X is first converted to fp16 in the context's workspace, stored in
-// MFMA fragment order.  A workgroup then owns a 128 (M) x 64 (N) tile of Y and
-// walks K in super-steps of 256 elements: four producer waves dequantize W for
-// the next super-step into LDS while four consumer waves multiply the current
-// one, their A fragments loaded straight from the tiled X (see qgemm_kernel).
+// MFMA fragment order (x_tile_kernel here, or the element-wise step before the
+// GEMM writing that order itself: aih_decoder.hip's x_tile_pre_kernel).  A
+// workgroup then owns a 128 (M) x 64 (N) tile of Y and walks K in super-steps
+// of 256 elements: four producer waves dequantize W for the next super-step
+// into LDS while four consumer waves multiply the current one, their A
+// fragments loaded straight from the tiled X (see qgemm_kernel).  Large grids
+// use 256 x 64 tiles with every wave in both roles (qgemm256_kernel).  The
+// epilogue stores Y or adds into it (the residual add of a layer).
 //
 // Precision.  Both operands are rounded to fp16 (11-bit significand) and the
 // products accumulate in fp32: normwise error near 3e-4 against the fp32

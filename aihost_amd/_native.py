@@ -24,8 +24,8 @@ HIP_ERROR_OUT_OF_MEMORY = 2
 
 F32, Q4_0, Q8_0, Q4_K, Q6_K = 0, 2, 8, 12, 14
 F16_IEEE, F16_REFCPU = 0, 1
-PRE_NONE, PRE_RMSNORM, PRE_SILU_MUL, PRE_SILU_PAIRS = 0, 1, 2, 3
-POST_STORE, POST_ACCUMULATE, POST_SILU_PAIRS = 0, 1, 2
+PRE_NONE, PRE_RMSNORM, PRE_SILU_MUL, PRE_SILU_PAIRS, PRE_F16_OPERAND = 0, 1, 2, 3, 4
+POST_STORE, POST_ACCUMULATE, POST_SILU_PAIRS, POST_SILU_PAIRS_F16 = 0, 1, 2, 3
 
 
 class DeviceInfo(ctypes.Structure):

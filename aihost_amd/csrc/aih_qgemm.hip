@@ -76,6 +76,60 @@ x_tile_kernel(const float *__restrict__ X, int64_t M, int64_t K, _Float16 *__res
     }
 }
 
+// Epilogues: 0 store Y, 1 add into Y, 2 the SiLU-pairs operand (below).
+constexpr int kEpiStore = 0, kEpiAccumulate = 1, kEpiSiluOperand = 2;
+
+// SiLU(gate) * up of a wave's 32 x 64 output block whose column pairs
+// (2j, 2j+1) are gate and up rows (W interleaved), written as the fp16 operand
+// of a following GEMM with K = N / 2 in the order x_tile_kernel produces: the
+// 32 x 32 results pass through `lds` (32 rows x 40 halves, private to the
+// wave) so that every lane writes whole 16-byte fragment slots.  Rows at or
+// past M are zero; m0w is the wave's first row, n0 the block's first column.
+// The arithmetic is silu_mul_pairs_kernel's, (g * (1 / (1 + e^-g))) * u in
+// fp32, then rounded to fp16 as the GEMM's conversion rounds that kernel's
+// stored output, so the operand is the same bits.
+__device__ __forceinline__ void silu_pairs_operand(const f16v &acc0, const f16v &acc1, int lane, int64_t m0w,
+                                                   int64_t n0, int64_t M, int64_t N, _Float16 *lds,
+                                                   _Float16 *__restrict__ out)
+{
+    const int fr = lane & 31, hf = lane >> 5;
+    constexpr int LS = 40;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        // the up value of this lane's column pair, from the odd neighbour
+        const float u0 = __builtin_amdgcn_update_dpp(0.0f, acc0[r], 0xB1, 0xF, 0xF, false);
+        const float u1 = __builtin_amdgcn_update_dpp(0.0f, acc1[r], 0xB1, 0xF, 0xF, false);
+        if ((fr & 1) == 0) {
+            const int i = 8 * (r >> 2) + 4 * hf + (r & 3);
+            const float g0 = acc0[r], g1 = acc1[r];
+            float y0 = (g0 * (1.0f / (1.0f + expf(-g0)))) * u0;
+            float y1 = (g1 * (1.0f / (1.0f + expf(-g1)))) * u1;
+            // round to fp32 first, as the separate operator's stored result is:
+            // the empty asm keeps the compiler from folding the last multiply
+            // and the conversion into one mixed-precision instruction (a single
+            // rounding straight to fp16)
+            asm("" : "+v"(y0), "+v"(y1));
+            lds[i * LS + (fr >> 1)] = (_Float16)y0;
+            lds[i * LS + 16 + (fr >> 1)] = (_Float16)y1;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // lane: row fr of the block, outputs 16 hf .. 16 hf + 15 (two slots)
+    const int64_t m = m0w + fr;
+    const int64_t mpad = (M + 31) / 32 * 32;
+    if (m >= mpad) return;
+    const int64_t kd = N / 2, kc = kd / 16;
+    const int64_t k0 = n0 / 2 + 16 * hf;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        h8 v = m < M ? *reinterpret_cast<const h8 *>(&lds[fr * LS + 16 * hf + 8 * q]) : h8{};
+        const int64_t k = k0 + 8 * q;
+        *reinterpret_cast<h8 *>(out + (((m >> 5) * kc + (k >> 4)) * 64 + (m & 31) + 32 * ((k >> 3) & 1)) * 8) = v;
+    }
+}
+
 // Eight waves per workgroup in two roles, one of each on every SIMD; the
 // workgroup owns a 128 (M) x 64 (N) tile of Y and walks K in super-steps of
 // 256 (a Q4_K/Q6_K super-block, 8 blocks of Q8_0/Q4_0), with one LDS barrier
@@ -102,7 +156,7 @@ template <> struct GRing<G6K> { static constexpr int PR = 2; };
 template <class T>
 __global__ void __launch_bounds__(512)
 qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
-             const _Float16 *__restrict__ Xt, int64_t M, float *__restrict__ Y, int accumulate)
+             const _Float16 *__restrict__ Xt, int64_t M, float *__restrict__ Y, int epi)
 {
     constexpr int PR = GRing<T>::PR;
     __shared__ __align__(16) _Float16 wsh[2][BN][LD2];
@@ -234,14 +288,20 @@ qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
         }
     }
 
+    if (epi == kEpiSiluOperand) {
+        // the tile buffer of super-step nss: nothing reads or writes it any more
+        silu_pairs_operand(acc0, acc1, lane, m0 + 32 * wave, n0, M, N, &wsh[nss & 1][0][0] + wave * 32 * 40,
+                           reinterpret_cast<_Float16 *>(Y));
+        return;
+    }
     const int64_t na = n0 + fr, nb = n0 + 32 + fr;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int i = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         const int64_t m = m0 + 32 * wave + i;
         if (m < M) {
-            if (na < N) Y[m * N + na] = accumulate ? Y[m * N + na] + acc0[r] : acc0[r];
-            if (nb < N) Y[m * N + nb] = accumulate ? Y[m * N + nb] + acc1[r] : acc1[r];
+            if (na < N) Y[m * N + na] = epi == kEpiAccumulate ? Y[m * N + na] + acc0[r] : acc0[r];
+            if (nb < N) Y[m * N + nb] = epi == kEpiAccumulate ? Y[m * N + nb] + acc1[r] : acc1[r];
         }
     }
 }
@@ -265,7 +325,7 @@ constexpr int PR256 = 2;
 template <class T>
 __global__ void __launch_bounds__(512)
 qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
-                const _Float16 *__restrict__ Xt, int64_t M, float *__restrict__ Y, int accumulate)
+                const _Float16 *__restrict__ Xt, int64_t M, float *__restrict__ Y, int epi)
 {
     constexpr int PR = PR256;
     typedef typename Piece32<T>::type P;
@@ -380,21 +440,27 @@ qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
         if (it < nss) body(std::true_type{}, it, ring[(j + 1) % PR], it + 1 < nss, it + 1 + PR < nss);
     }
 
+    if (epi == kEpiSiluOperand) {
+        // after the last barrier the tile buffers are free
+        silu_pairs_operand(acc0, acc1, lane, m0 + 32 * wave, n0, M, N, &wsh[0][0][0] + wave * 32 * 40,
+                           reinterpret_cast<_Float16 *>(Y));
+        return;
+    }
     const int64_t na = n0 + fr, nb = n0 + 32 + fr;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int i = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         const int64_t m = m0 + 32 * wave + i;
         if (m < M) {
-            if (na < N) Y[m * N + na] = accumulate ? Y[m * N + na] + acc0[r] : acc0[r];
-            if (nb < N) Y[m * N + nb] = accumulate ? Y[m * N + nb] + acc1[r] : acc1[r];
+            if (na < N) Y[m * N + na] = epi == kEpiAccumulate ? Y[m * N + na] + acc0[r] : acc0[r];
+            if (nb < N) Y[m * N + nb] = epi == kEpiAccumulate ? Y[m * N + nb] + acc1[r] : acc1[r];
         }
     }
 }
 
 template <class T>
 int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
-           const _Float16 *Xh, int64_t M, float *Y, int accumulate)
+           const _Float16 *Xh, int64_t M, float *Y, int epi)
 {
     const int64_t gx = (N + BN - 1) / BN, gy = (M + BM - 1) / BM, gy2 = (M + BM2 - 1) / BM2;
     if (gy > 65535 || gx > 0x7FFFFFFF) return AIH_E_LIMIT;
@@ -406,27 +472,27 @@ int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t row_byt
     const int64_t rounds = (gx * gy + cus - 1) / cus, rounds2 = (gx * gy2 + cus - 1) / cus;
     if (5 * rounds2 < 4 * rounds)
         hipLaunchKernelGGL((qgemm256_kernel<T>), dim3((unsigned)gx, (unsigned)gy2), dim3(512), 0, ctx->stream,
-                           W, N, K, row_bytes, Xh, M, Y, accumulate);
+                           W, N, K, row_bytes, Xh, M, Y, epi);
     else
         hipLaunchKernelGGL((qgemm_kernel<T>), dim3((unsigned)gx, (unsigned)gy), dim3(512), 0, ctx->stream,
-                           W, N, K, row_bytes, Xh, M, Y, accumulate);
+                           W, N, K, row_bytes, Xh, M, Y, epi);
     return aih_launch_status();
 }
 
 }  // namespace
 
 int aih_launch_qgemm_tiled(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const void *Xtv,
-                           int64_t M, float *Y, int accumulate)
+                           int64_t M, float *Y, int epi)
 {
     if (K % BK != 0) return AIH_E_LIMIT;
     const int64_t rb = aih_row_bytes(type, K);
     const uint8_t *w = static_cast<const uint8_t *>(W);
     const _Float16 *Xt = static_cast<const _Float16 *>(Xtv);
     switch (type) {
-    case AIH_TYPE_Q4_K: return launch<G4K>(ctx, w, N, K, rb, Xt, M, Y, accumulate);
-    case AIH_TYPE_Q6_K: return launch<G6K>(ctx, w, N, K, rb, Xt, M, Y, accumulate);
-    case AIH_TYPE_Q8_0: return launch<G80>(ctx, w, N, K, rb, Xt, M, Y, accumulate);
-    case AIH_TYPE_Q4_0: return launch<G40>(ctx, w, N, K, rb, Xt, M, Y, accumulate);
+    case AIH_TYPE_Q4_K: return launch<G4K>(ctx, w, N, K, rb, Xt, M, Y, epi);
+    case AIH_TYPE_Q6_K: return launch<G6K>(ctx, w, N, K, rb, Xt, M, Y, epi);
+    case AIH_TYPE_Q8_0: return launch<G80>(ctx, w, N, K, rb, Xt, M, Y, epi);
+    case AIH_TYPE_Q4_0: return launch<G40>(ctx, w, N, K, rb, Xt, M, Y, epi);
     default: return AIH_E_UNSUPPORTED;
     }
 }

@@ -532,17 +532,22 @@ int aih_qgemm_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
     if (!aih_is_quant(type)) return AIH_E_UNSUPPORTED;
     aih_block_geom g = aih_geom(type);
     if (N < 0 || M < 0 || K <= 0 || K % g.elems) return AIH_E_INVALID;
-    if (pre < AIH_PRE_NONE || pre > AIH_PRE_SILU_PAIRS) return AIH_E_INVALID;
-    if (post != AIH_POST_STORE && post != AIH_POST_ACCUMULATE) return AIH_E_INVALID;
+    if (pre < AIH_PRE_NONE || pre > AIH_PRE_F16_OPERAND) return AIH_E_INVALID;
+    if (post != AIH_POST_STORE && post != AIH_POST_ACCUMULATE && post != AIH_POST_SILU_PAIRS_F16)
+        return AIH_E_INVALID;
+    if (post == AIH_POST_SILU_PAIRS_F16 && N % 128) return AIH_E_INVALID;
     const bool uses_x2 = pre == AIH_PRE_RMSNORM || pre == AIH_PRE_SILU_MUL;
     if (uses_x2 && !X2) return AIH_E_INVALID;
     if (!N || !M) return AIH_OK;
     if (!W || !X || !Y) return AIH_E_INVALID;
     if (K % 64 != 0) return AIH_E_LIMIT;
-    if (reinterpret_cast<uintptr_t>(X) % 16 || (uses_x2 && reinterpret_cast<uintptr_t>(X2) % 16))
+    if (reinterpret_cast<uintptr_t>(X) % 16 || (uses_x2 && reinterpret_cast<uintptr_t>(X2) % 16) ||
+        (post == AIH_POST_SILU_PAIRS_F16 && reinterpret_cast<uintptr_t>(Y) % 16))
         return AIH_E_INVALID;
     int rc = select_device(ctx);
     if (rc) return rc;
+    const int epi = post == AIH_POST_ACCUMULATE ? 1 : post == AIH_POST_SILU_PAIRS_F16 ? 2 : 0;
+    if (pre == AIH_PRE_F16_OPERAND) return aih_launch_qgemm_tiled(ctx, type, W, N, K, X, M, Y, epi);
     const int64_t mpad = (M + 31) / 32 * 32;
     void *work = nullptr;
     rc = aih_stage(ctx, nullptr, (size_t)mpad * (size_t)K * 2, &work);
@@ -550,7 +555,7 @@ int aih_qgemm_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
     rc = pre == AIH_PRE_NONE ? aih_launch_x_tile(ctx, X, M, K, work)
                              : aih_launch_x_tile_pre(ctx, pre, X, X2, eps, M, K, work);
     if (rc) return rc;
-    return aih_launch_qgemm_tiled(ctx, type, W, N, K, work, M, Y, post == AIH_POST_ACCUMULATE);
+    return aih_launch_qgemm_tiled(ctx, type, W, N, K, work, M, Y, epi);
 }
 
 int aih_matmul_weights_q_noalloc(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,

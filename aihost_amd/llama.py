@@ -294,7 +294,8 @@ class LlamaDecoder:
         Q|K|V GEMM with the attention RMSNorm computed into its operand, RoPE
         and the cache store, attention reading the query block in place, the
         W_o GEMM adding into x, the gate|up GEMM with the FFN RMSNorm in its
-        operand, the down GEMM with SiLU(gate)*up in its operand adding into x.
+        operand and SiLU(gate)*up written as the down GEMM's fp16 operand, the
+        down GEMM adding into x.
         Bit for bit the result of the separate operators (layer())."""
         c, L, h, p = self.cfg, self.L, self.h, "blk.%d." % l
         qd = c.n_heads * c.head_dim
@@ -310,7 +311,11 @@ class LlamaDecoder:
                                           self.scratch, self.scratch_floats), "attention")
         self._mmx(p + "attn_output", self.att, None, nat.PRE_NONE, nat.POST_ACCUMULATE, rows, self.x)
         norm = self.w.ptr(p + "ffn_norm")
-        if p + "ffn_gate_up" in self.w:
+        if p + "ffn_gate_up" in self.w and (2 * c.ffn) % 128 == 0:
+            # SiLU(gate)*up leaves the gate|up GEMM as the down GEMM's fp16 operand
+            self._mmx(p + "ffn_gate_up", self.x, norm, nat.PRE_RMSNORM, nat.POST_SILU_PAIRS_F16, rows, self.gate)
+            self._mmx(p + "ffn_down", self.gate, None, nat.PRE_F16_OPERAND, nat.POST_ACCUMULATE, rows, self.x)
+        elif p + "ffn_gate_up" in self.w:
             self._mmx(p + "ffn_gate_up", self.x, norm, nat.PRE_RMSNORM, nat.POST_STORE, rows, self.gate)
             self._mmx(p + "ffn_down", self.gate, None, nat.PRE_SILU_PAIRS, nat.POST_ACCUMULATE, rows, self.x)
         else:

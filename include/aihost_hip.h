@@ -221,6 +221,15 @@ int aih_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
 /* aih_qgemm_fused only:  x[k] = SiLU(X[2k]) * X[2k+1]  (X rows of 2K floats:
  * the output of a GEMM over gate/up rows interleaved; X2 unused). */
 #define AIH_PRE_SILU_PAIRS  3
+/* aih_qgemm_fused only: X is the GEMM's fp16 operand image of M rows, as
+ * AIH_POST_SILU_PAIRS_F16 writes it (X2 unused). */
+#define AIH_PRE_F16_OPERAND 4
+/* aih_qgemm_fused only: SiLU(y[m, 2i]) * y[m, 2i+1] (W holds gate and up rows
+ * interleaved, N a multiple of 128), rounded to fp16 and stored in Y as the
+ * fp16 operand image of a GEMM over those N/2 columns (mpad * N bytes, mpad =
+ * M rounded up to 32), for a following aih_qgemm_fused with
+ * pre = AIH_PRE_F16_OPERAND and K = N/2. */
+#define AIH_POST_SILU_PAIRS_F16 3
 int aih_qmatvec_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *X,
                       const float *X2, float eps, int pre, int post, float *Y);
 
@@ -247,12 +256,19 @@ int aih_matmul_weights_q(aih_ctx *ctx, int type, const void *W, int64_t N, int64
  *   pre = AIH_PRE_SILU_MUL    x = SiLU(X) * X2                               (X2: M x K)
  *   pre = AIH_PRE_SILU_PAIRS  x[m, k] = SiLU(X[m, 2k]) * X[m, 2k+1]           (X: M x 2K)
  * and
- *   post = AIH_POST_STORE       Y[m, n] = y[m, n]
- *   post = AIH_POST_ACCUMULATE  Y[m, n] += y[m, n]      (the residual add)
+ *   pre = AIH_PRE_F16_OPERAND x: the fp16 operand image X (see below)
+ * and
+ *   post = AIH_POST_STORE           Y[m, n] = y[m, n]
+ *   post = AIH_POST_ACCUMULATE      Y[m, n] += y[m, n]      (the residual add)
+ *   post = AIH_POST_SILU_PAIRS_F16  Y = the fp16 operand image of
+ *                                   SiLU(y[m, 2i]) * y[m, 2i+1]
  * The element-wise step writes the GEMM's fp16 operand directly (no fp32
  * intermediate, no separate conversion) with the formulas of aih_rmsnorm,
  * aih_silu_mul, aih_silu_mul_pairs and aih_add, so the result is bit for bit
- * that of the separate operator, then aih_qgemm (and aih_add).  Workspace,
+ * that of the separate operator, then aih_qgemm (and aih_add); likewise the
+ * gate|up GEMM with AIH_POST_SILU_PAIRS_F16 followed by the down GEMM with
+ * AIH_PRE_F16_OPERAND gives the bits of the gate|up GEMM, aih_silu_mul_pairs
+ * and the down GEMM.  Workspace,
  * K and alignment rules as aih_qgemm; X, X2 16-byte aligned; Y must not
  * alias X or X2.  Replaces, for a prompt, the LayerNorm / SiLU+Multiply /
  * Add around MatMulWeights in ComputeOps.TransformerLayer

@@ -110,6 +110,42 @@ def test_qgemm_fused_equals_separate_operators(device, qtype, n, k, m):
         wb.dispose()
 
 
+# gate|up W of 2F rows (K = d), down W of d rows (K = F); (1024, 3072, 300)
+# takes the 256-row tiles for gate|up on a 256-CU device, (512, 128, 40) the
+# 128-row tiles
+@pytest.mark.parametrize("d,f,m,qt_down", [(512, 128, 40, nat.Q8_0), (1024, 3072, 300, nat.Q4_K)])
+def test_silu_pairs_operand_chain_equals_separate_operators(device, d, f, m, qt_down):
+    L, h = nat.lib(), device.handle
+    rng = np.random.default_rng(d + f + m)
+    w_gu = synth_weight(nat.Q4_K, 2 * f, d, seed=d)
+    w_dn = synth_weight(qt_down, d, f, seed=f)
+    x = rng.standard_normal((m, d)).astype(np.float32)
+    nw = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    y0 = rng.standard_normal((m, d)).astype(np.float32)
+    bufs = [upload(device, a) for a in (w_gu, w_dn, x, nw)]
+    wgu, wdn, xb, nb = bufs
+    xn, g, u, t = (device.create_buffer(n) for n in (m * d * 4, m * 2 * f * 4, m * f * 4, m * d * 4))
+    ya, yb = upload(device, y0), upload(device, y0)
+    try:
+        _check(L.aih_rmsnorm(h, xb.get_pointer(), nb.get_pointer(), xn.get_pointer(), m, d, EPS), "rmsnorm")
+        _check(L.aih_qgemm(h, nat.Q4_K, wgu.get_pointer(), 2 * f, d, xn.get_pointer(), m, g.get_pointer()), "gu")
+        _check(L.aih_silu_mul_pairs(h, g.get_pointer(), u.get_pointer(), m, f), "silu pairs")
+        _check(L.aih_qgemm(h, qt_down, wdn.get_pointer(), d, f, u.get_pointer(), m, t.get_pointer()), "down")
+        _check(L.aih_add(h, ya.get_pointer(), t.get_pointer(), ya.get_pointer(), m * d), "add")
+        # g (m x 2f floats) holds the operand image (mpad x 2f bytes)
+        _check(L.aih_qgemm_fused(h, nat.Q4_K, wgu.get_pointer(), 2 * f, d, xb.get_pointer(), nb.get_pointer(), EPS,
+                                 m, nat.PRE_RMSNORM, nat.POST_SILU_PAIRS_F16, g.get_pointer()), "gu fused")
+        _check(L.aih_qgemm_fused(h, qt_down, wdn.get_pointer(), d, f, g.get_pointer(), None, EPS, m,
+                                 nat.PRE_F16_OPERAND, nat.POST_ACCUMULATE, yb.get_pointer()), "down fused")
+        ref, got = _read(ya, m * d), _read(yb, m * d)
+        assert np.isfinite(ref).all()
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), "%d of %d differ" % (
+            int(np.sum(got != ref)), got.size)
+    finally:
+        for b in bufs + [xn, g, u, t, ya, yb]:
+            b.dispose()
+
+
 def test_qgemm_fused_argument_errors(device):
     L, h = nat.lib(), device.handle
     n, k, m = 64, 256, 16
@@ -120,7 +156,6 @@ def test_qgemm_fused_argument_errors(device):
         w, x, y = wb.get_pointer(), xb.get_pointer(), yb.get_pointer()
         assert L.aih_qgemm_fused(h, nat.Q4_K, w, n, k, x, None, EPS, m, nat.PRE_RMSNORM, 0, y) == nat.AIH_E_INVALID
         assert L.aih_qgemm_fused(h, nat.Q4_K, w, n, k, x, None, EPS, m, nat.PRE_SILU_MUL, 0, y) == nat.AIH_E_INVALID
-        assert L.aih_qgemm_fused(h, nat.Q4_K, w, n, k, x, None, EPS, m, 4, 0, y) == nat.AIH_E_INVALID
         assert L.aih_qgemm_fused(h, nat.Q4_K, w, n, k, x, None, EPS, m, 0, nat.POST_SILU_PAIRS, y) == \
             nat.AIH_E_INVALID
         assert L.aih_qgemm_fused(h, nat.Q4_K, w, n, k, x + 4, None, EPS, m, 0, 0, y) == nat.AIH_E_INVALID
@@ -128,6 +163,11 @@ def test_qgemm_fused_argument_errors(device):
         # K a whole number of Q8_0 blocks but not of 64-element GEMM steps
         assert L.aih_qgemm_fused(h, nat.Q8_0, w, n, 96, x, None, EPS, m, 0, 0, y) == nat.AIH_E_LIMIT
         assert L.aih_qgemm_fused(h, nat.Q4_K, w, n, k, x, None, EPS, 0, nat.PRE_SILU_PAIRS, 0, y) == nat.AIH_OK
+        assert L.aih_qgemm_fused(h, nat.Q4_K, w, n, k, x, None, EPS, m, 5, 0, y) == nat.AIH_E_INVALID
+        assert L.aih_qgemm_fused(h, nat.Q4_K, w, n, k, x, None, EPS, m, 0, 4, y) == nat.AIH_E_INVALID
+        # the SiLU-pairs operand needs N a multiple of 128
+        assert L.aih_qgemm_fused(h, nat.Q4_K, w, n, k, x, None, EPS, m, 0, nat.POST_SILU_PAIRS_F16, y) == \
+            nat.AIH_E_INVALID
     finally:
         for b in (wb, xb, yb):
             b.dispose()

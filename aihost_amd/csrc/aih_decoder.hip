@@ -657,38 +657,59 @@ attn_decode_combine(const float *__restrict__ part, float *__restrict__ O, int32
     O[(int64_t)h * kHD + t] = lsum > 0.f ? a / lsum : 0.f;
 }
 
-// Prefill on the matrix cores: v_mfma_f32_16x16x4_f32 takes fp32 operands
-// and accumulates in fp32, as the reference's scalar loops do (only the
-// order of the additions differs).  Workgroup (h, tile) of 256 threads owns
-// kQTile = 64 query rows; wave w the 16 rows 16w .. 16w+15.  Per tile of 64
-// keys, staged in LDS: S = Q K^T (16 x 64 per wave), an online softmax per
-// query row, O += P V (16 x 128 per wave).
+// Prefill on the fp16 matrix cores with split operands.  Every fp32
+// operand x becomes x 2^e = hi + lo, two fp16 values, with a power of two
+// 2^e that puts the largest |x| of its group in [2^14, 2^15): hi = fp16(x 2^e)
+// and lo = fp16(x 2^e - hi), 22 significant bits, and an absolute error of at
+// most 2^-25 in the scaled units, so small members of a group lose nothing
+// that matters beside its largest.  v_mfma_f32_16x16x32_f16 forms
+// hi.hi + hi.lo + lo.hi (each product exact in fp32, sums in fp32); the
+// dropped lo.lo term is below 2^-22 of a product.  Three fp16 MFMAs cost a
+// sixth of the cycles of the fp32 MFMAs for the same products.
 //
-// MFMA 16x16x4 layouts (lane l, g = l/16, c = l%16): A[i][k] is lane
-// i + 16k, B[k][j] lane j + 16k, D[i][j] lane j + 16(i/4), register i%4.
-//   S: A = Q (lane holds query c, dims 4s + g for the 32 k-steps s),
-//      B = K^T (key c of a 16-key block, dim 4s + g): D row 4g + r = query,
-//      column c = key.
-//   O: A = P (query c, key 4s + g), B = V (key 4s + g, dim c of a 16-dim
-//      block): D row 4g + r = query, column c = dim.
-// So every lane keeps the running max and sum of its four D rows 4g + r,
-// and P goes through LDS to change from the D to the A layout.  The LDS
-// images are permuted so that one 16-byte read gives a lane four k-steps:
-//   K tile: key j, dim d at [j][(d%4) * 32 + d/4]        (row stride kRK)
-//   V tile: dim d, key j at [d][(j%4) * 16 + j/4]        (row stride kRV)
-//   P:      query q, key j at [q][(j%4) * 16 + j/4]      (row stride kRP)
+// Groups: a query row (Q), and per KV head the K and the V rows of a 64-key
+// tile (one power of two each).  Scores are unscaled exactly (the power of
+// two joins the reference's scale), and the softmax runs in base 2:
+// t = score log2(e), p = 2^(t - max).  The V tile's factor goes into P:
+// P'' = P 2^(A - ev) with A = 15 + the smallest ev seen so far, so
+// P'' <= 2^15 and the O accumulators hold 2^A O; when A drops, they are
+// rescaled by the exact power of two with the softmax correction.
+//
+// Workgroup (h, tile) of 256 threads owns kQTile = 64 queries; wave w the
+// 16 queries 16w .. 16w+15.  The products are transposed, S^T = K Q^T and
+// O^T = V^T P^T, so that the softmax output is already the B operand of the
+// second product and never leaves the registers.  16x16x32 layouts (lane l,
+// g = l/16, c = l%16): A[i][k] lane i + 16(k/8) element k%8, B[k][j] lane
+// j + 16(k/8) element k%8, D[i][j] lane j + 16(i/4) register i%4.
+//   S^T block kb (keys 16kb .. +15): A = K (key c, dims 32s + 8g .. +7),
+//      B = Q^T (query c, the same dims): lane (c, g) gets query c's scores
+//      for keys 16kb + 4g + r, r = 0..3.
+//   O^T block db (dims 16db .. +15), key step t (keys 32t .. +31): the 32
+//      k-slots are ordered so that slot 8g + e holds key
+//      32t + 16(e/4) + 4g + e%4, i.e. P of block kb = 2t + e/4, register
+//      e%4 of the lane itself.  A = V^T in the same slot order.
+// Every lane keeps the running max of its query (reduced over the four
+// lanes that hold it), a partial sum over its own keys and the rows
+// 16db + 4g + r of O^T.
+//
+// LDS holds the split tile as four images: K hi, K lo (row = key, 128 dims)
+// and V^T hi, V^T lo (row = dim, 64 slots).  Rows are padded by 16 bytes,
+// so that the 16 lanes of a quarter wave read 16 different rows on disjoint
+// banks.
 constexpr int kKT = 64;       // keys per tile
-constexpr int kRK = 132;      // strides in floats: 16-byte rows, 4 banks apart
-constexpr int kRV = 68;
-constexpr int kRP = 68;
+constexpr int kRKH = 136;     // K image row (key) stride in LDS, halves: 128 dims + 16 bytes
+constexpr int kRVH = 72;      // V^T image row (dim) stride in LDS, halves: 64 slots + 16 bytes
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 hl2 __attribute__((ext_vector_type(2)));   // {hi, lo}
 
 // Causal balance: query tiles are dispatched longest first, and a tile whose
 // keys span at least kSplitKT key tiles is done by two workgroups, dispatched
 // one after the other, over its first n_kt / 2 and its last n_kt - n_kt / 2
 // key tiles.  Part 0
 // leaves its unnormalised output in O and part 1 in part_o, with each row's
-// running max and sum in part_ml; attn_prefill_merge combines them.  Every
-// row of such a tile attends to the first key of part 1's range (its
+// running max (base 2) and sum in part_ml; attn_prefill_merge combines them.
+// Every row of such a tile attends to the first key of part 1's range (its
 // positions are at least p_last - 63 >= 64 (n_kt / 2) when n_kt >= 3, since
 // p_last >= 64 (n_kt - 1)), so both parts' softmax states start finite.
 constexpr int kSplitKT = 3;
@@ -699,15 +720,121 @@ __device__ __forceinline__ int64_t prefill_key_tiles(int64_t i0, int64_t n_q, in
     return p_last < 0 ? 0 : p_last / kKT + 1;
 }
 
-__global__ void __launch_bounds__(256)
+// The power of two 2^e that puts amax in [2^14, 2^15) (e = 15 for zero).
+__device__ __forceinline__ int split_exp(float amax)
+{
+    return 15 - __builtin_amdgcn_frexp_expf(amax);
+}
+
+__device__ __forceinline__ hl2 split_f16(float x, int e)
+{
+    const float xs = ldexpf(x, e);
+    const _Float16 hi = (_Float16)xs;
+    return hl2{hi, (_Float16)(xs - (float)hi)};
+}
+
+__device__ __forceinline__ float xor_lanes_max(float v)   // over lanes l, l^16, l^32, l^48
+{
+    v = fmaxf(v, __shfl_xor(v, 16));
+    return fmaxf(v, __shfl_xor(v, 32));
+}
+
+// One tile of one KV head in registers, as the 256 threads of a workgroup
+// load it: K thread (keys kt_key + 16i, dims 8 kt_ch .. +7), V thread (dims
+// 4 vt_dq .. +3 of the 8 keys of slots 32 vt_t + 8 vt_g .. +7); rows past
+// p_last are zeros.
+struct KVTile {
+    f4 kr[8], vr[8];
+
+    __device__ __forceinline__ void load(const float *__restrict__ Kc, const float *__restrict__ Vc,
+                                         int64_t kv_stride, int kvh, int64_t j0, int64_t p_last, int tid)
+    {
+        const int kt_key = tid >> 4, kt_ch = tid & 15;
+        const int vt_t = tid >> 7, vt_g = (tid >> 5) & 3, vt_dq = tid & 31;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t jk = j0 + kt_key + 16 * i;
+            const float *kp = Kc + jk * kv_stride + kvh * kHD + 8 * kt_ch;
+            kr[2 * i] = jk <= p_last ? *reinterpret_cast<const f4 *>(kp) : f4{0.f, 0.f, 0.f, 0.f};
+            kr[2 * i + 1] = jk <= p_last ? *reinterpret_cast<const f4 *>(kp + 4) : f4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int64_t jv = j0 + 32 * vt_t + 16 * (e / 4) + 4 * vt_g + e % 4;
+            vr[e] = jv <= p_last ? *reinterpret_cast<const f4 *>(Vc + jv * kv_stride + kvh * kHD + 4 * vt_dq)
+                                 : f4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+
+    // this wave's max |K| and |V|, into tmax[0][w] and tmax[1][w]
+    __device__ __forceinline__ void wave_max(float (*tmax)[4], int lane, int w) const
+    {
+        float mk = 0.f, mv = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                mk = fmaxf(mk, fabsf(kr[i][u]));
+                mv = fmaxf(mv, fabsf(vr[i][u]));
+            }
+        mk = xor_lanes_max(row16_max(mk));
+        mv = xor_lanes_max(row16_max(mv));
+        if (lane == 0) {
+            tmax[0][w] = mk;
+            tmax[1][w] = mv;
+        }
+    }
+
+    // this thread's 16 split chunks into the padded LDS images (K hi, K lo,
+    // V^T hi, V^T lo from lds)
+    __device__ __forceinline__ void split_to_lds(int ek, int ev, int tid, _Float16 *lds) const
+    {
+        const int kt_key = tid >> 4, kt_ch = tid & 15;
+        const int vt_t = tid >> 7, vt_g = (tid >> 5) & 3, vt_dq = tid & 31;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            h8 hi, lo;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const hl2 v = split_f16(kr[2 * i + e / 4][e % 4], ek);
+                hi[e] = v.x;
+                lo[e] = v.y;
+            }
+            _Float16 *at = lds + (kt_key + 16 * i) * kRKH + 8 * kt_ch;
+            *reinterpret_cast<h8 *>(at) = hi;
+            *reinterpret_cast<h8 *>(at + kKT * kRKH) = lo;
+        }
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            h8 hi, lo;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const hl2 v = split_f16(vr[e][d], ev);
+                hi[e] = v.x;
+                lo[e] = v.y;
+            }
+            _Float16 *at = lds + 2 * kKT * kRKH + (4 * vt_dq + d) * kRVH + 32 * vt_t + 8 * vt_g;
+            *reinterpret_cast<h8 *>(at) = hi;
+            *reinterpret_cast<h8 *>(at + kHD * kRVH) = lo;
+        }
+    }
+};
+
+__device__ __forceinline__ int split_exp_of(const float (*tmax)[4], int which)
+{
+    return split_exp(fmaxf(fmaxf(tmax[which][0], tmax[which][1]), fmaxf(tmax[which][2], tmax[which][3])));
+}
+
+
+__global__ void __launch_bounds__(256, 2)
 attn_prefill_kernel(const float *__restrict__ Q, int64_t ldq, const float *__restrict__ Kc,
                     const float *__restrict__ Vc, float *__restrict__ O, int64_t n_q, int32_t n_heads,
                     int32_t n_kv_heads, int32_t start, const int32_t *pos, int32_t max_len, float scale,
                     float *__restrict__ part_o, float *__restrict__ part_ml)
 {
-    __shared__ __align__(16) float ks[kKT * kRK];
-    __shared__ __align__(16) float vt[kHD * kRV];
-    __shared__ __align__(16) float ps[4][16 * kRP];
+    __shared__ __align__(16) _Float16 lds[2 * kKT * kRKH + 2 * kHD * kRVH];   // K hi, K lo, V^T hi, V^T lo
+    __shared__ float tmax[2][4];                                               // [K, V][wave]: the next tile
+    _Float16 *const ksh = lds, *const vsh = lds + 2 * kKT * kRKH;
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
     const int kvh = h / (n_heads / n_kv_heads);
@@ -726,156 +853,146 @@ attn_prefill_kernel(const float *__restrict__ Q, int64_t ldq, const float *__res
     const int64_t j_begin = split && part == 1 ? kKT * (n_kt / 2) : 0;
     const int64_t j_end = split && part == 0 ? kKT * (n_kt / 2) : p_last + 1;
 
-    // Q fragments: query 16w + c, dims 4s + g (rows past n_q read the last row, never stored)
-    float qf[32];
+    // Q^T operand: query 16w + c, dims 32s + 8g .. +7, split with the row's
+    // power of two (rows past n_q read the last row, never stored)
+    h8 qh[4], ql[4];
+    int eq;
     {
-        const float *qrow = Q + min<int64_t>(i0 + 16 * w + c, n_q - 1) * ldq + (int64_t)h * kHD;
+        const float *qrow = Q + min<int64_t>(i0 + 16 * w + c, n_q - 1) * ldq + (int64_t)h * kHD + 8 * g;
+        f4 qv[8];
+        float mx = 0.f;
 #pragma unroll
-        for (int s = 0; s < 32; ++s) qf[s] = qrow[4 * s + g];
+        for (int s = 0; s < 4; ++s) {
+            qv[2 * s] = *reinterpret_cast<const f4 *>(qrow + 32 * s);
+            qv[2 * s + 1] = *reinterpret_cast<const f4 *>(qrow + 32 * s + 4);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) mx = fmaxf(mx, fabsf(qv[i][u]));
+        eq = split_exp(xor_lanes_max(mx));
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const hl2 v = split_f16(qv[2 * s + e / 4][e % 4], eq);
+                qh[s][e] = v.x;
+                ql[s][e] = v.y;
+            }
     }
-    // the position of each of this lane's four D rows (last key it attends to)
-    int64_t qp[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) qp[r] = p0 + min<int64_t>(i0 + 16 * w + 4 * g + r, n_q - 1);
-    float m[4], l[4];
+    const int64_t qpos = p0 + min<int64_t>(i0 + 16 * w + c, n_q - 1);   // last key the query attends to
+    const float sl = scale * 1.44269504088896341f;                       // scale log2(e)
+    float m = -INFINITY, l = 0.f;
+    int A = 1 << 20;   // O accumulators hold 2^A O (lowered by the first tile)
     f4 o[8];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        m[r] = -INFINITY;
-        l[r] = 0.f;
-    }
 #pragma unroll
     for (int db = 0; db < 8; ++db) o[db] = f4{0.f, 0.f, 0.f, 0.f};
 
-    // staging: K thread (key kr_j + 8i, dims kr_d .. +3), V thread (key
-    // vr_j, dims vr_d + 4i .. +3), so that each layout's LDS writes are
-    // spread over the banks
-    const int kr_j = tid >> 5, kr_d = 4 * (tid & 31);
-    const int vr_j = tid & 63, vr_d = 32 * (tid >> 6);
-    f4 kr[8], vr[8];
-    auto gload = [&](int64_t j0) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int64_t jk = j0 + kr_j + 8 * i, jv = j0 + vr_j;
-            kr[i] = jk <= p_last ? *reinterpret_cast<const f4 *>(Kc + jk * kv_stride + kvh * kHD + kr_d)
-                                 : f4{0.f, 0.f, 0.f, 0.f};
-            vr[i] = jv <= p_last ? *reinterpret_cast<const f4 *>(Vc + jv * kv_stride + kvh * kHD + vr_d + 4 * i)
-                                 : f4{0.f, 0.f, 0.f, 0.f};
-        }
-    };
-    gload(j_begin);
-    float *pw = ps[w];
+    // the next tile's rows in registers
+    KVTile kv;
+    kv.load(Kc, Vc, kv_stride, kvh, j_begin, p_last, tid);
+    kv.wave_max(tmax, lane, w);
     for (int64_t j0 = j_begin; j0 < j_end; j0 += kKT) {
-        __syncthreads();   // the previous tile is consumed
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            float *kd = ks + (kr_j + 8 * i) * kRK + kr_d / 4;
-            kd[0] = kr[i].x;
-            kd[32] = kr[i].y;
-            kd[64] = kr[i].z;
-            kd[96] = kr[i].w;
-            float *vd = vt + (vr_d + 4 * i) * kRV + (vr_j % 4) * 16 + vr_j / 4;
-            vd[0] = vr[i].x;
-            vd[kRV] = vr[i].y;
-            vd[2 * kRV] = vr[i].z;
-            vd[3 * kRV] = vr[i].w;
-        }
+        __syncthreads();   // the previous tile is consumed; tmax holds this one's maxima
+        const int ek = split_exp_of(tmax, 0), ev = split_exp_of(tmax, 1);
+        kv.split_to_lds(ek, ev, tid, lds);
         __syncthreads();
-        gload(j0 + kKT);   // the next tile's rows in flight (zeros past p_last)
+        if (j0 + kKT < j_end) kv.load(Kc, Vc, kv_stride, kvh, j0 + kKT, p_last, tid);   // the next tile in flight
 
-        // S = Q K^T, four blocks of 16 keys
+        // S^T = K Q^T, four blocks of 16 keys
         f4 sc[4];
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
             f4 acc = {0.f, 0.f, 0.f, 0.f};
-            const float *kp = ks + (16 * kb + c) * kRK + 32 * g;
+            const int at = (16 * kb + c) * kRKH + 8 * g;
 #pragma unroll
-            for (int s4 = 0; s4 < 8; ++s4) {
-                const f4 kf = *reinterpret_cast<const f4 *>(kp + 4 * s4);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[4 * s4 + 0], kf.x, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[4 * s4 + 1], kf.y, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[4 * s4 + 2], kf.z, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[4 * s4 + 3], kf.w, acc, 0, 0, 0);
+            for (int s = 0; s < 4; ++s) {
+                const h8 kh = *reinterpret_cast<const h8 *>(&ksh[at + 32 * s]);
+                const h8 kl = *reinterpret_cast<const h8 *>(&ksh[kKT * kRKH + at + 32 * s]);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[s], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[s], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[s], acc, 0, 0, 0);
             }
             sc[kb] = acc;
         }
-        // scale, causal mask, online softmax of rows 4g + r (16 lanes each)
+        // t = score log2(e) (the powers of two undone exactly in the
+        // multiplier), causal mask, online softmax of query c in base 2
+        const float cs = ldexpf(sl, -(eq + ek));
+        float mx = -INFINITY;
+        const int lim = (int)min<int64_t>(qpos - j0, kKT);   // keys past j0 + lim are masked
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            float mx = -INFINITY;
+        for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
-                const float v = j0 + 16 * kb + c > qp[r] ? -INFINITY : sc[kb][r] * scale;
+            for (int r = 0; r < 4; ++r) {
+                const float v = 16 * kb + 4 * g + r > lim ? -INFINITY : sc[kb][r] * cs;
                 sc[kb][r] = v;
                 mx = fmaxf(mx, v);
             }
-            mx = row16_max(mx);
-            // key 0 lies in the first tile of every row: mn is finite from then on
-            const float mn = fmaxf(m[r], mx), corr = expf(m[r] - mn);
-            float sum = 0.f;
+        mx = xor_lanes_max(mx);
+        // part 0 starts at key 0 and part 1 at a key every row attends to: mn is finite
+        const float mn = fmaxf(m, mx), corr = __builtin_amdgcn_exp2f(m - mn);
+        const int An = min(A, ev + 15);
+        const float f = corr * ldexpf(1.f, max(An - A, -160));
+        m = mn;
+        A = An;
+        const int ep = An - ev;   // P'' = P 2^(A - ev) <= 2^15
+        h8 ph[2], pl[2];
+        float sum = 0.f;
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
-                const float pj = expf(sc[kb][r] - mn);
-                sc[kb][r] = pj;
-                sum += pj;
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float p = __builtin_amdgcn_exp2f(sc[kb][r] - mn);
+                sum += p;
+                const hl2 v = split_f16(p, ep);
+                ph[kb / 2][4 * (kb % 2) + r] = v.x;
+                pl[kb / 2][4 * (kb % 2) + r] = v.y;
             }
-            sum = row16_sum(sum);
-            l[r] = l[r] * corr + sum;
-            m[r] = mn;
+        l = l * corr + sum;
 #pragma unroll
-            for (int db = 0; db < 8; ++db) o[db][r] *= corr;
-        }
-        // P from the D layout (row 4g + r, key 16kb + c) to the A layout through LDS
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-            for (int kb = 0; kb < 4; ++kb) pw[(4 * g + r) * kRP + (c % 4) * 16 + 4 * kb + c / 4] = sc[kb][r];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        f4 pa[4];
-#pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) pa[s4] = *reinterpret_cast<const f4 *>(pw + c * kRP + 16 * g + 4 * s4);
-        // O += P V, eight blocks of 16 dims
+        for (int db = 0; db < 8; ++db) o[db] *= f;
+        // O^T += V^T P^T, eight blocks of 16 dims, two steps of 32 keys
 #pragma unroll
         for (int db = 0; db < 8; ++db) {
-            const float *vp = vt + (16 * db + c) * kRV + 16 * g;
+            const int at = (16 * db + c) * kRVH + 8 * g;
 #pragma unroll
-            for (int s4 = 0; s4 < 4; ++s4) {
-                const f4 vf = *reinterpret_cast<const f4 *>(vp + 4 * s4);
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[s4].x, vf.x, o[db], 0, 0, 0);
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[s4].y, vf.y, o[db], 0, 0, 0);
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[s4].z, vf.z, o[db], 0, 0, 0);
-                o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[s4].w, vf.w, o[db], 0, 0, 0);
+            for (int t = 0; t < 2; ++t) {
+                const h8 vh = *reinterpret_cast<const h8 *>(&vsh[at + 32 * t]);
+                const h8 vl = *reinterpret_cast<const h8 *>(&vsh[kHD * kRVH + at + 32 * t]);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, ph[t], o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, pl[t], o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, ph[t], o[db], 0, 0, 0);
             }
         }
+        if (j0 + kKT < j_end) kv.wave_max(tmax, lane, w);   // the next tile's maxima (its loads have landed)
     }
+    // the four lanes of a query hold sums over disjoint keys, all scaled by the same corrections
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    const int64_t i = i0 + 16 * w + c;
+    if (i < n_q) {
+        const float u = ldexpf(1.f, -A);
+        float *orow = (split && part == 1 ? part_o : O) + i * q_stride + (int64_t)h * kHD + 4 * g;
+        if (split) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int64_t i = i0 + 16 * w + 4 * g + r;
-        if (i < n_q) {
-            if (split) {
-                float *orow = (part == 0 ? O + i * q_stride : part_o + i * q_stride) + (int64_t)h * kHD + c;
-#pragma unroll
-                for (int db = 0; db < 8; ++db) orow[16 * db] = o[db][r];
-                if (c == 0) {
-                    float *ml = part_ml + ((int64_t)part * n_heads * n_q + (int64_t)h * n_q + i) * 2;
-                    ml[0] = m[r];
-                    ml[1] = l[r];
-                }
-            } else {
-                float *orow = O + i * q_stride + (int64_t)h * kHD + c;
-#pragma unroll
-                for (int db = 0; db < 8; ++db) orow[16 * db] = o[db][r] / l[r];
+            for (int db = 0; db < 8; ++db) *reinterpret_cast<f4 *>(orow + 16 * db) = o[db] * u;
+            if (g == 0) {
+                float *ml = part_ml + ((int64_t)part * n_heads * n_q + (int64_t)h * n_q + i) * 2;
+                ml[0] = m;
+                ml[1] = l;
             }
+        } else {
+#pragma unroll
+            for (int db = 0; db < 8; ++db) *reinterpret_cast<f4 *>(orow + 16 * db) = o[db] * u / l;
         }
     }
 }
 
 // The two parts of each split tile: workgroup (h, tile, z) merges rows
-// 2z, 2z + 1 of query tile `tile` (attn_prefill_kernel's longest-first
-// order; workgroups of other tiles exit), one element per thread:
-//   O = (e^(m0 - M) o0 + e^(m1 - M) o1) / (e^(m0 - M) l0 + e^(m1 - M) l1),  M = max(m0, m1).
+// 8z .. 8z + 7 of query tile `tile` (attn_prefill_kernel's longest-first
+// order; workgroups of other tiles exit), four elements per thread, with the
+// parts' base-2 maxima:
+//   O = (2^(m0 - M) o0 + 2^(m1 - M) o1) / (2^(m0 - M) l0 + 2^(m1 - M) l1),  M = max(m0, m1).
 __global__ void __launch_bounds__(256)
 attn_prefill_merge(float *__restrict__ O, const float *__restrict__ part_o, const float *__restrict__ part_ml,
                    int64_t n_q, int32_t n_heads, int32_t start, const int32_t *pos, int32_t max_len)
@@ -883,16 +1000,15 @@ attn_prefill_merge(float *__restrict__ O, const float *__restrict__ part_o, cons
     const int h = blockIdx.x;
     const int64_t i0 = (int64_t)(gridDim.y - 1 - blockIdx.y) * kQTile;
     if (prefill_key_tiles(i0, n_q, dev_pos(start, pos), max_len) < kSplitKT) return;
-    const int64_t i = i0 + 2 * blockIdx.z + (threadIdx.x >> 7);
+    const int64_t i = i0 + 8 * blockIdx.z + (threadIdx.x >> 5);
     if (i >= n_q) return;
-    const int64_t q_stride = (int64_t)n_heads * kHD;
-    const int64_t e = i * q_stride + (int64_t)h * kHD + (threadIdx.x & (kHD - 1));
+    const int64_t e = i * (int64_t)n_heads * kHD + (int64_t)h * kHD + 4 * (threadIdx.x & 31);
     const float *ml0 = part_ml + ((int64_t)h * n_q + i) * 2;
     const float *ml1 = part_ml + ((int64_t)n_heads * n_q + (int64_t)h * n_q + i) * 2;
     const float m0 = ml0[0], l0 = ml0[1], m1 = ml1[0], l1 = ml1[1];
-    const float o0 = O[e], o1 = part_o[e];
-    const float mm = fmaxf(m0, m1), a0 = expf(m0 - mm), a1 = expf(m1 - mm);
-    O[e] = (a0 * o0 + a1 * o1) / (a0 * l0 + a1 * l1);
+    const f4 o0 = *reinterpret_cast<const f4 *>(O + e), o1 = *reinterpret_cast<const f4 *>(part_o + e);
+    const float mm = fmaxf(m0, m1), a0 = exp2f(m0 - mm), a1 = exp2f(m1 - mm);
+    *reinterpret_cast<f4 *>(O + e) = (a0 * o0 + a1 * o1) / (a0 * l0 + a1 * l1);
 }
 
 // ---------------------------------------------------------------- argmax
@@ -1272,7 +1388,7 @@ int aih_attention_strided(aih_ctx *ctx, const float *Q, int64_t ldq, const float
                        part_ml);
     int rc = aih_launch_status();
     if (rc || !part_o) return rc;
-    hipLaunchKernelGGL(attn_prefill_merge, dim3(n_heads, (unsigned)tiles, kQTile / 2), dim3(256), 0, ctx->stream, O,
+    hipLaunchKernelGGL(attn_prefill_merge, dim3(n_heads, (unsigned)tiles, kQTile / 8), dim3(256), 0, ctx->stream, O,
                        part_o, part_ml, n_q, n_heads, start, pos, max_len);
     return aih_launch_status();
 }

@@ -170,6 +170,23 @@ def _attn(device, bufs, n_q, start, L_cache, nh=32, nkv=8, pos_dev=None, seed=11
     kvd = nkv * 128
     q = rnd(seed, n_q, nh * 128)
     K, V = rnd(seed + 1, L_cache, kvd), rnd(seed + 2, L_cache, kvd)
+    return _attn_of(device, bufs, q, K, V, start, nh, nkv, pos_dev)
+
+
+def _run_attn(device, bufs, q, K, V, start, nh, nkv):
+    n_q, L_cache = q.shape[0], K.shape[0]
+    Q, KC, VC = bufs.up(q), bufs.up(K), bufs.up(V)
+    O = bufs.empty(q.nbytes)
+    nsc = int(L.aih_attention_scratch_floats(nh, L_cache))
+    S = bufs.empty(nsc * 4)
+    scale = float(np.float32(1) / np.sqrt(np.float32(128)))
+    nat.check(L.aih_attention(device.handle, Q, KC, VC, O, n_q, nh, nkv, 128, start, None, L_cache, scale, S, nsc),
+              "attention")
+    return bufs.read(O, q.size).reshape(q.shape)
+
+
+def _attn_of(device, bufs, q, K, V, start, nh, nkv, pos_dev=None):
+    n_q, L_cache = q.shape[0], K.shape[0]
     Q, KC, VC = bufs.up(q), bufs.up(K), bufs.up(V)
     O = bufs.empty(q.nbytes)
     nsc = int(L.aih_attention_scratch_floats(nh, L_cache))
@@ -221,6 +238,64 @@ def test_attention_prefill(device, bufs, n_q, start):
     # query tiles of 64 and key tiles of 64: full and partial tiles of both,
     # rows that end at the cache's last row (start + n_q = 640)
     _attn(device, bufs, n_q, start, 640)
+
+
+def test_attention_prefill_power_of_two_invariance(device, bufs):
+    # the products run on fp16 hi/lo operands with per-row (Q) and per-tile
+    # (K, V) powers of two: scaling Q by 2^a, K by 2^-a and V by 2^b changes
+    # no rounding, so the output is the unscaled one times 2^b, bit for bit
+    nh, nkv, n_q, L_cache = 8, 2, 200, 256
+    q, K, V = rnd(51, n_q, nh * 128), rnd(52, L_cache, nkv * 128), rnd(53, L_cache, nkv * 128)
+    base = _run_attn(device, bufs, q, K, V, 0, nh, nkv)
+    for a, b in [(40, -30), (-60, 50), (7, 0)]:
+        o = _run_attn(device, bufs, q * np.float32(2.0 ** a), K * np.float32(2.0 ** -a), V * np.float32(2.0 ** b),
+                      0, nh, nkv)
+        assert np.array_equal(o, base * np.float32(2.0 ** b)), (a, b)
+
+
+def test_attention_prefill_value_magnitudes(device, bufs):
+    # V tiles of 64 keys from 1e-6 to 1e6 times N(0, 1), and rows of Q from
+    # 1e-3 to 1: every row (including those that see only the smallest
+    # tiles) within 1e-5 of the oracle, row by row
+    nh, nkv, n_q, L_cache = 4, 2, 320, 320
+    q, K, V = rnd(61, n_q, nh * 128), rnd(62, L_cache, nkv * 128), rnd(63, L_cache, nkv * 128)
+    V *= (10.0 ** (3 * ((np.arange(L_cache) // 64) % 5 - 2))).astype(np.float32)[:, None]
+    q *= (10.0 ** -(np.arange(n_q) % 4)).astype(np.float32)[:, None]
+    o = _run_attn(device, bufs, q, K, V, 0, nh, nkv)
+    ref = ol.attention(q, K, V, list(range(n_q)), nh, nkv, 128)
+    err = np.linalg.norm(o - ref, axis=1) / np.linalg.norm(ref, axis=1)
+    assert err.max() < 1e-5, err.max()
+
+
+def test_attention_prefill_without_workspace(device, bufs):
+    # captured on a fresh context, whose workspace cannot grow inside the
+    # capture: the query tiles run whole and split their own K/V tiles (the
+    # path without the shared K/V images); replays of the graph, with eager
+    # calls between them, all within 1e-5 of the oracle
+    nh, nkv, n_q, L_cache, start = 32, 8, 300, 640, 40
+    q, K, V = rnd(71, n_q, nh * 128), rnd(72, L_cache, nkv * 128), rnd(73, L_cache, nkv * 128)
+    Q, KC, VC, O = bufs.up(q), bufs.up(K), bufs.up(V), bufs.empty(q.nbytes)
+    ref = ol.attention(q, K, V, list(range(start, start + n_q)), nh, nkv, 128)
+    scale = float(np.float32(1) / np.sqrt(np.float32(128)))
+    fresh = C.HipComputeDevice(0)
+    try:
+        h = fresh.handle
+        nat.check(L.aih_capture_begin(h), "capture_begin")
+        rc = L.aih_attention(h, Q, KC, VC, O, n_q, nh, nkv, 128, start, None, L_cache, scale, None, 0)
+        g = ctypes.c_void_p()
+        nat.check(L.aih_capture_end(h, ctypes.byref(g)), "capture_end")
+        nat.check(rc, "attention (captured)")
+        for _ in range(3):
+            nat.check(L.aih_memset(device.handle, O, 0xFF, q.nbytes), "memset")   # NaN until written
+            device.synchronize()
+            nat.check(L.aih_graph_launch(h, g.value), "graph_launch")
+            fresh.synchronize()
+            o = bufs.read(O, q.size).reshape(q.shape)
+            assert np.linalg.norm(o - ref) / np.linalg.norm(ref) < 1e-5
+            _attn(device, bufs, 70, 3, 640)   # eager work between the replays
+        nat.check(L.aih_graph_destroy(g.value), "graph_destroy")
+    finally:
+        fresh.dispose()
 
 
 def test_attention_prefill_at_device_position(device, bufs):

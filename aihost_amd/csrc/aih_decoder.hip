@@ -733,6 +733,54 @@ __device__ __forceinline__ hl2 split_f16(float x, int e)
     return hl2{hi, (_Float16)(xs - (float)hi)};
 }
 
+typedef float fl2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u4x __attribute__((ext_vector_type(4)));
+
+// split_f16 of two values at once (the conversions as packed pairs):
+// {hi, lo} as two words of two halves
+__device__ __forceinline__ void split_pair(float x0, float x1, int e, uint32_t &hi, uint32_t &lo)
+{
+    const fl2 xs = {ldexpf(x0, e), ldexpf(x1, e)};
+    const hl2 h = __builtin_convertvector(xs, hl2);
+    const hl2 l = __builtin_convertvector(xs - __builtin_convertvector(h, fl2), hl2);
+    hi = __builtin_bit_cast(uint32_t, h);
+    lo = __builtin_bit_cast(uint32_t, l);
+}
+
+// 8 values (a: elements 0..3, b: 4..7) split into an h8 of hi and one of lo
+__device__ __forceinline__ void split8(const f4 &a, const f4 &b, int e, h8 &hi, h8 &lo)
+{
+    uint32_t h0, h1, h2, h3, l0, l1, l2, l3;
+    split_pair(a[0], a[1], e, h0, l0);
+    split_pair(a[2], a[3], e, h1, l1);
+    split_pair(b[0], b[1], e, h2, l2);
+    split_pair(b[2], b[3], e, h3, l3);
+    hi = __builtin_bit_cast(h8, u4x{h0, h1, h2, h3});
+    lo = __builtin_bit_cast(h8, u4x{l0, l1, l2, l3});
+}
+
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+
+// a raw buffer over `bytes` bytes from base: 16-byte loads at or past the
+// end return zeros
+__device__ __forceinline__ Rsrc make_rsrc(const void *base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// a pointer the compiler cannot prove uniform, read from the first lane
+__device__ __forceinline__ const float *uniform_ptr(const float *p)
+{
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<const float *>(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ f4 bld16(Rsrc r, uint32_t vo)
+{
+    return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, 0, 0));
+}
+
 __device__ __forceinline__ float xor_lanes_max(float v)   // over lanes l, l^16, l^32, l^48
 {
     v = fmaxf(v, __shfl_xor(v, 16));
@@ -749,21 +797,23 @@ struct KVTile {
     __device__ __forceinline__ void load(const float *__restrict__ Kc, const float *__restrict__ Vc,
                                          int64_t kv_stride, int kvh, int64_t j0, int64_t p_last, int tid)
     {
+        // one buffer per tile over its rows up to p_last (j0 <= p_last):
+        // the rows past it load as zeros
+        const uint32_t row = (uint32_t)kv_stride * 4;
+        const uint32_t bytes = __builtin_amdgcn_readfirstlane((uint32_t)min<int64_t>(p_last + 1 - j0, kKT) * row);
+        const int64_t base = j0 * kv_stride + kvh * kHD;
+        const Rsrc rk = make_rsrc(uniform_ptr(Kc + base), bytes), rv = make_rsrc(uniform_ptr(Vc + base), bytes);
         const int kt_key = tid >> 4, kt_ch = tid & 15;
         const int vt_t = tid >> 7, vt_g = (tid >> 5) & 3, vt_dq = tid & 31;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int64_t jk = j0 + kt_key + 16 * i;
-            const float *kp = Kc + jk * kv_stride + kvh * kHD + 8 * kt_ch;
-            kr[2 * i] = jk <= p_last ? *reinterpret_cast<const f4 *>(kp) : f4{0.f, 0.f, 0.f, 0.f};
-            kr[2 * i + 1] = jk <= p_last ? *reinterpret_cast<const f4 *>(kp + 4) : f4{0.f, 0.f, 0.f, 0.f};
+            const uint32_t at = (uint32_t)(kt_key + 16 * i) * row + 32 * kt_ch;
+            kr[2 * i] = bld16(rk, at);
+            kr[2 * i + 1] = bld16(rk, at + 16);
         }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int64_t jv = j0 + 32 * vt_t + 16 * (e / 4) + 4 * vt_g + e % 4;
-            vr[e] = jv <= p_last ? *reinterpret_cast<const f4 *>(Vc + jv * kv_stride + kvh * kHD + 4 * vt_dq)
-                                 : f4{0.f, 0.f, 0.f, 0.f};
-        }
+        for (int e = 0; e < 8; ++e)
+            vr[e] = bld16(rv, (uint32_t)(32 * vt_t + 16 * (e / 4) + 4 * vt_g + e % 4) * row + 16 * vt_dq);
     }
 
     // this wave's max |K| and |V|, into tmax[0][w] and tmax[1][w]
@@ -794,12 +844,7 @@ struct KVTile {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             h8 hi, lo;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const hl2 v = split_f16(kr[2 * i + e / 4][e % 4], ek);
-                hi[e] = v.x;
-                lo[e] = v.y;
-            }
+            split8(kr[2 * i], kr[2 * i + 1], ek, hi, lo);
             _Float16 *at = lds + (kt_key + 16 * i) * kRKH + 8 * kt_ch;
             *reinterpret_cast<h8 *>(at) = hi;
             *reinterpret_cast<h8 *>(at + kKT * kRKH) = lo;
@@ -807,12 +852,8 @@ struct KVTile {
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
             h8 hi, lo;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const hl2 v = split_f16(vr[e][d], ev);
-                hi[e] = v.x;
-                lo[e] = v.y;
-            }
+            split8(f4{vr[0][d], vr[1][d], vr[2][d], vr[3][d]}, f4{vr[4][d], vr[5][d], vr[6][d], vr[7][d]}, ev, hi,
+                   lo);
             _Float16 *at = lds + 2 * kKT * kRKH + (4 * vt_dq + d) * kRVH + 32 * vt_t + 8 * vt_g;
             *reinterpret_cast<h8 *>(at) = hi;
             *reinterpret_cast<h8 *>(at + kHD * kRVH) = lo;
@@ -942,12 +983,11 @@ attn_prefill_kernel(const float *__restrict__ Q, int64_t ldq, const float *__res
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float p = __builtin_amdgcn_exp2f(sc[kb][r] - mn);
-                sum += p;
-                const hl2 v = split_f16(p, ep);
-                ph[kb / 2][4 * (kb % 2) + r] = v.x;
-                pl[kb / 2][4 * (kb % 2) + r] = v.y;
+                sc[kb][r] = __builtin_amdgcn_exp2f(sc[kb][r] - mn);
+                sum += sc[kb][r];
             }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) split8(sc[2 * t], sc[2 * t + 1], ep, ph[t], pl[t]);
         l = l * corr + sum;
 #pragma unroll
         for (int db = 0; db < 8; ++db) o[db] *= f;

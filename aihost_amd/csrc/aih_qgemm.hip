@@ -306,33 +306,36 @@ qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
     }
 }
 
-// Wide tiles for large products: a workgroup of eight waves owns a 256 (M) x
-// 64 (N) tile, so each dequantized weight feeds twice as many outputs as in
-// qgemm_kernel.  Every wave takes both roles in each super-step s:
+// Wide tiles for large products: a workgroup of eight waves owns a 256 MB (M)
+// x 64 (N) tile (MB = 1 or 2), so each dequantized weight feeds 2 MB times as
+// many outputs as in qgemm_kernel.  Every wave takes both roles in each
+// super-step s:
 //   - it dequantizes its 8 of the 64 weight rows (row 8w + lane / 8) for
 //     super-step s+1 into the other LDS buffer, 32 weights per lane
 //     (Piece32), from packed loads PR256 super-steps ahead;
-//   - it multiplies super-step s: wave w owns rows 32w .. 32w+31 of the M tile
-//     and all 64 columns (two 32x32 accumulators sharing each A fragment), A
-//     fragments from the tiled X one super-step ahead, B fragments from LDS.
+//   - it multiplies super-step s: wave w owns rows 32 MB w .. +32 MB - 1 of
+//     the M tile and all 64 columns (2 MB 32x32 accumulators: each A fragment
+//     feeds two, each B fragment MB), A fragments from the tiled X AD 64-k
+//     chunks ahead, B fragments from LDS.
 // The two waves of a SIMD (w and w + 4) run the two halves in opposite
 // orders, so that one dequantizes while the other multiplies.  On MI355X a
-// workgroup takes about 1.25 times as long as a 128-row one, for twice the
-// outputs.
+// 256-row workgroup takes about 1.25 times as long as a 128-row one, for
+// twice the outputs.
 constexpr int BM2 = 256;
 constexpr int PR256 = 2;
 
-template <class T>
+template <class T, int MB, int AD>
 __global__ void __launch_bounds__(512)
 qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
                 const _Float16 *__restrict__ Xt, int64_t M, float *__restrict__ Y, int epi)
 {
+    static_assert(SC % AD == 0, "A ring depth divides a super-step");
     constexpr int PR = PR256;
     typedef typename Piece32<T>::type P;
     typedef typename P::Raw Raw;
     __shared__ __align__(16) _Float16 wsh[2][BN][LD2];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t m0 = (int64_t)blockIdx.y * BM2, n0 = (int64_t)blockIdx.x * BN;
+    const int64_t m0 = (int64_t)blockIdx.y * BM2 * MB, n0 = (int64_t)blockIdx.x * BN;
     const int nch = (int)(K / 64);
     const int nss = (nch + SC - 1) / SC;
 
@@ -356,19 +359,25 @@ qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
             *reinterpret_cast<h8 *>(d + P::col(ph, q)) = decltype(tail)::value && c >= nch ? h8{} : o[q];
     };
 
-    // multiplication share: rows 32 wave .. +31 of the M tile
+    // multiplication share: rows 32 MB wave .. +32 MB - 1 of the M tile
     const int fr = lane & 31, fk = 8 * (lane >> 5);
     const int64_t kc = K / 16, mblocks = (M + 31) / 32;
-    int64_t mb = (m0 + 32 * wave) / 32;
-    mb = mb < mblocks ? mb : mblocks - 1;
-    const _Float16 *xa = Xt + (mb * kc * 64 + lane) * 8;
-    struct AF { h8 a[4]; };
+    const _Float16 *xa[MB];
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+        int64_t mb = (m0 + 32 * (MB * wave + j)) / 32;
+        mb = mb < mblocks ? mb : mblocks - 1;
+        xa[j] = Xt + (mb * kc * 64 + lane) * 8;
+    }
+    struct AF { h8 a[MB][4]; };
     auto aload = [&](int kb, AF &f) {
         kb = kb < nch ? kb : nch - 1;
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) f.a[kk] = ldg<h8>(xa + ((int64_t)kb * 4 + kk) * 512);
+        for (int j = 0; j < MB; ++j)
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) f.a[j][kk] = ldg<h8>(xa[j] + ((int64_t)kb * 4 + kk) * 512);
     };
-    f16v acc0 = {}, acc1 = {};
+    f16v acc[MB][2] = {};
     struct BF { h8 b0[4], b1[4]; };
     auto bload = [&](int buf, int t, BF &b) {
 #pragma unroll
@@ -379,10 +388,12 @@ qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
     };
     auto mm = [&](const AF &f, const BF &b) {
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[kk], b.b0[kk], acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[kk], b.b1[kk], acc1, 0, 0, 0);
-        }
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+            for (int j = 0; j < MB; ++j) {
+                acc[j][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[j][kk], b.b0[kk], acc[j][0], 0, 0, 0);
+                acc[j][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[j][kk], b.b1[kk], acc[j][1], 0, 0, 0);
+            }
     };
 
     // Iteration it: products of super-step it from buffer it & 1, and, if
@@ -390,8 +401,9 @@ qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
     // from ring slot r, whose loads are then reissued for super-step
     // it + 1 + PR when `reload`.
     Raw ring[PR][1];
-    AF f[SC];
-    BF bb[2];
+    AF f[AD];   // chunk g of the A operand in f[g % AD]
+    constexpr int BD = MB == 1 ? 2 : 1;   // B chunks in registers (the next one loaded early when 2)
+    BF bb[BD];
     // The two waves of a SIMD (w and w + 4) take the two halves in opposite
     // orders, so that one dequantizes while the other multiplies.
     const bool valu_first = wave < 4;
@@ -404,14 +416,17 @@ qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
             }
             __builtin_amdgcn_sched_barrier(0);
         };
-        bload(buf, 0, bb[0]);
+        if (BD == 2) bload(buf, 0, bb[0]);
         if (valu_first) deq();
 #pragma unroll
         for (int t = 0; t < SC; ++t) {
-            if (t + 1 < SC) bload(buf, t + 1, bb[(t + 1) & 1]);
+            if (BD == 1)
+                bload(buf, t, bb[0]);
+            else if (t + 1 < SC)
+                bload(buf, t + 1, bb[(t + 1) % BD]);
             __builtin_amdgcn_sched_barrier(0);
-            mm(f[t], bb[t & 1]);
-            aload(SC * (it + 1) + t, f[t]);
+            mm(f[t % AD], bb[t % BD]);
+            aload(SC * it + t + AD, f[t % AD]);
             __builtin_amdgcn_sched_barrier(0);
         }
         if (!valu_first) deq();
@@ -422,7 +437,7 @@ qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
 #pragma unroll
     for (int j = 0; j < PR; ++j) gload(j, ring[j]);
 #pragma unroll
-    for (int t = 0; t < SC; ++t) aload(t, f[t]);
+    for (int t = 0; t < AD; ++t) aload(t, f[t]);
     stage(std::true_type{}, 0, 0, ring[0]);
     gload(PR, ring[0]);
     __builtin_amdgcn_sched_barrier(0);
@@ -442,20 +457,28 @@ qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
 
     if (epi == kEpiSiluOperand) {
         // after the last barrier the tile buffers are free
-        silu_pairs_operand(acc0, acc1, lane, m0 + 32 * wave, n0, M, N, &wsh[0][0][0] + wave * 32 * 40,
-                           reinterpret_cast<_Float16 *>(Y));
+#pragma unroll
+        for (int j = 0; j < MB; ++j) {
+            silu_pairs_operand(acc[j][0], acc[j][1], lane, m0 + 32 * (MB * wave + j), n0, M, N,
+                               &wsh[0][0][0] + wave * 32 * 40, reinterpret_cast<_Float16 *>(Y));
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");   // the block is read before it is rewritten
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
         return;
     }
     const int64_t na = n0 + fr, nb = n0 + 32 + fr;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int i = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        const int64_t m = m0 + 32 * wave + i;
-        if (m < M) {
-            if (na < N) Y[m * N + na] = epi == kEpiAccumulate ? Y[m * N + na] + acc0[r] : acc0[r];
-            if (nb < N) Y[m * N + nb] = epi == kEpiAccumulate ? Y[m * N + nb] + acc1[r] : acc1[r];
+    for (int j = 0; j < MB; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int i = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            const int64_t m = m0 + 32 * (MB * wave + j) + i;
+            if (m < M) {
+                if (na < N) Y[m * N + na] = epi == kEpiAccumulate ? Y[m * N + na] + acc[j][0][r] : acc[j][0][r];
+                if (nb < N) Y[m * N + nb] = epi == kEpiAccumulate ? Y[m * N + nb] + acc[j][1][r] : acc[j][1][r];
+            }
         }
-    }
 }
 
 template <class T>
@@ -464,14 +487,20 @@ int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t row_byt
 {
     const int64_t gx = (N + BN - 1) / BN, gy = (M + BM - 1) / BM, gy2 = (M + BM2 - 1) / BM2;
     if (gy > 65535 || gx > 0x7FFFFFFF) return AIH_E_LIMIT;
-    // 256-row tiles halve the dequantization per output, and a workgroup of
-    // them takes about 1.25 times as long as one of 128 rows (measured on
-    // MI355X); they are taken when that wins on rounds of workgroups over the
-    // device's CUs
+    // 256-row tiles halve the dequantization per output and 512-row tiles
+    // halve it again; a workgroup of them takes about 1.25 and 2.35 times as
+    // long as one of 128 rows (measured on MI355X at K = 4096).  The shape
+    // with the fewest such rounds of workgroups over the device's CUs wins
+    // (ties to the smaller tile).
+    const int64_t gy4 = (M + 2 * BM2 - 1) / (2 * BM2);
     const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-    const int64_t rounds = (gx * gy + cus - 1) / cus, rounds2 = (gx * gy2 + cus - 1) / cus;
-    if (5 * rounds2 < 4 * rounds)
-        hipLaunchKernelGGL((qgemm256_kernel<T>), dim3((unsigned)gx, (unsigned)gy2), dim3(512), 0, ctx->stream,
+    const int64_t c1 = 20 * ((gx * gy + cus - 1) / cus), c2 = 25 * ((gx * gy2 + cus - 1) / cus),
+                  c4 = 47 * ((gx * gy4 + cus - 1) / cus);
+    if (c4 < c2 && c4 < c1)
+        hipLaunchKernelGGL((qgemm256_kernel<T, 2, 2>), dim3((unsigned)gx, (unsigned)gy4), dim3(512), 0, ctx->stream,
+                           W, N, K, row_bytes, Xh, M, Y, epi);
+    else if (c2 < c1)
+        hipLaunchKernelGGL((qgemm256_kernel<T, 1, SC>), dim3((unsigned)gx, (unsigned)gy2), dim3(512), 0, ctx->stream,
                            W, N, K, row_bytes, Xh, M, Y, epi);
     else
         hipLaunchKernelGGL((qgemm_kernel<T>), dim3((unsigned)gx, (unsigned)gy), dim3(512), 0, ctx->stream,

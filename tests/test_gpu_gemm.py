@@ -48,11 +48,14 @@ def test_shapes(device, orc, qtype, n, k, m):
 
 
 # Grids large enough for the 256-row tiles on a 256-CU device (fewer rounds of
-# workgroups than the 128-row tiles): partial tiles in M and N, and for Q8_0 a
-# partial last super-step.
+# workgroups than the 128-row tiles), and the 512-row tiles of the largest
+# grids: partial tiles in M and N, and for Q8_0 a partial last super-step.
 @pytest.mark.parametrize("qtype,n,k,m", [
     (nat.Q4_K, 6377, 1536, 300), (nat.Q6_K, 6400, 1024, 384),
     (nat.Q8_0, 6377, 1600, 300), (nat.Q4_0, 6400, 1600, 257),
+    # 512-row tiles (more than 256 rows over 447-448 column tiles)
+    (nat.Q4_K, 28600, 512, 300), (nat.Q6_K, 28672, 768, 512),
+    (nat.Q8_0, 28000, 832, 450), (nat.Q4_0, 28672, 576, 257),
 ])
 def test_wide_tiles(device, orc, qtype, n, k, m):
     w = synth_weight(qtype, n, k, seed=n + k)

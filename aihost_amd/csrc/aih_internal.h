@@ -53,6 +53,10 @@ struct aih_ctx {
     // (graphs captured earlier still point at it); all are freed by aih_destroy.
     void *work = nullptr;
     size_t work_bytes = 0;
+    // A second one, for the partial sums of a GEMM split over K (its operand
+    // may sit in the first).
+    void *work2 = nullptr;
+    size_t work2_bytes = 0;
     std::vector<void *> work_retired;
     // Device address of this GPU's static staging buffer (the allocation-free
     // entry point's), set by aih_init.
@@ -64,6 +68,8 @@ struct aih_ctx {
 // (AIH_E_LIMIT): run the operation once outside the capture first.  Returns
 // AIH_OK or a status.
 int aih_workspace(aih_ctx *ctx, size_t bytes, void **out);
+// The second workspace (split-K partial sums), same rules.
+int aih_workspace2(aih_ctx *ctx, size_t bytes, void **out);
 
 // Staging memory a caller supplies in place of the context workspace (the
 // allocation-free entry point passes its static device buffer).
@@ -97,7 +103,8 @@ int aih_launch_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t
                        const float *X, int64_t ldx, float *Y, int64_t ldy, int batch,
                        const aih_scratch *ext = nullptr);
 int aih_launch_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
-                     const float *X, int64_t M, float *Y, const aih_scratch *ext = nullptr);
+                     const float *X, int64_t M, float *Y, const aih_scratch *ext = nullptr,
+                     bool may_split = false);
 // The prefill GEMM in parts: X (M x K fp32) -> the fp16 fragment-order
 // operand Xt (mpad * K halves, mpad = M rounded up to 32); the same operand
 // computed by a fused element-wise step (AIH_PRE_RMSNORM / SILU_MUL /
@@ -107,8 +114,10 @@ int aih_launch_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K
 int aih_launch_x_tile(aih_ctx *ctx, const float *X, int64_t M, int64_t K, void *Xt);
 int aih_launch_x_tile_pre(aih_ctx *ctx, int pre, const float *X, const float *X2, float eps, int64_t M, int64_t K,
                           void *Xt);
+// may_split: the GEMM may split K over workgroups, with partial sums in the
+// second workspace and a reduction (never with caller-provided staging).
 int aih_launch_qgemm_tiled(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const void *Xt,
-                           int64_t M, float *Y, int epi);
+                           int64_t M, float *Y, int epi, bool may_split = false);
 int aih_launch_qmatvec_mfma(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
                             const float *X, int64_t ldx, float *Y, int64_t ldy, int batch,
                             const aih_scratch *ext = nullptr);

@@ -327,36 +327,40 @@ constexpr int PR256 = 2;
 template <class T, int MB, int AD>
 __global__ void __launch_bounds__(512)
 qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
-                const _Float16 *__restrict__ Xt, int64_t M, float *__restrict__ Y, int epi)
+                const _Float16 *__restrict__ Xt, int64_t M, float *__restrict__ Y, int epi,
+                float *__restrict__ P, int ssper)
 {
     static_assert(SC % AD == 0, "A ring depth divides a super-step");
     constexpr int PR = PR256;
-    typedef typename Piece32<T>::type P;
-    typedef typename P::Raw Raw;
+    typedef typename Piece32<T>::type Pc;
+    typedef typename Pc::Raw Raw;
     __shared__ __align__(16) _Float16 wsh[2][BN][LD2];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t m0 = (int64_t)blockIdx.y * BM2 * MB, n0 = (int64_t)blockIdx.x * BN;
     const int nch = (int)(K / 64);
-    const int nss = (nch + SC - 1) / SC;
+    // split z of K (gridDim.z > 1: partial sums into P): super-steps
+    // ss0 .. ss0 + nss - 1; chunk indices below stay absolute
+    const int ss0 = (int)blockIdx.z * ssper;
+    const int nss = min(ssper, (nch + SC - 1) / SC - ss0);
 
     // dequantization share: row 8 wave + rl, 32 weights per lane (chunk pc, half ph)
     const int rl = lane >> 3, p = lane & 7, pc = p >> 1, ph = p & 1;
     const int64_t wn = n0 + 8 * wave + rl;
     const uint8_t *wrow = W + (wn < N ? wn : N - 1) * row_bytes;
     auto gload = [&](int ss, Raw *r) {
-        int c = ss * SC + pc;
+        int c = (ss0 + ss) * SC + pc;
         c = c < nch ? c : nch - 1;
-        P::load(wrow, c, ph, r[0]);
+        Pc::load(wrow, c, ph, r[0]);
     };
     // chunks past K exist only in a last, partial super-step, staged as zeros
     auto stage = [&](auto tail, int ss, int buf, const Raw *r) {
-        const int c = ss * SC + pc;
+        const int c = (ss0 + ss) * SC + pc;
         h8 o[4];
-        P::piece(r[0], c, ph, o);
+        Pc::piece(r[0], c, ph, o);
         _Float16 *d = &wsh[buf][8 * wave + rl][64 * pc];
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-            *reinterpret_cast<h8 *>(d + P::col(ph, q)) = decltype(tail)::value && c >= nch ? h8{} : o[q];
+            *reinterpret_cast<h8 *>(d + Pc::col(ph, q)) = decltype(tail)::value && c >= nch ? h8{} : o[q];
     };
 
     // multiplication share: rows 32 MB wave .. +32 MB - 1 of the M tile
@@ -371,6 +375,7 @@ qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
     }
     struct AF { h8 a[MB][4]; };
     auto aload = [&](int kb, AF &f) {
+        kb += SC * ss0;
         kb = kb < nch ? kb : nch - 1;
 #pragma unroll
         for (int j = 0; j < MB; ++j)
@@ -468,6 +473,7 @@ qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
         return;
     }
     const int64_t na = n0 + fr, nb = n0 + 32 + fr;
+    float *const Pz = P ? P + (int64_t)blockIdx.z * M * N : nullptr;
 #pragma unroll
     for (int j = 0; j < MB; ++j)
 #pragma unroll
@@ -475,33 +481,84 @@ qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
             const int i = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
             const int64_t m = m0 + 32 * (MB * wave + j) + i;
             if (m < M) {
-                if (na < N) Y[m * N + na] = epi == kEpiAccumulate ? Y[m * N + na] + acc[j][0][r] : acc[j][0][r];
-                if (nb < N) Y[m * N + nb] = epi == kEpiAccumulate ? Y[m * N + nb] + acc[j][1][r] : acc[j][1][r];
+                if (Pz) {
+                    if (na < N) Pz[m * N + na] = acc[j][0][r];
+                    if (nb < N) Pz[m * N + nb] = acc[j][1][r];
+                } else {
+                    if (na < N) Y[m * N + na] = epi == kEpiAccumulate ? Y[m * N + na] + acc[j][0][r] : acc[j][0][r];
+                    if (nb < N) Y[m * N + nb] = epi == kEpiAccumulate ? Y[m * N + nb] + acc[j][1][r] : acc[j][1][r];
+                }
             }
         }
 }
 
+// The splits of a GEMM split over K: Y = P_0 + P_1 + ... (in that order),
+// added into Y (Y + sum, the order of the accumulate epilogue) when
+// `accumulate`.  Four elements per thread.
+__global__ void __launch_bounds__(256)
+split_k_sum_kernel(const float *__restrict__ P, int S, int64_t MN, float *__restrict__ Y, int accumulate)
+{
+    for (int64_t i = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x); i < MN; i += 4 * (int64_t)gridDim.x * 256) {
+        f4 s = *reinterpret_cast<const f4 *>(P + i);
+        for (int z = 1; z < S; ++z) s += *reinterpret_cast<const f4 *>(P + (int64_t)z * MN + i);
+        f4 *y = reinterpret_cast<f4 *>(Y + i);
+        *y = accumulate ? *y + s : s;
+    }
+}
+
 template <class T>
 int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
-           const _Float16 *Xh, int64_t M, float *Y, int epi)
+           const _Float16 *Xh, int64_t M, float *Y, int epi, bool may_split)
 {
     const int64_t gx = (N + BN - 1) / BN, gy = (M + BM - 1) / BM, gy2 = (M + BM2 - 1) / BM2;
     if (gy > 65535 || gx > 0x7FFFFFFF) return AIH_E_LIMIT;
     // 256-row tiles halve the dequantization per output and 512-row tiles
     // halve it again; a workgroup of them takes about 1.25 and 2.35 times as
-    // long as one of 128 rows (measured on MI355X at K = 4096).  The shape
-    // with the fewest such rounds of workgroups over the device's CUs wins
-    // (ties to the smaller tile).
+    // long as one of 128 rows (measured on MI355X).  The shape with the
+    // fewest such rounds of workgroups over the device's CUs wins (ties to
+    // the smaller tile).  Costs in units of 1/20 of a 128-row workgroup.
     const int64_t gy4 = (M + 2 * BM2 - 1) / (2 * BM2);
     const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-    const int64_t c1 = 20 * ((gx * gy + cus - 1) / cus), c2 = 25 * ((gx * gy2 + cus - 1) / cus),
-                  c4 = 47 * ((gx * gy4 + cus - 1) / cus);
+    auto rounds = [&](int64_t wgs) { return (double)((wgs + cus - 1) / cus); };
+    const double c1 = 20 * rounds(gx * gy), c2 = 25 * rounds(gx * gy2), c4 = 47 * rounds(gx * gy4);
+    // Products of more than 256 rows whose 512-row tiles leave CUs idle split
+    // K over workgroups: S splits of at least two whole super-steps, partial
+    // sums in the second workspace, then a summing pass (estimated at 5 TB/s
+    // over the partials, Y and the output, plus 2 us of launch; a 128-row
+    // workgroup takes about 29 us per 4096 of K)
+    const int nss = (int)((K / 64 + SC - 1) / SC);
+    int S = 1, ssper = nss;
+    double cs = 1e30;
+    if (may_split && epi != kEpiSiluOperand && M > BM2 && gx * gy4 < cus && M * N % 4 == 0 &&
+        (reinterpret_cast<uintptr_t>(Y) & 15) == 0) {
+        const int want = (int)std::min<int64_t>(std::min<int64_t>(cus / (gx * gy4), nss / 2), 8);
+        if (want >= 2) {
+            ssper = (nss + want - 1) / want;
+            S = (nss + ssper - 1) / ssper;
+            const double unit_us = 29.0 * (double)K / 4096.0 / 20.0;
+            const double sum_us = (double)(S + 2) * (double)(M * N) * 4.0 / 5e12 * 1e6 + 2.0;
+            cs = 47 * rounds(gx * gy4 * S) * (double)ssper / (double)nss + sum_us / unit_us;
+        }
+    }
+    if (S > 1 && cs < c1 && cs < c2 && cs < c4) {
+        void *p = nullptr;
+        if (aih_workspace2(ctx, (size_t)S * (size_t)(M * N) * sizeof(float), &p) == AIH_OK) {
+            hipLaunchKernelGGL((qgemm256_kernel<T, 2, 2>), dim3((unsigned)gx, (unsigned)gy4, (unsigned)S), dim3(512),
+                               0, ctx->stream, W, N, K, row_bytes, Xh, M, Y, epi, static_cast<float *>(p), ssper);
+            int rc = aih_launch_status();
+            if (rc) return rc;
+            const int64_t groups = (M * N / 4 + 255) / 256;
+            hipLaunchKernelGGL(split_k_sum_kernel, dim3((unsigned)std::min<int64_t>(groups, 8 * cus)), dim3(256), 0,
+                               ctx->stream, static_cast<const float *>(p), S, M * N, Y, epi == kEpiAccumulate ? 1 : 0);
+            return aih_launch_status();
+        }
+    }
     if (c4 < c2 && c4 < c1)
         hipLaunchKernelGGL((qgemm256_kernel<T, 2, 2>), dim3((unsigned)gx, (unsigned)gy4), dim3(512), 0, ctx->stream,
-                           W, N, K, row_bytes, Xh, M, Y, epi);
+                           W, N, K, row_bytes, Xh, M, Y, epi, nullptr, nss);
     else if (c2 < c1)
         hipLaunchKernelGGL((qgemm256_kernel<T, 1, SC>), dim3((unsigned)gx, (unsigned)gy2), dim3(512), 0, ctx->stream,
-                           W, N, K, row_bytes, Xh, M, Y, epi);
+                           W, N, K, row_bytes, Xh, M, Y, epi, nullptr, nss);
     else
         hipLaunchKernelGGL((qgemm_kernel<T>), dim3((unsigned)gx, (unsigned)gy), dim3(512), 0, ctx->stream,
                            W, N, K, row_bytes, Xh, M, Y, epi);
@@ -511,17 +568,17 @@ int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t row_byt
 }  // namespace
 
 int aih_launch_qgemm_tiled(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const void *Xtv,
-                           int64_t M, float *Y, int epi)
+                           int64_t M, float *Y, int epi, bool may_split)
 {
     if (K % BK != 0) return AIH_E_LIMIT;
     const int64_t rb = aih_row_bytes(type, K);
     const uint8_t *w = static_cast<const uint8_t *>(W);
     const _Float16 *Xt = static_cast<const _Float16 *>(Xtv);
     switch (type) {
-    case AIH_TYPE_Q4_K: return launch<G4K>(ctx, w, N, K, rb, Xt, M, Y, epi);
-    case AIH_TYPE_Q6_K: return launch<G6K>(ctx, w, N, K, rb, Xt, M, Y, epi);
-    case AIH_TYPE_Q8_0: return launch<G80>(ctx, w, N, K, rb, Xt, M, Y, epi);
-    case AIH_TYPE_Q4_0: return launch<G40>(ctx, w, N, K, rb, Xt, M, Y, epi);
+    case AIH_TYPE_Q4_K: return launch<G4K>(ctx, w, N, K, rb, Xt, M, Y, epi, may_split);
+    case AIH_TYPE_Q6_K: return launch<G6K>(ctx, w, N, K, rb, Xt, M, Y, epi, may_split);
+    case AIH_TYPE_Q8_0: return launch<G80>(ctx, w, N, K, rb, Xt, M, Y, epi, may_split);
+    case AIH_TYPE_Q4_0: return launch<G40>(ctx, w, N, K, rb, Xt, M, Y, epi, may_split);
     default: return AIH_E_UNSUPPORTED;
     }
 }
@@ -538,7 +595,7 @@ int aih_launch_x_tile(aih_ctx *ctx, const float *X, int64_t M, int64_t K, void *
 }
 
 int aih_launch_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
-                     const float *X, int64_t M, float *Y, const aih_scratch *ext)
+                     const float *X, int64_t M, float *Y, const aih_scratch *ext, bool may_split)
 {
     // K advances in 64-element steps.
     if (K % BK != 0) return AIH_E_LIMIT;
@@ -549,5 +606,5 @@ int aih_launch_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K
     if (rc) return rc;
     rc = aih_launch_x_tile(ctx, X, M, K, work);
     if (rc) return rc;
-    return aih_launch_qgemm_tiled(ctx, type, W, N, K, work, M, Y, 0);
+    return aih_launch_qgemm_tiled(ctx, type, W, N, K, work, M, Y, 0, may_split && ext == nullptr);
 }

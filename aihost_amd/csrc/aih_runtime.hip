@@ -57,6 +57,7 @@ int release(aih_ctx *ctx)
     for (int i = 0; i < aih_ctx::kEvents; ++i)
         if (ctx->ev[i]) (void)hipEventDestroy(ctx->ev[i]);
     if (ctx->work) (void)hipFree(ctx->work);
+    if (ctx->work2) (void)hipFree(ctx->work2);
     for (void *p : ctx->work_retired) (void)hipFree(p);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -65,10 +66,12 @@ int release(aih_ctx *ctx)
 
 }  // namespace
 
-int aih_workspace(aih_ctx *ctx, size_t bytes, void **out)
+namespace {
+
+int grow_workspace(aih_ctx *ctx, void *&work, size_t &work_bytes, size_t bytes, void **out)
 {
-    if (bytes <= ctx->work_bytes) {
-        *out = ctx->work;
+    if (bytes <= work_bytes) {
+        *out = work;
         return AIH_OK;
     }
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
@@ -77,27 +80,39 @@ int aih_workspace(aih_ctx *ctx, size_t bytes, void **out)
     // whole MiB, at least double the current size (the retired ones then
     // add up to less than the current one)
     size_t sz = (bytes + ((size_t)1 << 20) - 1) & ~(((size_t)1 << 20) - 1);
-    if (sz < 2 * ctx->work_bytes) sz = 2 * ctx->work_bytes;
+    if (sz < 2 * work_bytes) sz = 2 * work_bytes;
     void *p = nullptr;
     hipError_t e = hipMalloc(&p, sz);
     if (e != hipSuccess) {
         (void)hipGetLastError();
         return (int)e;
     }
-    if (ctx->work) {
+    if (work) {
         // kept until aih_destroy (graphs captured earlier hold its address);
         // the list may allocate on the host: nothing may throw across the C ABI
         try {
-            ctx->work_retired.push_back(ctx->work);
+            ctx->work_retired.push_back(work);
         } catch (...) {
             (void)hipFree(p);
             return (int)hipErrorOutOfMemory;
         }
     }
-    ctx->work = p;
-    ctx->work_bytes = sz;
-    *out = ctx->work;
+    work = p;
+    work_bytes = sz;
+    *out = work;
     return AIH_OK;
+}
+
+}  // namespace
+
+int aih_workspace(aih_ctx *ctx, size_t bytes, void **out)
+{
+    return grow_workspace(ctx, ctx->work, ctx->work_bytes, bytes, out);
+}
+
+int aih_workspace2(aih_ctx *ctx, size_t bytes, void **out)
+{
+    return grow_workspace(ctx, ctx->work2, ctx->work2_bytes, bytes, out);
 }
 
 int aih_stage(aih_ctx *ctx, const aih_scratch *ext, size_t bytes, void **out)
@@ -483,7 +498,7 @@ int qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const f
 }
 
 int qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *X, int64_t M, float *Y,
-          const aih_scratch *ext)
+          const aih_scratch *ext, bool may_split)
 {
     if (!ctx) return AIH_E_INVALID;
     if (!aih_is_quant(type)) return AIH_E_UNSUPPORTED;
@@ -493,14 +508,16 @@ int qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const flo
     if (!W || !X || !Y) return AIH_E_INVALID;
     int rc = select_device(ctx);
     if (rc) return rc;
-    return aih_launch_qgemm(ctx, type, W, N, K, X, M, Y, ext);
+    return aih_launch_qgemm(ctx, type, W, N, K, X, M, Y, ext, may_split);
 }
 
 int matmul_weights_q(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *X, int64_t M,
                      float *Y, const aih_scratch *ext)
 {
     if (M >= 1 && M <= 8) return qmatvec(ctx, type, W, N, K, X, K, Y, N, (int)M, ext);
-    return qgemm(ctx, type, W, N, K, X, M, Y, ext);
+    // never split over K: the allocation-free variant, which shares this
+    // path, has no room for partial sums, and both return the same bits
+    return qgemm(ctx, type, W, N, K, X, M, Y, ext, false);
 }
 
 }  // namespace
@@ -516,7 +533,7 @@ int aih_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
 int aih_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
               const float *X, int64_t M, float *Y)
 {
-    return qgemm(ctx, type, W, N, K, X, M, Y, nullptr);
+    return qgemm(ctx, type, W, N, K, X, M, Y, nullptr, true);
 }
 
 int aih_matmul_weights_q(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
@@ -547,7 +564,7 @@ int aih_qgemm_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
     int rc = select_device(ctx);
     if (rc) return rc;
     const int epi = post == AIH_POST_ACCUMULATE ? 1 : post == AIH_POST_SILU_PAIRS_F16 ? 2 : 0;
-    if (pre == AIH_PRE_F16_OPERAND) return aih_launch_qgemm_tiled(ctx, type, W, N, K, X, M, Y, epi);
+    if (pre == AIH_PRE_F16_OPERAND) return aih_launch_qgemm_tiled(ctx, type, W, N, K, X, M, Y, epi, true);
     const int64_t mpad = (M + 31) / 32 * 32;
     void *work = nullptr;
     rc = aih_stage(ctx, nullptr, (size_t)mpad * (size_t)K * 2, &work);
@@ -555,7 +572,7 @@ int aih_qgemm_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
     rc = pre == AIH_PRE_NONE ? aih_launch_x_tile(ctx, X, M, K, work)
                              : aih_launch_x_tile_pre(ctx, pre, X, X2, eps, M, K, work);
     if (rc) return rc;
-    return aih_launch_qgemm_tiled(ctx, type, W, N, K, work, M, Y, epi);
+    return aih_launch_qgemm_tiled(ctx, type, W, N, K, work, M, Y, epi, true);
 }
 
 int aih_matmul_weights_q_noalloc(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,

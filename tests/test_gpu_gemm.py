@@ -64,6 +64,31 @@ def test_wide_tiles(device, orc, qtype, n, k, m):
     assert_close(y, orc.matvec(qtype, w, n, k, x, nthreads=16), TOL, "type %d %dx%d M=%d" % (qtype, n, k, m))
 
 
+# Products of more than 256 rows whose 512-row tiles leave CUs idle split K
+# over workgroups (aih_qgemm;
+# aih_matmul_weights_q never splits): the oracle's bound, and the unsplit
+# result to summation-order rounding; Q8_0 at K = 4160 and Q4_0 at K = 2112
+# end on a partial super-step inside the last split.
+@pytest.mark.parametrize("qtype,n,k,m", [
+    (nat.Q4_K, 1024, 14336, 300), (nat.Q6_K, 1000, 14336, 512),
+    (nat.Q8_0, 512, 4160, 300), (nat.Q4_0, 256, 2112, 290),
+])
+def test_split_k(device, orc, qtype, n, k, m):
+    w = synth_weight(qtype, n, k, seed=n + k + 1)
+    x = x_of(m, k, seed=m + 5)
+    y = qgemm(device, qtype, w, n, k, x)
+    assert_close(y, orc.matvec(qtype, w, n, k, x, nthreads=16), TOL, "type %d %dx%d M=%d" % (qtype, n, k, m))
+    wb, xb, yb = upload(device, w), upload(device, x), device.create_buffer(m * n * 4)
+    try:
+        nat.check(nat.lib().aih_matmul_weights_q(device.handle, int(qtype), wb.get_pointer(), n, k, xb.get_pointer(),
+                                                 m, yb.get_pointer()), "aih_matmul_weights_q")
+        ref = yb.read_range(0, m * n, np.float32).reshape(m, n)
+    finally:
+        for b in (wb, xb, yb):
+            b.dispose()
+    assert np.linalg.norm(y - ref) / np.linalg.norm(ref) < 1e-6
+
+
 def test_subnormal_scales(device, orc):
     rng = np.random.default_rng(9)
     n, k, m = 70, 512, 33

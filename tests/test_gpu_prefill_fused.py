@@ -80,9 +80,11 @@ MODES = [(nat.PRE_RMSNORM, nat.POST_STORE), (nat.PRE_NONE, nat.POST_ACCUMULATE),
          (nat.PRE_RMSNORM, nat.POST_ACCUMULATE), (nat.PRE_NONE, nat.POST_STORE)]
 
 
-# (Q4_K, 6400, 1024, 300) takes the 256-row tiles on a 256-CU device
+# (Q4_K, 6400, 1024, 300) takes the 256-row tiles on a 256-CU device, and
+# (Q4_K, 1024, 14336, 300) the 512-row tiles split over K (both paths split)
 @pytest.mark.parametrize("qtype,n,k,m", [(nat.Q4_K, 192, 512, 40), (nat.Q6_K, 100, 768, 77),
-                                         (nat.Q8_0, 70, 320, 9), (nat.Q4_K, 6400, 1024, 300)])
+                                         (nat.Q8_0, 70, 320, 9), (nat.Q4_K, 6400, 1024, 300),
+                                         (nat.Q4_K, 1024, 14336, 300)])
 def test_qgemm_fused_equals_separate_operators(device, qtype, n, k, m):
     rng = np.random.default_rng(n + k + m)
     w = synth_weight(qtype, n, k, seed=k)

@@ -16,8 +16,11 @@
 // of 256 elements: four producer waves dequantize W for the next super-step
 // into LDS while four consumer waves multiply the current one, their A
 // fragments loaded straight from the tiled X (see qgemm_kernel).  Large grids
-// use 256 x 64 tiles with every wave in both roles (qgemm256_kernel).  The
-// epilogue stores Y or adds into it (the residual add of a layer).
+// use 256 x 64 or 512 x 64 tiles with every wave in both roles
+// (qgemm256_kernel); tall products whose 512-row grid leaves CUs idle split
+// K over workgroups and sum the partials in a second pass
+// (split_k_sum_kernel).  The epilogue stores Y or adds into it (the residual
+// add of a layer).
 //
 // Precision.  Both operands are rounded to fp16 (11-bit significand) and the
 // products accumulate in fp32: normwise error near 3e-4 against the fp32

@@ -296,7 +296,11 @@ class LlamaDecoder:
         W_o GEMM adding into x, the gate|up GEMM with the FFN RMSNorm in its
         operand and SiLU(gate)*up written as the down GEMM's fp16 operand, the
         down GEMM adding into x.
-        Bit for bit the result of the separate operators (layer())."""
+        Bit for bit the result of the separate operators (layer()), except
+        where a product of more than 256 rows splits K over workgroups here
+        (aih_qgemm_fused: the 8B shape's down projection at 512 rows) and not
+        there (aih_matmul_weights_q): its sums then differ by the fp32
+        rounding of their order."""
         c, L, h, p = self.cfg, self.L, self.h, "blk.%d." % l
         qd = c.n_heads * c.head_dim
         ld = qd + 2 * c.kv_dim

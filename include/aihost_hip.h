@@ -240,12 +240,20 @@ int aih_qmatvec_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t 
  * of 64 (else AIH_E_LIMIT) and X 16-byte aligned.  The workspace cannot grow
  * while the stream is being captured (AIH_E_LIMIT): run the largest GEMM once
  * before capturing.  A workspace replaced by a larger one stays allocated
- * until aih_destroy, so graphs captured earlier stay valid.  Replaces TempF32 + ComputeOps.MatMulWeights for M > 8. */
+ * until aih_destroy, so graphs captured earlier stay valid.  A product of
+ * more than 256 rows whose tiles would leave CUs idle splits K over
+ * workgroups: its partial sums (splits * M * N floats, Y 16-byte aligned) go
+ * to a second context workspace under the same rules and are added in a
+ * fixed order, so a result depends only on the shape, not on the call;
+ * where that workspace cannot grow, the product runs unsplit (the sums then
+ * differ by fp32 rounding of their order).  Replaces TempF32 +
+ * ComputeOps.MatMulWeights for M > 8. */
 int aih_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
               const float *X, int64_t M, float *Y);
 
 /* ComputeOps.MatMulWeights semantics for a quantized weight: routes M <= 8 to
- * aih_qmatvec and larger M to aih_qgemm. */
+ * aih_qmatvec and larger M to aih_qgemm, never split over K (the results of
+ * aih_matmul_weights_q_noalloc, which has no room for partial sums). */
 int aih_matmul_weights_q(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
                          const float *X, int64_t M, float *Y);
 
@@ -268,7 +276,7 @@ int aih_matmul_weights_q(aih_ctx *ctx, int type, const void *W, int64_t N, int64
  * that of the separate operator, then aih_qgemm (and aih_add); likewise the
  * gate|up GEMM with AIH_POST_SILU_PAIRS_F16 followed by the down GEMM with
  * AIH_PRE_F16_OPERAND gives the bits of the gate|up GEMM, aih_silu_mul_pairs
- * and the down GEMM.  Workspace,
+ * and the down GEMM.  Workspace, split over K,
  * K and alignment rules as aih_qgemm; X, X2 16-byte aligned; Y must not
  * alias X or X2.  Replaces, for a prompt, the LayerNorm / SiLU+Multiply /
  * Add around MatMulWeights in ComputeOps.TransformerLayer
@@ -363,7 +371,9 @@ int64_t aih_attention_scratch_floats(int32_t n_heads, int32_t max_len);
  * the query positions must already be in the cache.  head_dim must be 128.
  * One query row uses a split-over-keys kernel and a combine kernel, with
  * `scratch` (aih_attention_scratch_floats floats); more rows use a tiled
- * kernel with an online softmax, whose query tiles with long key ranges run
+ * kernel with an online softmax on the fp16 matrix cores, each fp32 operand
+ * split into two fp16 halves (22 significant bits, products exact, sums in
+ * fp32; normwise error about 1e-7), whose query tiles with long key ranges run
  * as two halves merged afterwards, staged in the context workspace
  * (n_q * n_heads * (head_dim + 4) floats; grown on demand, and where it
  * cannot grow -- inside a capture -- the tiles run whole).  Calls sharing a scratch must not overlap.  Replaces ComputeOps.MultiHeadAttention and FusedMHAGenerate

@@ -238,6 +238,44 @@ rope_qkv_kernel(float *Q, int64_t ldq, const float *K, int64_t ldk, const float 
     }
 }
 
+// rope_qkv_kernel four floats at a time (two rotation pairs), with 32-bit
+// column arithmetic: workgroup (x, y) takes columns 1024 x .. + 1023 of the
+// q|k|v row y (and y + gridDim.y, ...).  Needs head_dim, the row strides and
+// the cache and Q/K/V bases in units of 4 floats and 16-byte aligned, and
+// the table 16-byte aligned; the same products and roundings per element.
+__global__ void __launch_bounds__(256)
+rope_qkv_vec_kernel(float *Q, int64_t ldq, const float *K, int64_t ldk, const float *V, int64_t ldv,
+                    float *__restrict__ Kc, float *__restrict__ Vc, int64_t rows, int32_t q_dim, int32_t kv_dim,
+                    int32_t head_dim, int32_t start, const int32_t *pos, const float *__restrict__ table,
+                    int32_t table_rows, int64_t cache_rows)
+{
+    const int half = head_dim / 2;
+    const int c = 4 * ((int)blockIdx.x * 256 + (int)threadIdx.x);
+    if (c >= q_dim + 2 * kv_dim) return;
+    const int32_t p0 = dev_pos(start, pos);
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+        const int64_t p = p0 + r;
+        if (p < 0 || p >= table_rows) continue;
+        if (c >= q_dim && p >= cache_rows) continue;
+        if (c < q_dim + kv_dim) {
+            const bool is_q = c < q_dim;
+            const int cc = is_q ? c : c - q_dim;
+            const int i = (cc % head_dim) / 2;   // first of the two pairs
+            const f4 t = *reinterpret_cast<const f4 *>(table + 2 * (p * half + i));   // c0, s0, c1, s1
+            const f4 x = *reinterpret_cast<const f4 *>(is_q ? Q + r * ldq + cc : K + r * ldk + cc);
+            f4 y;
+            y.x = x.x * t.x - x.y * t.y;
+            y.y = x.x * t.y + x.y * t.x;
+            y.z = x.z * t.z - x.w * t.w;
+            y.w = x.z * t.w + x.w * t.z;
+            *reinterpret_cast<f4 *>(is_q ? Q + r * ldq + cc : Kc + p * kv_dim + cc) = y;
+        } else {
+            const int cv = c - q_dim - kv_dim;
+            *reinterpret_cast<f4 *>(Vc + p * kv_dim + cv) = *reinterpret_cast<const f4 *>(V + r * ldv + cv);
+        }
+    }
+}
+
 // ---------------------------------------------------------------- row store
 // Y[(p + r) * cols + c] = X[r * cols + c] for rows whose position p + r is
 // below y_rows (a KV cache append).
@@ -1322,6 +1360,15 @@ int aih_rope_qkv(aih_ctx *ctx, float *Q, int64_t ldq, const float *K, int64_t ld
         return AIH_E_INVALID;
     if (rows == 0) return AIH_OK;
     if (!pos && (start < 0 || start + rows > table_rows || start + rows > cache_rows)) return AIH_E_LIMIT;
+    const int64_t q_dim = (int64_t)n_heads * head_dim, kv_dim = (int64_t)n_kv_heads * head_dim;
+    if (head_dim % 4 == 0 && ldq % 4 == 0 && ldk % 4 == 0 && ldv % 4 == 0 && q_dim + 2 * kv_dim < (1 << 30) &&
+        aligned16(Q) && aligned16(K) && aligned16(V) && aligned16(Kc) && aligned16(Vc) && aligned16(table)) {
+        const int64_t gx = (q_dim + 2 * kv_dim + 1023) / 1024;
+        hipLaunchKernelGGL(rope_qkv_vec_kernel, dim3((unsigned)gx, (unsigned)std::min<int64_t>(rows, 65535)),
+                           dim3(256), 0, ctx->stream, Q, ldq, K, ldk, V, ldv, Kc, Vc, rows, (int32_t)q_dim,
+                           (int32_t)kv_dim, head_dim, start, pos, table, table_rows, cache_rows);
+        return aih_launch_status();
+    }
     const int64_t work = rows * (int64_t)(n_heads + 2 * n_kv_heads) * (head_dim / 2);
     hipLaunchKernelGGL(rope_qkv_kernel, dim3(grid_for(ctx, work)), dim3(256), 0, ctx->stream, Q, ldq, K, ldk, V, ldv,
                        Kc, Vc, rows, n_heads, n_kv_heads, head_dim, start, pos, table, table_rows, cache_rows);

@@ -346,17 +346,20 @@ def test_argmax_ties_nan_and_history(device, bufs):
     assert bufs.read(T, 1, np.int32)[0] == 0
 
 
-@pytest.mark.parametrize("rows,start,pos_dev", [(1, 0, 517), (40, 0, None), (3, 61, None)])
-def test_rope_qkv_equals_separate_ops(device, bufs, rows, start, pos_dev):
+# pad = 2: rows 2 floats longer than the three blocks, so the row stride is
+# not a multiple of 4 floats (the scalar kernel instead of the 16-byte one)
+@pytest.mark.parametrize("rows,start,pos_dev,pad", [(1, 0, 517, 0), (40, 0, None, 0), (3, 61, None, 0),
+                                                    (40, 0, None, 2)])
+def test_rope_qkv_equals_separate_ops(device, bufs, rows, start, pos_dev, pad):
     nh, nkv, hd, max_len = 32, 8, 128, 640
     qd, kvd = nh * hd, nkv * hd
     T, t = _table(device, bufs, 640)
-    fused = rnd(40 + rows, rows, qd + 2 * kvd)               # one fused projection output per row
-    q, k, v = fused[:, :qd], fused[:, qd:qd + kvd], fused[:, qd + kvd:]
+    fused = rnd(40 + rows, rows, qd + 2 * kvd + pad)         # one fused projection output per row
+    q, k, v = fused[:, :qd], fused[:, qd:qd + kvd], fused[:, qd + kvd:qd + 2 * kvd]
     F = bufs.up(fused)
     KC, VC = bufs.empty(max_len * kvd * 4, fill=0), bufs.empty(max_len * kvd * 4, fill=0)
     P = bufs.up(np.array([pos_dev], np.int32)) if pos_dev is not None else None
-    ld = qd + 2 * kvd
+    ld = qd + 2 * kvd + pad
     nat.check(L.aih_rope_qkv(device.handle, F, ld, F + qd * 4, ld, F + (qd + kvd) * 4, ld, KC, VC, rows, nh, nkv, hd,
                              start, P, T, 640, max_len), "rope_qkv")
     p0 = start + (pos_dev or 0)

@@ -835,10 +835,12 @@ struct KVTile {
     __device__ __forceinline__ void load(const float *__restrict__ Kc, const float *__restrict__ Vc,
                                          int64_t kv_stride, int kvh, int64_t j0, int64_t p_last, int tid)
     {
-        // one buffer per tile over its rows up to p_last (j0 <= p_last):
-        // the rows past it load as zeros
+        // one buffer per tile over its rows up to p_last: the rows past it
+        // (all of them when p_last < j0, as for a position before the
+        // cache) load as zeros
         const uint32_t row = (uint32_t)kv_stride * 4;
-        const uint32_t bytes = __builtin_amdgcn_readfirstlane((uint32_t)min<int64_t>(p_last + 1 - j0, kKT) * row);
+        const int64_t valid = max<int64_t>(0, min<int64_t>(p_last + 1 - j0, kKT));
+        const uint32_t bytes = __builtin_amdgcn_readfirstlane((uint32_t)valid * row);
         const int64_t base = j0 * kv_stride + kvh * kHD;
         const Rsrc rk = make_rsrc(uniform_ptr(Kc + base), bytes), rv = make_rsrc(uniform_ptr(Vc + base), bytes);
         const int kt_key = tid >> 4, kt_ch = tid & 15;

@@ -87,6 +87,8 @@ SIGNATURES = {
                            ctypes.c_int32, _vp, ctypes.c_int32, _f, _vp, _i64]),
     "aih_attention_strided": (_i, [_vp, _vp, _i64, _vp, _vp, _vp, _i64, ctypes.c_int32, ctypes.c_int32,
                                    ctypes.c_int32, ctypes.c_int32, _vp, ctypes.c_int32, _f, _vp, _i64]),
+    "aih_attention_operand": (_i, [_vp, _vp, _i64, _vp, _vp, _vp, _i64, ctypes.c_int32, ctypes.c_int32,
+                                   ctypes.c_int32, ctypes.c_int32, _vp, ctypes.c_int32, _f]),
     "aih_attention_decode_qkv": (_i, [_vp, _vp, _vp, _vp, _vp, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                       ctypes.c_int32, _vp, _vp, ctypes.c_int32, ctypes.c_int32, _f, _vp, _i64]),
     "aih_embed_q": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),

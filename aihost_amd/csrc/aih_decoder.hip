@@ -907,11 +907,22 @@ __device__ __forceinline__ int split_exp_of(const float (*tmax)[4], int which)
 }
 
 
+// Four consecutive values k0 .. k0 + 3 (k0 % 4 == 0) of row m of a GEMM
+// operand with K columns, rounded to fp16 into its MFMA fragment-order image
+// (the layout x_tile_kernel writes: 32-row blocks, 16-column k steps, 8
+// halves per lane slot).
+__device__ __forceinline__ void store_operand4(_Float16 *Xt, int64_t K, int64_t m, int64_t k0, f4 v)
+{
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const int64_t slot = ((m >> 5) * (K / 16) + (k0 >> 4)) * 64 + (m & 31) + 32 * ((k0 >> 3) & 1);
+    *reinterpret_cast<h4 *>(Xt + slot * 8 + (k0 & 7)) = h4{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+}
+
 __global__ void __launch_bounds__(256, 2)
 attn_prefill_kernel(const float *__restrict__ Q, int64_t ldq, const float *__restrict__ Kc,
                     const float *__restrict__ Vc, float *__restrict__ O, int64_t n_q, int32_t n_heads,
                     int32_t n_kv_heads, int32_t start, const int32_t *pos, int32_t max_len, float scale,
-                    float *__restrict__ part_o, float *__restrict__ part_ml)
+                    float *__restrict__ part_o, float *__restrict__ part_ml, _Float16 *__restrict__ Xt)
 {
     __shared__ __align__(16) _Float16 lds[2 * kKT * kRKH + 2 * kHD * kRVH];   // K hi, K lo, V^T hi, V^T lo
     __shared__ float tmax[2][4];                                               // [K, V][wave]: the next tile
@@ -1061,10 +1072,18 @@ attn_prefill_kernel(const float *__restrict__ Q, int64_t ldq, const float *__res
                 ml[0] = m;
                 ml[1] = l;
             }
+        } else if (Xt) {
+#pragma unroll
+            for (int db = 0; db < 8; ++db) store_operand4(Xt, q_stride, i, (int64_t)h * kHD + 16 * db + 4 * g, o[db] * u / l);
         } else {
 #pragma unroll
             for (int db = 0; db < 8; ++db) *reinterpret_cast<f4 *>(orow + 16 * db) = o[db] * u / l;
         }
+    } else if (Xt && part == 0 && i < (n_q + 31) / 32 * 32) {
+        // operand rows past n_q, up to the next multiple of 32, are zero
+#pragma unroll
+        for (int db = 0; db < 8; ++db)
+            store_operand4(Xt, q_stride, i, (int64_t)h * kHD + 16 * db + 4 * g, f4{0.f, 0.f, 0.f, 0.f});
     }
 }
 
@@ -1075,7 +1094,8 @@ attn_prefill_kernel(const float *__restrict__ Q, int64_t ldq, const float *__res
 //   O = (2^(m0 - M) o0 + 2^(m1 - M) o1) / (2^(m0 - M) l0 + 2^(m1 - M) l1),  M = max(m0, m1).
 __global__ void __launch_bounds__(256)
 attn_prefill_merge(float *__restrict__ O, const float *__restrict__ part_o, const float *__restrict__ part_ml,
-                   int64_t n_q, int32_t n_heads, int32_t start, const int32_t *pos, int32_t max_len)
+                   int64_t n_q, int32_t n_heads, int32_t start, const int32_t *pos, int32_t max_len,
+                   _Float16 *__restrict__ Xt)
 {
     const int h = blockIdx.x;
     const int64_t i0 = (int64_t)(gridDim.y - 1 - blockIdx.y) * kQTile;
@@ -1088,7 +1108,11 @@ attn_prefill_merge(float *__restrict__ O, const float *__restrict__ part_o, cons
     const float m0 = ml0[0], l0 = ml0[1], m1 = ml1[0], l1 = ml1[1];
     const f4 o0 = *reinterpret_cast<const f4 *>(O + e), o1 = *reinterpret_cast<const f4 *>(part_o + e);
     const float mm = fmaxf(m0, m1), a0 = exp2f(m0 - mm), a1 = exp2f(m1 - mm);
-    *reinterpret_cast<f4 *>(O + e) = (a0 * o0 + a1 * o1) / (a0 * l0 + a1 * l1);
+    const f4 r = (a0 * o0 + a1 * o1) / (a0 * l0 + a1 * l1);
+    if (Xt)
+        store_operand4(Xt, (int64_t)n_heads * kHD, i, (int64_t)h * kHD + 4 * (threadIdx.x & 31), r);
+    else
+        *reinterpret_cast<f4 *>(O + e) = r;
 }
 
 // ---------------------------------------------------------------- argmax
@@ -1412,6 +1436,38 @@ int aih_add(aih_ctx *ctx, const float *A, const float *B, float *Y, int64_t n)
     return aih_launch_status();
 }
 
+// The tiled (prefill) attention: the output as fp32 rows in O, or, with Xt,
+// as the fp16 operand image of a GEMM over its n_heads * kHD columns.  Split
+// query tiles stage their halves (and, for Xt, the first half's output) in
+// the context workspace; where it cannot grow (inside a capture) every tile
+// runs whole.
+static int prefill_attention(aih_ctx *ctx, const float *Q, int64_t ldq, const float *Kc, const float *Vc, float *O,
+                             _Float16 *Xt, int64_t n_q, int32_t n_heads, int32_t n_kv_heads, int32_t start,
+                             const int32_t *pos, int32_t max_len, float scale)
+{
+    const int64_t tiles = (n_q + kQTile - 1) / kQTile;
+    if (2 * tiles > 65535) return AIH_E_LIMIT;
+    const size_t img = (size_t)n_q * (size_t)n_heads * kHD;
+    float *part_o = nullptr, *part_ml = nullptr;
+    {
+        void *work = nullptr;
+        const size_t need = (img * (Xt ? 2 : 1) + (size_t)n_q * n_heads * 4) * sizeof(float);
+        if (aih_stage(ctx, nullptr, need, &work) == AIH_OK) {
+            part_o = static_cast<float *>(work);
+            part_ml = part_o + img;
+            if (Xt) O = part_ml + (size_t)n_q * n_heads * 4;   // the first halves' outputs
+        }
+    }
+    hipLaunchKernelGGL(attn_prefill_kernel, dim3(n_heads, (unsigned)(tiles * (part_o ? 2 : 1))), dim3(256), 0,
+                       ctx->stream, Q, ldq, Kc, Vc, O, n_q, n_heads, n_kv_heads, start, pos, max_len, scale, part_o,
+                       part_ml, Xt);
+    int rc = aih_launch_status();
+    if (rc || !part_o) return rc;
+    hipLaunchKernelGGL(attn_prefill_merge, dim3(n_heads, (unsigned)tiles, kQTile / 8), dim3(256), 0, ctx->stream, O,
+                       part_o, part_ml, n_q, n_heads, start, pos, max_len, Xt);
+    return aih_launch_status();
+}
+
 int64_t aih_attention_scratch_floats(int32_t n_heads, int32_t max_len)
 {
     if (n_heads <= 0 || max_len <= 0) return AIH_E_INVALID;
@@ -1458,28 +1514,23 @@ int aih_attention_strided(aih_ctx *ctx, const float *Q, int64_t ldq, const float
         hipLaunchKernelGGL(attn_decode_combine, dim3(n_heads), dim3(kHD), 0, ctx->stream, scratch, O, n_split);
         return aih_launch_status();
     }
-    const int64_t tiles = (n_q + kQTile - 1) / kQTile;
-    if (2 * tiles > 65535) return AIH_E_LIMIT;
-    // split tiles need one more output image and two floats per row and part,
-    // from the context workspace; without it (a capture that would have to
-    // grow it) every tile runs whole
-    float *part_o = nullptr, *part_ml = nullptr;
-    {
-        void *work = nullptr;
-        const size_t need = (size_t)n_q * (size_t)n_heads * (kHD + 4) * sizeof(float);
-        if (aih_stage(ctx, nullptr, need, &work) == AIH_OK) {
-            part_o = static_cast<float *>(work);
-            part_ml = part_o + (size_t)n_q * n_heads * kHD;
-        }
-    }
-    hipLaunchKernelGGL(attn_prefill_kernel, dim3(n_heads, (unsigned)(tiles * (part_o ? 2 : 1))), dim3(256), 0,
-                       ctx->stream, Q, ldq, Kc, Vc, O, n_q, n_heads, n_kv_heads, start, pos, max_len, scale, part_o,
-                       part_ml);
-    int rc = aih_launch_status();
-    if (rc || !part_o) return rc;
-    hipLaunchKernelGGL(attn_prefill_merge, dim3(n_heads, (unsigned)tiles, kQTile / 8), dim3(256), 0, ctx->stream, O,
-                       part_o, part_ml, n_q, n_heads, start, pos, max_len);
-    return aih_launch_status();
+    return prefill_attention(ctx, Q, ldq, Kc, Vc, O, nullptr, n_q, n_heads, n_kv_heads, start, pos, max_len, scale);
+}
+
+int aih_attention_operand(aih_ctx *ctx, const float *Q, int64_t ldq, const float *Kc, const float *Vc, void *Xt,
+                          int64_t n_q, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t start,
+                          const int32_t *pos, int32_t max_len, float scale)
+{
+    if (!ctx || !Q || !Kc || !Vc || !Xt || n_q < 0 || n_heads <= 0 || n_kv_heads <= 0 || max_len <= 0)
+        return AIH_E_INVALID;
+    if (ldq < (int64_t)n_heads * head_dim || ldq % 4) return AIH_E_INVALID;
+    if (n_heads % n_kv_heads) return AIH_E_INVALID;
+    if (head_dim != kHD) return AIH_E_UNSUPPORTED;
+    if (!aligned16(Q) || !aligned16(Kc) || !aligned16(Vc) || !aligned16(Xt)) return AIH_E_INVALID;
+    if (n_q == 0) return AIH_OK;
+    if (!pos && (start < 0 || start + n_q > max_len)) return AIH_E_LIMIT;
+    return prefill_attention(ctx, Q, ldq, Kc, Vc, nullptr, static_cast<_Float16 *>(Xt), n_q, n_heads, n_kv_heads,
+                             start, pos, max_len, scale);
 }
 
 int aih_attention_decode_qkv(aih_ctx *ctx, const float *QKV, float *Kc, float *Vc, float *O, int32_t n_heads,

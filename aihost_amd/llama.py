@@ -230,6 +230,8 @@ class LlamaDecoder:
         # prefill: gate and up (interleaved with a fused gate|up buffer), then
         # SiLU(gate) * up in self.up
         self.gate, self.up = buf(P * 2 * c.ffn * 4), buf(P * c.ffn * 4)
+        # the attention output as the W_o GEMM's fp16 operand (fused prefill)
+        self.att16 = buf((P + 31) // 32 * 32 * c.n_heads * c.head_dim * 2)
         # outputs of the fused Q|K|V projection (one row in decode, up to
         # max_prefill rows in the fused prefill) and of the decode gate|up
         # (SiLU-pairs) matvec
@@ -292,8 +294,8 @@ class LlamaDecoder:
     def _prefill_layer_fused(self, l, rows, start, pos):
         """One layer over `rows` > 8 prompt rows in six GEMM-centred steps: the
         Q|K|V GEMM with the attention RMSNorm computed into its operand, RoPE
-        and the cache store, attention reading the query block in place, the
-        W_o GEMM adding into x, the gate|up GEMM with the FFN RMSNorm in its
+        and the cache store, attention reading the query block in place and
+        writing the W_o GEMM's fp16 operand, the W_o GEMM adding into x, the gate|up GEMM with the FFN RMSNorm in its
         operand and SiLU(gate)*up written as the down GEMM's fp16 operand, the
         down GEMM adding into x.
         Bit for bit the result of the separate operators (layer()), except
@@ -310,10 +312,10 @@ class LlamaDecoder:
         nat.check(L.aih_rope_qkv(h, q, ld, k, ld, v, ld, self.kc[l], self.vc[l], rows, c.n_heads, c.n_kv_heads,
                                  c.head_dim, start, pos, self.table, self.max_len, self.max_len),
                   "rope q, k -> cache, v -> cache")
-        nat.check(L.aih_attention_strided(h, q, ld, self.kc[l], self.vc[l], self.att, rows, c.n_heads,
-                                          c.n_kv_heads, c.head_dim, start, pos, self.max_len, self.scale,
-                                          self.scratch, self.scratch_floats), "attention")
-        self._mmx(p + "attn_output", self.att, None, nat.PRE_NONE, nat.POST_ACCUMULATE, rows, self.x)
+        nat.check(L.aih_attention_operand(h, q, ld, self.kc[l], self.vc[l], self.att16, rows, c.n_heads,
+                                          c.n_kv_heads, c.head_dim, start, pos, self.max_len, self.scale),
+                  "attention")
+        self._mmx(p + "attn_output", self.att16, None, nat.PRE_F16_OPERAND, nat.POST_ACCUMULATE, rows, self.x)
         norm = self.w.ptr(p + "ffn_norm")
         if p + "ffn_gate_up" in self.w and (2 * c.ffn) % 128 == 0:
             # SiLU(gate)*up leaves the gate|up GEMM as the down GEMM's fp16 operand

@@ -392,6 +392,23 @@ int aih_attention_strided(aih_ctx *ctx, const float *Q, int64_t ldq, const float
                           const int32_t *pos, int32_t max_len, float scale, float *scratch,
                           int64_t scratch_floats);
 
+/* aih_attention_strided writing its output, instead of as fp32 rows, as the
+ * fp16 operand image of a GEMM over its n_heads*head_dim columns: the X of
+ * aih_qgemm_fused with AIH_PRE_F16_OPERAND (mpad = n_q rounded up to 32
+ * rows, rows past n_q zero; mpad*n_heads*head_dim*2 bytes, 16-byte aligned).
+ * For n_q > 1 the values are the ones aih_attention_strided computes,
+ * rounded to fp16 as aih_qgemm_fused rounds an fp32 X, so the GEMM that
+ * follows gives the bits of aih_attention_strided + aih_qgemm_fused
+ * (AIH_PRE_NONE), without the fp32 rows and their conversion pass.  Every
+ * n_q uses the tiled kernel (a single row there takes the decode kernel); split
+ * query tiles stage in the context workspace (n_q*n_heads*(2*head_dim+4)
+ * floats, same rules as aih_attention).  Replaces, for a prompt, the
+ * attention output that feeds the W_o MatMulWeights in
+ * ComputeOps.TransformerLayer (ComputeOps.cs:1250-1356). */
+int aih_attention_operand(aih_ctx *ctx, const float *Q, int64_t ldq, const float *Kc, const float *Vc, void *Xt,
+                          int64_t n_q, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t start,
+                          const int32_t *pos, int32_t max_len, float scale);
+
 /* One decode step's attention with the position steps before it fused in:
  * for the projection output QKV of one row at position p = start + *pos
  * (q | k | v: n_heads*head_dim, then n_kv_heads*head_dim twice, as one fused

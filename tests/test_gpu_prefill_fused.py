@@ -6,6 +6,8 @@
   partial last row block (rows past M are zero in the operand);
 - aih_attention_strided reading the query block of a Q|K|V row in place vs
   aih_attention on a contiguous copy;
+- aih_attention_operand vs aih_attention_strided's fp32 output rounded into
+  the GEMM operand layout, and the W_o GEMM from either;
 - a decoder prefill through the fused layer vs the same prompt through the
   separate operators: logits and K/V caches identical.
 """
@@ -209,6 +211,72 @@ def test_attention_strided_equals_contiguous(device, n_q, start):
     finally:
         for x in bufs + [o1, o2, sb]:
             x.dispose()
+
+
+def _operand_image(x, mpad):
+    """x (M x K fp32) as the fp16 MFMA fragment-order operand of mpad rows
+    (rows past M zero): element (m, k) at half ((m/32 * K/16 + k/16) * 64 +
+    m%32 + 32 * (k/8 % 2)) * 8 + k%8."""
+    m_, k_ = x.shape
+    img = np.zeros(mpad * k_, np.float16)
+    m = np.arange(mpad)[:, None]
+    k = np.arange(k_)[None, :]
+    idx = (((m // 32) * (k_ // 16) + k // 16) * 64 + m % 32 + 32 * ((k // 8) % 2)) * 8 + k % 8
+    full = np.zeros((mpad, k_), np.float32)
+    full[:m_] = x
+    img[idx.ravel()] = full.ravel().astype(np.float16)
+    return img
+
+
+# (300, 0) has split query tiles (three or more key tiles), (70, 30) a
+# partial last row block, (2, 100) two rows
+@pytest.mark.parametrize("n_q,start", [(300, 0), (70, 30), (2, 100)])
+def test_attention_operand_equals_fp32_output_rounded(device, n_q, start):
+    """aih_attention_operand: the fp32 output of aih_attention_strided,
+    rounded to fp16 in the GEMM operand layout, bit for bit, and through the
+    W_o GEMM the bits of the fp32 path."""
+    L, h = nat.lib(), device.handle
+    n_heads, n_kv, hd, max_len = 8, 2, 128, 320
+    qd, kvd = n_heads * hd, n_kv * hd
+    ld = qd + 2 * kvd
+    rng = np.random.default_rng(n_q + start + 7)
+    qkv = rng.standard_normal((n_q, ld)).astype(np.float32)
+    kc = rng.standard_normal((max_len, kvd)).astype(np.float32)
+    vc = rng.standard_normal((max_len, kvd)).astype(np.float32)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    mpad = (n_q + 31) // 32 * 32
+    n_out = 192
+    w = synth_weight(nat.Q4_K, n_out, qd, seed=5)
+    bufs = [upload(device, a) for a in (qkv, kc, vc, w)]
+    o = device.create_buffer(n_q * qd * 4)
+    xt = upload(device, np.full(mpad * qd, np.float16(np.nan)))   # every half must be written
+    y1, y2 = device.create_buffer(n_q * n_out * 4), device.create_buffer(n_q * n_out * 4)
+    sf = int(L.aih_attention_scratch_floats(n_heads, max_len))
+    sb = device.create_buffer(sf * 4)
+    try:
+        qs, kb, vb, wb = bufs
+        _check(L.aih_attention_strided(h, qs.get_pointer(), ld, kb.get_pointer(), vb.get_pointer(), o.get_pointer(),
+                                       n_q, n_heads, n_kv, hd, start, None, max_len, scale, sb.get_pointer(), sf),
+               "strided")
+        _check(L.aih_attention_operand(h, qs.get_pointer(), ld, kb.get_pointer(), vb.get_pointer(), xt.get_pointer(),
+                                       n_q, n_heads, n_kv, hd, start, None, max_len, scale), "operand")
+        out = _read(o, n_q * qd).reshape(n_q, qd)
+        img = np.empty(mpad * qd, np.float16)
+        nat.check(L.aih_memcpy_d2h(h, img.ctypes.data, xt.get_pointer(), img.nbytes), "d2h")
+        assert np.isfinite(out).all()
+        assert np.array_equal(img.view(np.uint16), _operand_image(out, mpad).view(np.uint16))
+        _check(L.aih_qgemm_fused(h, nat.Q4_K, wb.get_pointer(), n_out, qd, o.get_pointer(), None, EPS, n_q,
+                                 nat.PRE_NONE, nat.POST_STORE, y1.get_pointer()), "fp32 X")
+        _check(L.aih_qgemm_fused(h, nat.Q4_K, wb.get_pointer(), n_out, qd, xt.get_pointer(), None, EPS, n_q,
+                                 nat.PRE_F16_OPERAND, nat.POST_STORE, y2.get_pointer()), "operand X")
+        a, b = _read(y1, n_q * n_out), _read(y2, n_q * n_out)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        assert L.aih_attention_operand(h, qs.get_pointer(), ld, kb.get_pointer(), vb.get_pointer(),
+                                       xt.get_pointer() + 8, n_q, n_heads, n_kv, hd, start, None, max_len,
+                                       scale) == nat.AIH_E_INVALID
+    finally:
+        for b in bufs + [o, xt, y1, y2, sb]:
+            b.dispose()
 
 
 CFG = llama.LlamaConfig(n_layers=2, dim=512, n_heads=4, n_kv_heads=2, head_dim=128, ffn=1024, vocab=1000)

@@ -713,8 +713,8 @@ attn_decode_combine(const float *__restrict__ part, float *__restrict__ O, int32
 // P'' <= 2^15 and the O accumulators hold 2^A O; when A drops, they are
 // rescaled by the exact power of two with the softmax correction.
 //
-// Workgroup (h, tile) of 256 threads owns kQTile = 64 queries; wave w the
-// 16 queries 16w .. 16w+15.  The products are transposed, S^T = K Q^T and
+// Workgroup (h, tile) owns kQTile = 64 queries; wave w of each half (below)
+// the 16 queries 16w .. 16w+15.  The products are transposed, S^T = K Q^T and
 // O^T = V^T P^T, so that the softmax output is already the B operand of the
 // second product and never leaves the registers.  16x16x32 layouts (lane l,
 // g = l/16, c = l%16): A[i][k] lane i + 16(k/8) element k%8, B[k][j] lane
@@ -741,15 +741,14 @@ constexpr int kRVH = 72;      // V^T image row (dim) stride in LDS, halves: 64 s
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 hl2 __attribute__((ext_vector_type(2)));   // {hi, lo}
 
-// Causal balance: query tiles are dispatched longest first, and a tile whose
-// keys span at least kSplitKT key tiles is done by two workgroups, dispatched
-// one after the other, over its first n_kt / 2 and its last n_kt - n_kt / 2
-// key tiles.  Part 0
-// leaves its unnormalised output in O and part 1 in part_o, with each row's
-// running max (base 2) and sum in part_ml; attn_prefill_merge combines them.
-// Every row of such a tile attends to the first key of part 1's range (its
-// positions are at least p_last - 63 >= 64 (n_kt / 2) when n_kt >= 3, since
-// p_last >= 64 (n_kt - 1)), so both parts' softmax states start finite.
+// Causal balance: a workgroup of 512 threads owns a query tile, dispatched
+// longest first, as two halves of four waves with an LDS image each.  A tile
+// whose keys span at least kSplitKT key tiles gives half 0 its first n_kt / 2
+// key tiles and half 1 the last n_kt - n_kt / 2; a shorter one gives half 1
+// all of them.  Every row of a split tile attends to the first key of half
+// 1's range (its positions are at least p_last - 63 >= 64 (n_kt / 2) when
+// n_kt >= 3, since p_last >= 64 (n_kt - 1)), so both halves' softmax states
+// start finite.  The halves merge through LDS at the end.
 constexpr int kSplitKT = 3;
 
 __device__ __forceinline__ int64_t prefill_key_tiles(int64_t i0, int64_t n_q, int32_t p0, int32_t max_len)
@@ -918,32 +917,33 @@ __device__ __forceinline__ void store_operand4(_Float16 *Xt, int64_t K, int64_t 
     *reinterpret_cast<h4 *>(Xt + slot * 8 + (k0 & 7)) = h4{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
 }
 
-__global__ void __launch_bounds__(256, 2)
+__global__ void __launch_bounds__(512, 1)
 attn_prefill_kernel(const float *__restrict__ Q, int64_t ldq, const float *__restrict__ Kc,
                     const float *__restrict__ Vc, float *__restrict__ O, int64_t n_q, int32_t n_heads,
                     int32_t n_kv_heads, int32_t start, const int32_t *pos, int32_t max_len, float scale,
-                    float *__restrict__ part_o, float *__restrict__ part_ml, _Float16 *__restrict__ Xt)
+                    _Float16 *__restrict__ Xt)
 {
-    __shared__ __align__(16) _Float16 lds[2 * kKT * kRKH + 2 * kHD * kRVH];   // K hi, K lo, V^T hi, V^T lo
-    __shared__ float tmax[2][4];                                               // [K, V][wave]: the next tile
-    _Float16 *const ksh = lds, *const vsh = lds + 2 * kKT * kRKH;
-    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    // per half: K hi, K lo, V^T hi, V^T lo
+    __shared__ __align__(16) _Float16 lds2[2][2 * kKT * kRKH + 2 * kHD * kRVH];
+    __shared__ float tmax2[2][2][4];   // [half][K, V][wave]: the half's next tile
+    const int tid = threadIdx.x, half = tid >> 8, ht = tid & 255, lane = tid & 63, w = (tid >> 6) & 3;
+    _Float16 *const lds = lds2[half], *const ksh = lds, *const vsh = lds + 2 * kKT * kRKH;
+    float(*const tmax)[4] = tmax2[half];
+    const int h = blockIdx.x;
     const int g = lane >> 4, c = lane & 15;
     const int kvh = h / (n_heads / n_kv_heads);
     const int64_t kv_stride = (int64_t)n_kv_heads * kHD, q_stride = (int64_t)n_heads * kHD;
     const int32_t p0 = dev_pos(start, pos);
-    // blockIdx.y = 2 * rank + part, tiles longest first (two parts per tile
-    // with part_o, else one)
-    const int parts = part_o ? 2 : 1;
-    const int part = (int)blockIdx.y % parts;
-    const int64_t i0 = (int64_t)(gridDim.y / parts - 1 - blockIdx.y / parts) * kQTile;
+    // query tiles longest first
+    const int64_t i0 = (int64_t)(gridDim.y - 1 - blockIdx.y) * kQTile;
     // keys beyond the cache (a position past max_len) are never read
     const int64_t p_last = min<int64_t>(p0 + min<int64_t>(i0 + kQTile, n_q) - 1, (int64_t)max_len - 1);
     const int64_t n_kt = prefill_key_tiles(i0, n_q, p0, max_len);
-    const bool split = part_o && n_kt >= kSplitKT;
-    if (part == 1 && !split) return;
-    const int64_t j_begin = split && part == 1 ? kKT * (n_kt / 2) : 0;
-    const int64_t j_end = split && part == 0 ? kKT * (n_kt / 2) : p_last + 1;
+    // key ranges: half 0 the first n_kt / 2 tiles and half 1 the rest when
+    // the tile spans kSplitKT or more, else half 1 all of them
+    const int64_t mid = n_kt >= kSplitKT ? kKT * (n_kt / 2) : 0;
+    const int64_t j_begin = half ? mid : 0, j_end = half ? p_last + 1 : mid;
+    const int64_t n_iter = (p_last + 1 - mid + kKT - 1) / kKT;   // the longer (second) half's tiles
 
     // Q^T operand: query 16w + c, dims 32s + 8g .. +7, split with the row's
     // power of two (rows past n_q read the last row, never stored)
@@ -980,16 +980,23 @@ attn_prefill_kernel(const float *__restrict__ Q, int64_t ldq, const float *__res
 #pragma unroll
     for (int db = 0; db < 8; ++db) o[db] = f4{0.f, 0.f, 0.f, 0.f};
 
-    // the next tile's rows in registers
+    // the next tile's rows in registers; both halves take n_iter steps (a
+    // half whose range has ended idles through its last ones), so that the
+    // workgroup barriers line up
     KVTile kv;
-    kv.load(Kc, Vc, kv_stride, kvh, j_begin, p_last, tid);
-    kv.wave_max(tmax, lane, w);
-    for (int64_t j0 = j_begin; j0 < j_end; j0 += kKT) {
+    if (j_begin < j_end) {
+        kv.load(Kc, Vc, kv_stride, kvh, j_begin, p_last, ht);
+        kv.wave_max(tmax, lane, w);
+    }
+    for (int64_t it = 0; it < n_iter; ++it) {
+        const int64_t j0 = j_begin + kKT * it;
+        const bool act = j0 < j_end;
         __syncthreads();   // the previous tile is consumed; tmax holds this one's maxima
         const int ek = split_exp_of(tmax, 0), ev = split_exp_of(tmax, 1);
-        kv.split_to_lds(ek, ev, tid, lds);
+        if (act) kv.split_to_lds(ek, ev, ht, lds);
         __syncthreads();
-        if (j0 + kKT < j_end) kv.load(Kc, Vc, kv_stride, kvh, j0 + kKT, p_last, tid);   // the next tile in flight
+        if (!act) continue;
+        if (j0 + kKT < j_end) kv.load(Kc, Vc, kv_stride, kvh, j0 + kKT, p_last, ht);   // the next tile in flight
 
         // S^T = K Q^T, four blocks of 16 keys
         f4 sc[4];
@@ -1060,59 +1067,43 @@ attn_prefill_kernel(const float *__restrict__ Q, int64_t ldq, const float *__res
     // the four lanes of a query hold sums over disjoint keys, all scaled by the same corrections
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
+    // half 1 leaves its unnormalised output and (max, sum) per query in its
+    // LDS (64 rows of 132 floats); half 0 merges:
+    //   O = (2^(m0 - M) o0 + 2^(m1 - M) o1) / (2^(m0 - M) l0 + 2^(m1 - M) l1),  M = max(m0, m1)
+    // (a half with no keys has m = -inf, l = 0, o = 0 and weight 0; half 1
+    // always has keys)
+    const float u = ldexpf(1.f, -A);
+    float *const pub = reinterpret_cast<float *>(lds2[1]) + (16 * w + c) * 132;
+    __syncthreads();
+    if (half == 1) {
+#pragma unroll
+        for (int db = 0; db < 8; ++db) *reinterpret_cast<f4 *>(pub + 16 * db + 4 * g) = o[db] * u;
+        if (g == 0) {
+            pub[128] = m;
+            pub[129] = l;
+        }
+    }
+    __syncthreads();
+    if (half == 1) return;
     const int64_t i = i0 + 16 * w + c;
     if (i < n_q) {
-        const float u = ldexpf(1.f, -A);
-        float *orow = (split && part == 1 ? part_o : O) + i * q_stride + (int64_t)h * kHD + 4 * g;
-        if (split) {
+        const float m1 = pub[128], l1 = pub[129];
+        const float mm = fmaxf(m, m1), a0 = exp2f(m - mm), a1 = exp2f(m1 - mm);
+        const float den = a0 * l + a1 * l1;
 #pragma unroll
-            for (int db = 0; db < 8; ++db) *reinterpret_cast<f4 *>(orow + 16 * db) = o[db] * u;
-            if (g == 0) {
-                float *ml = part_ml + ((int64_t)part * n_heads * n_q + (int64_t)h * n_q + i) * 2;
-                ml[0] = m;
-                ml[1] = l;
-            }
-        } else if (Xt) {
-#pragma unroll
-            for (int db = 0; db < 8; ++db) store_operand4(Xt, q_stride, i, (int64_t)h * kHD + 16 * db + 4 * g, o[db] * u / l);
-        } else {
-#pragma unroll
-            for (int db = 0; db < 8; ++db) *reinterpret_cast<f4 *>(orow + 16 * db) = o[db] * u / l;
+        for (int db = 0; db < 8; ++db) {
+            const f4 r = (a0 * (o[db] * u) + a1 * *reinterpret_cast<const f4 *>(pub + 16 * db + 4 * g)) / den;
+            if (Xt)
+                store_operand4(Xt, q_stride, i, (int64_t)h * kHD + 16 * db + 4 * g, r);
+            else
+                *reinterpret_cast<f4 *>(O + i * q_stride + (int64_t)h * kHD + 16 * db + 4 * g) = r;
         }
-    } else if (Xt && part == 0 && i < (n_q + 31) / 32 * 32) {
+    } else if (Xt && i < (n_q + 31) / 32 * 32) {
         // operand rows past n_q, up to the next multiple of 32, are zero
 #pragma unroll
         for (int db = 0; db < 8; ++db)
             store_operand4(Xt, q_stride, i, (int64_t)h * kHD + 16 * db + 4 * g, f4{0.f, 0.f, 0.f, 0.f});
     }
-}
-
-// The two parts of each split tile: workgroup (h, tile, z) merges rows
-// 8z .. 8z + 7 of query tile `tile` (attn_prefill_kernel's longest-first
-// order; workgroups of other tiles exit), four elements per thread, with the
-// parts' base-2 maxima:
-//   O = (2^(m0 - M) o0 + 2^(m1 - M) o1) / (2^(m0 - M) l0 + 2^(m1 - M) l1),  M = max(m0, m1).
-__global__ void __launch_bounds__(256)
-attn_prefill_merge(float *__restrict__ O, const float *__restrict__ part_o, const float *__restrict__ part_ml,
-                   int64_t n_q, int32_t n_heads, int32_t start, const int32_t *pos, int32_t max_len,
-                   _Float16 *__restrict__ Xt)
-{
-    const int h = blockIdx.x;
-    const int64_t i0 = (int64_t)(gridDim.y - 1 - blockIdx.y) * kQTile;
-    if (prefill_key_tiles(i0, n_q, dev_pos(start, pos), max_len) < kSplitKT) return;
-    const int64_t i = i0 + 8 * blockIdx.z + (threadIdx.x >> 5);
-    if (i >= n_q) return;
-    const int64_t e = i * (int64_t)n_heads * kHD + (int64_t)h * kHD + 4 * (threadIdx.x & 31);
-    const float *ml0 = part_ml + ((int64_t)h * n_q + i) * 2;
-    const float *ml1 = part_ml + ((int64_t)n_heads * n_q + (int64_t)h * n_q + i) * 2;
-    const float m0 = ml0[0], l0 = ml0[1], m1 = ml1[0], l1 = ml1[1];
-    const f4 o0 = *reinterpret_cast<const f4 *>(O + e), o1 = *reinterpret_cast<const f4 *>(part_o + e);
-    const float mm = fmaxf(m0, m1), a0 = exp2f(m0 - mm), a1 = exp2f(m1 - mm);
-    const f4 r = (a0 * o0 + a1 * o1) / (a0 * l0 + a1 * l1);
-    if (Xt)
-        store_operand4(Xt, (int64_t)n_heads * kHD, i, (int64_t)h * kHD + 4 * (threadIdx.x & 31), r);
-    else
-        *reinterpret_cast<f4 *>(O + e) = r;
 }
 
 // ---------------------------------------------------------------- argmax
@@ -1437,34 +1428,15 @@ int aih_add(aih_ctx *ctx, const float *A, const float *B, float *Y, int64_t n)
 }
 
 // The tiled (prefill) attention: the output as fp32 rows in O, or, with Xt,
-// as the fp16 operand image of a GEMM over its n_heads * kHD columns.  Split
-// query tiles stage their halves (and, for Xt, the first half's output) in
-// the context workspace; where it cannot grow (inside a capture) every tile
-// runs whole.
+// as the fp16 operand image of a GEMM over its n_heads * kHD columns.
 static int prefill_attention(aih_ctx *ctx, const float *Q, int64_t ldq, const float *Kc, const float *Vc, float *O,
                              _Float16 *Xt, int64_t n_q, int32_t n_heads, int32_t n_kv_heads, int32_t start,
                              const int32_t *pos, int32_t max_len, float scale)
 {
     const int64_t tiles = (n_q + kQTile - 1) / kQTile;
-    if (2 * tiles > 65535) return AIH_E_LIMIT;
-    const size_t img = (size_t)n_q * (size_t)n_heads * kHD;
-    float *part_o = nullptr, *part_ml = nullptr;
-    {
-        void *work = nullptr;
-        const size_t need = (img * (Xt ? 2 : 1) + (size_t)n_q * n_heads * 4) * sizeof(float);
-        if (aih_stage(ctx, nullptr, need, &work) == AIH_OK) {
-            part_o = static_cast<float *>(work);
-            part_ml = part_o + img;
-            if (Xt) O = part_ml + (size_t)n_q * n_heads * 4;   // the first halves' outputs
-        }
-    }
-    hipLaunchKernelGGL(attn_prefill_kernel, dim3(n_heads, (unsigned)(tiles * (part_o ? 2 : 1))), dim3(256), 0,
-                       ctx->stream, Q, ldq, Kc, Vc, O, n_q, n_heads, n_kv_heads, start, pos, max_len, scale, part_o,
-                       part_ml, Xt);
-    int rc = aih_launch_status();
-    if (rc || !part_o) return rc;
-    hipLaunchKernelGGL(attn_prefill_merge, dim3(n_heads, (unsigned)tiles, kQTile / 8), dim3(256), 0, ctx->stream, O,
-                       part_o, part_ml, n_q, n_heads, start, pos, max_len, Xt);
+    if (tiles > 65535) return AIH_E_LIMIT;
+    hipLaunchKernelGGL(attn_prefill_kernel, dim3(n_heads, (unsigned)tiles), dim3(512), 0, ctx->stream, Q, ldq, Kc,
+                       Vc, O, n_q, n_heads, n_kv_heads, start, pos, max_len, scale, Xt);
     return aih_launch_status();
 }
 

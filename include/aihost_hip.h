@@ -373,10 +373,10 @@ int64_t aih_attention_scratch_floats(int32_t n_heads, int32_t max_len);
  * `scratch` (aih_attention_scratch_floats floats); more rows use a tiled
  * kernel with an online softmax on the fp16 matrix cores, each fp32 operand
  * split into two fp16 halves (22 significant bits, products exact, sums in
- * fp32; normwise error about 1e-7), whose query tiles with long key ranges run
- * as two halves merged afterwards, staged in the context workspace
- * (n_q * n_heads * (head_dim + 4) floats; grown on demand, and where it
- * cannot grow -- inside a capture -- the tiles run whole).  Calls sharing a scratch must not overlap.  Replaces ComputeOps.MultiHeadAttention and FusedMHAGenerate
+ * fp32; normwise error about 1e-7), one workgroup per 64-query tile whose
+ * two halves take the first and last halves of a long key range and merge
+ * in LDS (no workspace).  Calls sharing a scratch must not overlap.
+ * Replaces ComputeOps.MultiHeadAttention and FusedMHAGenerate
  * (ComputeOps.cs:1015-1102, shaders ComputeShaders.cs:656-733), without the
  * latter's 4096-key limit. */
 int aih_attention(aih_ctx *ctx, const float *Q, const float *Kc, const float *Vc, float *O, int64_t n_q,
@@ -400,9 +400,8 @@ int aih_attention_strided(aih_ctx *ctx, const float *Q, int64_t ldq, const float
  * rounded to fp16 as aih_qgemm_fused rounds an fp32 X, so the GEMM that
  * follows gives the bits of aih_attention_strided + aih_qgemm_fused
  * (AIH_PRE_NONE), without the fp32 rows and their conversion pass.  Every
- * n_q uses the tiled kernel (a single row there takes the decode kernel); split
- * query tiles stage in the context workspace (n_q*n_heads*(2*head_dim+4)
- * floats, same rules as aih_attention).  Replaces, for a prompt, the
+ * n_q uses the tiled kernel (a single row there takes the decode kernel).
+ * Replaces, for a prompt, the
  * attention output that feeds the W_o MatMulWeights in
  * ComputeOps.TransformerLayer (ComputeOps.cs:1250-1356). */
 int aih_attention_operand(aih_ctx *ctx, const float *Q, int64_t ldq, const float *Kc, const float *Vc, void *Xt,

@@ -267,11 +267,10 @@ def test_attention_prefill_value_magnitudes(device, bufs):
     assert err.max() < 1e-5, err.max()
 
 
-def test_attention_prefill_without_workspace(device, bufs):
-    # captured on a fresh context, whose workspace cannot grow inside the
-    # capture: the query tiles run whole and split their own K/V tiles (the
-    # path without the shared K/V images); replays of the graph, with eager
-    # calls between them, all within 1e-5 of the oracle
+def test_attention_prefill_captured_on_a_fresh_context(device, bufs):
+    # captured on a fresh context, whose workspace never grew: the tiled
+    # attention needs none; replays of the graph, with eager calls between
+    # them, all within 1e-5 of the oracle
     nh, nkv, n_q, L_cache, start = 32, 8, 300, 640, 40
     q, K, V = rnd(71, n_q, nh * 128), rnd(72, L_cache, nkv * 128), rnd(73, L_cache, nkv * 128)
     Q, KC, VC, O = bufs.up(q), bufs.up(K), bufs.up(V), bufs.empty(q.nbytes)

@@ -19,7 +19,7 @@ AIH_E_NOT_ALLOCATED = -4
 AIH_E_LIMIT = -5
 AIH_E_NO_DEVICE = -6
 AIH_E_SCRATCH = -7
-NOALLOC_SCRATCH_BYTES = 16 << 20      # AIH_NOALLOC_SCRATCH_BYTES
+NOALLOC_SCRATCH_BYTES = (16 << 20) + (64 << 10)   # AIH_NOALLOC_SCRATCH_BYTES
 HIP_ERROR_OUT_OF_MEMORY = 2
 
 F32, Q4_0, Q8_0, Q4_K, Q6_K = 0, 2, 8, 12, 14
@@ -70,6 +70,7 @@ SIGNATURES = {
     "aih_qgemm": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),
     "aih_qgemm_fused": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _vp, _f, _i64, _i, _i, _vp]),
     "aih_matmul_weights_q": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),
+    "aih_operand_bytes": (_i64, [_i64, _i64]),
     "aih_matmul_weights_q_noalloc": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),
     "aih_probe_stream_read": (_i, [_vp, _vp, _u64, _i, _vp]),
     "aih_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _i64, _i64, _f]),
@@ -134,6 +135,16 @@ def lib():
 
 def strerror(status):
     return lib().aih_strerror(int(status)).decode()
+
+
+def operand_bytes(m, k):
+    """Bytes of the fp16 GEMM operand image of an m x k activation matrix
+    (aih_operand_bytes): what AIH_POST_SILU_PAIRS_F16 and
+    aih_attention_operand write and AIH_PRE_F16_OPERAND reads."""
+    n = lib().aih_operand_bytes(int(m), int(k))
+    if n < 0:
+        raise AihError(int(n), "aih_operand_bytes")
+    return n
 
 
 def check(status, what):

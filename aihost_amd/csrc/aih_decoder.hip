@@ -27,6 +27,7 @@
 // formulas round like the reference's (x / rms * w, x1*c - x2*s, ...);
 // attention contracts its dot products with explicit fmaf.
 #include "aih_internal.h"
+#include "aih_operand.h"
 
 namespace {
 
@@ -1086,23 +1087,52 @@ attn_prefill_kernel(const float *__restrict__ Q, int64_t ldq, const float *__res
     __syncthreads();
     if (half == 1) return;
     const int64_t i = i0 + 16 * w + c;
-    if (i < n_q) {
+    f4 r[8];
+    {
         const float m1 = pub[128], l1 = pub[129];
         const float mm = fmaxf(m, m1), a0 = exp2f(m - mm), a1 = exp2f(m1 - mm);
         const float den = a0 * l + a1 * l1;
 #pragma unroll
-        for (int db = 0; db < 8; ++db) {
-            const f4 r = (a0 * (o[db] * u) + a1 * *reinterpret_cast<const f4 *>(pub + 16 * db + 4 * g)) / den;
-            if (Xt)
-                store_operand4(Xt, q_stride, i, (int64_t)h * kHD + 16 * db + 4 * g, r);
-            else
-                *reinterpret_cast<f4 *>(O + i * q_stride + (int64_t)h * kHD + 16 * db + 4 * g) = r;
-        }
-    } else if (Xt && i < (n_q + 31) / 32 * 32) {
-        // operand rows past n_q, up to the next multiple of 32, are zero
-#pragma unroll
         for (int db = 0; db < 8; ++db)
-            store_operand4(Xt, q_stride, i, (int64_t)h * kHD + 16 * db + 4 * g, f4{0.f, 0.f, 0.f, 0.f});
+            r[db] = (a0 * (o[db] * u) + a1 * *reinterpret_cast<const f4 *>(pub + 16 * db + 4 * g)) / den;
+    }
+    if (!Xt) {
+        if (i < n_q)
+#pragma unroll
+            for (int db = 0; db < 8; ++db)
+                *reinterpret_cast<f4 *>(O + i * q_stride + (int64_t)h * kHD + 16 * db + 4 * g) = r[db];
+        return;
+    }
+    // The operand image: block b of this head (columns 32 b .. +31 of the
+    // head, dims 16 db + 4 g with db = 2b, 2b + 1) of row i is held by the
+    // four lanes g of the row; its exponent comes from their maximum
+    // (aih_operand.h).  Rows past n_q, up to the next multiple of 32, are zero.
+    if (i >= n_q)
+#pragma unroll
+        for (int db = 0; db < 8; ++db) r[db] = f4{0.f, 0.f, 0.f, 0.f};
+    int eb[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        float mx = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) mx = fmaxf(mx, fmaxf(fabsf(r[2 * b][q]), fabsf(r[2 * b + 1][q])));
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        eb[b] = aih_operand::block_exp(mx);
+    }
+    const int64_t mpad = aih_operand::mpad_of(n_q);
+    if (i < mpad) {
+#pragma unroll
+        for (int db = 0; db < 8; ++db) {
+            const int e = eb[db >> 1] == aih_operand::kZeroBlock ? 0 : eb[db >> 1];
+            store_operand4(Xt, q_stride, i, (int64_t)h * kHD + 16 * db + 4 * g,
+                           f4{ldexpf(r[db].x, e), ldexpf(r[db].y, e), ldexpf(r[db].z, e), ldexpf(r[db].w, e)});
+        }
+        char *const img = reinterpret_cast<char *>(Xt);
+        const int eg = g == 0 ? eb[0] : g == 1 ? eb[1] : g == 2 ? eb[2] : eb[3];
+        reinterpret_cast<int8_t *>(img + aih_operand::block_exp_offset(mpad, q_stride))[i * (q_stride / 32) + 4 * h + g] =
+            (int8_t)eg;
+        if (h == 0 && g == 0) reinterpret_cast<int32_t *>(img + aih_operand::row_exp_offset(mpad, q_stride))[i] = 0;
     }
 }
 
@@ -1189,29 +1219,49 @@ argmax_kernel(const float *__restrict__ X, int64_t n, int32_t *token, int32_t *p
 
 // ---------------------------------------------------------------- GEMM operand
 // The activation operand of the prefill GEMM computed by the element-wise step
-// before it and written straight in the GEMM's fp16 fragment order
-// (aih_qgemm.hip: the A operand of v_mfma_f32_32x32x16_f16 for rows
-// 32 mb .. +31 and k 16 kk .. +15 is the 1 KB block mb * K/16 + kk, lane
-// l = row % 32 + 32 * (k / 8 % 2) at 16 bytes * l).  One workgroup per row;
-// rows M .. mpad-1 (mpad = M rounded up to 32) are zero.  The arithmetic is
-// that of rmsnorm_kernel, silu_mul_kernel and silu_mul_pairs_kernel, rounded
-// to fp16 as the GEMM's own conversion does, so the operand is the one the
-// separate operator and aih_qgemm would have built.
+// before it and written straight in the GEMM's fp16 fragment-order image
+// (aih_operand.h), with the row's power of two (the row exponent) chosen from
+// the largest magnitude of its values.  One workgroup per row; rows M ..
+// mpad-1 (mpad = M rounded up to 32) are zero.  The arithmetic is that of
+// rmsnorm_kernel, silu_mul_kernel and silu_mul_pairs_kernel, so the operand
+// is the one the separate operator and the GEMM's own conversion
+// (PRE = AIH_PRE_NONE) would have built:
+//   PRE = AIH_PRE_NONE        x = X
 //   PRE = AIH_PRE_RMSNORM     x = (X / sqrt(mean(X^2) + eps)) * X2   (X2: K weights)
 //   PRE = AIH_PRE_SILU_MUL    x = SiLU(X) * X2                        (X2: M x K)
 //   PRE = AIH_PRE_SILU_PAIRS  x[k] = SiLU(X[2k]) * X[2k+1]            (X: M x 2K)
+// Rows of up to 8 * 256 * kRowIt values stay in registers between the maximum
+// and the rounding; longer rows are computed twice.
+constexpr int kRowIt = 8;
+
+template <int NT>
+__device__ __forceinline__ float block_max(float v, float *red)
+{
+    v = wave_max(v);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float t = red[0];
+#pragma unroll
+    for (int i = 1; i < NT / 64; ++i) t = fmaxf(t, red[i]);
+    return t;
+}
+
 template <int PRE>
 __global__ void __launch_bounds__(256)
 x_tile_pre_kernel(const float *__restrict__ X, const float *__restrict__ X2, float eps, int64_t M, int64_t K,
                   _Float16 *__restrict__ Xt)
 {
     typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-    __shared__ float red[4];
+    __shared__ float red[4], redm[4];
     const int64_t m = blockIdx.x;
+    const int64_t mpad = aih_operand::mpad_of(M);
+    int32_t *const E = reinterpret_cast<int32_t *>(reinterpret_cast<char *>(Xt) + aih_operand::row_exp_offset(mpad, K));
     _Float16 *base = Xt + (((m >> 5) * (K / 16)) * 64 + (m & 31)) * 8;
     auto slot = [&](int64_t k) { return reinterpret_cast<h8 *>(base + ((k >> 4) * 64 + ((k >> 3) & 1) * 32) * 8); };
     if (m >= M) {
         for (int64_t k = 8 * (int64_t)threadIdx.x; k < K; k += 8 * 256) *slot(k) = h8{};
+        if (threadIdx.x == 0) E[m] = 0;
         return;
     }
     const f4 *x4 = reinterpret_cast<const f4 *>(X + m * (PRE == AIH_PRE_SILU_PAIRS ? 2 * K : K));
@@ -1225,9 +1275,12 @@ x_tile_pre_kernel(const float *__restrict__ X, const float *__restrict__ X2, flo
         ss = block_sum<256>(ss, red);
         rms = sqrtf(ss / (float)K + eps);
     }
-    for (int64_t k = 8 * (int64_t)threadIdx.x; k < K; k += 8 * 256) {
-        float o[8];
-        if (PRE == AIH_PRE_RMSNORM) {
+    // the 8 values x[k .. k+7]
+    auto values = [&](int64_t k, float *o) {
+        if (PRE == AIH_PRE_NONE) {
+            const f4 a = x4[k / 4], b = x4[k / 4 + 1];
+            o[0] = a.x, o[1] = a.y, o[2] = a.z, o[3] = a.w, o[4] = b.x, o[5] = b.y, o[6] = b.z, o[7] = b.w;
+        } else if (PRE == AIH_PRE_RMSNORM) {
             const f4 *w4 = reinterpret_cast<const f4 *>(X2);
             const f4 v[2] = {x4[k / 4], x4[k / 4 + 1]}, w[2] = {w4[k / 4], w4[k / 4 + 1]};
 #pragma unroll
@@ -1262,10 +1315,45 @@ x_tile_pre_kernel(const float *__restrict__ X, const float *__restrict__ X2, flo
                 o[j] = (g[j] * sig) * u[j];
             }
         }
+    };
+    auto store = [&](int64_t k, const float *o, int e) {
         h8 r;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) r[j] = (_Float16)o[j];
+        for (int j = 0; j < 8; ++j) r[j] = (_Float16)ldexpf(o[j], e);
         *slot(k) = r;
+    };
+    if (K <= 8 * 256 * kRowIt) {
+        float o[kRowIt][8];
+        float mx = 0.f;
+#pragma unroll
+        for (int it = 0; it < kRowIt; ++it) {
+            const int64_t k = 8 * (int64_t)threadIdx.x + 2048 * it;
+            if (k < K) {
+                values(k, o[it]);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(o[it][j]));
+            }
+        }
+        const int e = aih_operand::range_exp(block_max<256>(mx, redm));
+#pragma unroll
+        for (int it = 0; it < kRowIt; ++it) {
+            const int64_t k = 8 * (int64_t)threadIdx.x + 2048 * it;
+            if (k < K) store(k, o[it], e);
+        }
+        if (threadIdx.x == 0) E[m] = e;
+    } else {
+        float o[8], mx = 0.f;
+        for (int64_t k = 8 * (int64_t)threadIdx.x; k < K; k += 8 * 256) {
+            values(k, o);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(o[j]));
+        }
+        const int e = aih_operand::range_exp(block_max<256>(mx, redm));
+        for (int64_t k = 8 * (int64_t)threadIdx.x; k < K; k += 8 * 256) {
+            values(k, o);
+            store(k, o, e);
+        }
+        if (threadIdx.x == 0) E[m] = e;
     }
 }
 
@@ -1312,6 +1400,10 @@ int aih_launch_x_tile_pre(aih_ctx *ctx, int pre, const float *X, const float *X2
     if (mpad > 0x7FFFFFFF) return AIH_E_LIMIT;
     _Float16 *xt = static_cast<_Float16 *>(Xt);
     switch (pre) {
+    case AIH_PRE_NONE:
+        hipLaunchKernelGGL(x_tile_pre_kernel<AIH_PRE_NONE>, dim3((unsigned)mpad), dim3(256), 0, ctx->stream, X, X2,
+                           eps, M, K, xt);
+        break;
     case AIH_PRE_RMSNORM:
         hipLaunchKernelGGL(x_tile_pre_kernel<AIH_PRE_RMSNORM>, dim3((unsigned)mpad), dim3(256), 0, ctx->stream, X, X2,
                            eps, M, K, xt);

@@ -106,14 +106,17 @@ int aih_launch_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K
                      const float *X, int64_t M, float *Y, const aih_scratch *ext = nullptr,
                      bool may_split = false);
 // The prefill GEMM in parts: X (M x K fp32) -> the fp16 fragment-order
-// operand Xt (mpad * K halves, mpad = M rounded up to 32); the same operand
-// computed by a fused element-wise step (AIH_PRE_RMSNORM / SILU_MUL /
-// SILU_PAIRS, aih_decoder.hip); the GEMM from Xt with epilogue `epi`: 0
-// stores Y, 1 adds into Y, 2 writes SiLU of its gate/up column pairs into Y
-// as the fp16 operand image of a GEMM over N/2 columns.
+// operand image Xt with its row exponents (aih_operand.h; mpad = M rounded up
+// to 32); the same operand computed by a fused element-wise step
+// (AIH_PRE_RMSNORM / SILU_MUL / SILU_PAIRS, aih_decoder.hip); the pass that
+// gives every row of an image written in 32-column blocks one exponent; the
+// GEMM from Xt with epilogue `epi`: 0 stores Y, 1 adds into Y, 2 writes SiLU
+// of its gate/up column pairs into Y as the fp16 operand image of a GEMM over
+// N/2 columns.
 int aih_launch_x_tile(aih_ctx *ctx, const float *X, int64_t M, int64_t K, void *Xt);
 int aih_launch_x_tile_pre(aih_ctx *ctx, int pre, const float *X, const float *X2, float eps, int64_t M, int64_t K,
                           void *Xt);
+int aih_launch_operand_fixup(aih_ctx *ctx, void *Xt, int64_t M, int64_t K);
 // may_split: the GEMM may split K over workgroups, with partial sums in the
 // second workspace and a reduction (never with caller-provided staging).
 int aih_launch_qgemm_tiled(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const void *Xt,

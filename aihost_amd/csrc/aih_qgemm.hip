@@ -10,8 +10,9 @@
 // cores (v_mfma_f32_32x32x16_f16, fp32 accumulation).
 //
 // Tiling.  X is first converted to fp16 in the context's workspace, stored in
-// MFMA fragment order (x_tile_kernel here, or the element-wise step before the
-// GEMM writing that order itself: aih_decoder.hip's x_tile_pre_kernel).  A
+// MFMA fragment order with a power of two per row (aih_operand.h; the
+// conversion is aih_decoder.hip's x_tile_pre_kernel, which also computes the
+// element-wise step before the GEMM when there is one).  A
 // workgroup then owns a 128 (M) x 64 (N) tile of Y and walks K in super-steps
 // of 256 elements: four producer waves dequantize W for the next super-step
 // into LDS while four consumer waves multiply the current one, their A
@@ -24,12 +25,16 @@
 //
 // Precision.  Both operands are rounded to fp16 (11-bit significand) and the
 // products accumulate in fp32: normwise error near 3e-4 against the fp32
-// reference.  bf16 operands (8-bit significand) would give about 2.4e-3, more
-// than the 1e-3 the path is held to.  Weights are dequantized in fp32 with the
+// reference.  Each activation row carries a power of two that keeps its
+// largest value inside fp16's range (aih_operand.h), undone exactly in the
+// fp32 epilogue, so that rows above 65504 or far below 1 keep their 11 bits.
+// bf16 operands (8-bit significand) would give about 2.4e-3, more than the
+// 1e-3 the path is held to.  Weights are dequantized in fp32 with the
 // reference's formulas (ComputeOps.cs:1629-1678 for Q4_K, :1735-1774 for Q6_K,
 // the GGUF definitions for Q8_0 and Q4_0), computed as one fused fp32
 // multiply-add per weight with fp16 output (aih_pieces.h).
 #include "aih_pieces.h"
+#include "aih_operand.h"
 
 #include <type_traits>
 
@@ -52,51 +57,27 @@ __device__ __forceinline__ void lds_barrier()
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// X (fp32, M x K) -> fp16, stored in the order the matrix cores read it.
-// The A operand of v_mfma_f32_32x32x16_f16 for rows 32*mb .. +31 and k
-// 16*kk .. +15 holds, in lane l, the 8 halves X[32*mb + l%32][16*kk +
-// 8*(l/32) .. +7]; here that fragment is the 1 KB block (mb*KC + kk) of Xt
-// (KC = K/16), lane l at 16 bytes * l.  A wave then loads a fragment with one
-// fully coalesced 16-byte load per lane, straight into registers.  Rows past
-// M (up to the next multiple of 32) are zero.  One thread per 8 halves.
-__global__ void __launch_bounds__(256)
-x_tile_kernel(const float *__restrict__ X, int64_t M, int64_t K, _Float16 *__restrict__ Xt, int64_t nslots)
-{
-    const int64_t kc = K / 16;
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nslots; i += (int64_t)gridDim.x * 256) {
-        const int l = (int)(i & 63);
-        const int64_t frag = i >> 6;
-        const int64_t mb = frag / kc, kk = frag - mb * kc;
-        const int64_t row = 32 * mb + (l & 31);
-        const int64_t k = 16 * kk + 8 * (l >> 5);
-        h8 v = {};
-        if (row < M) {
-            const f4 a = ldg<f4>(X + row * K + k), b = ldg<f4>(X + row * K + k + 4);
-            const float f[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-            v = pack8(f);
-        }
-        *reinterpret_cast<h8 *>(Xt + 8 * i) = v;
-    }
-}
-
 // Epilogues: 0 store Y, 1 add into Y, 2 the SiLU-pairs operand (below).
 constexpr int kEpiStore = 0, kEpiAccumulate = 1, kEpiSiluOperand = 2;
 
 // SiLU(gate) * up of a wave's 32 x 64 output block whose column pairs
-// (2j, 2j+1) are gate and up rows (W interleaved), written as the fp16 operand
-// of a following GEMM with K = N / 2 in the order x_tile_kernel produces: the
-// 32 x 32 results pass through `lds` (32 rows x 40 halves, private to the
-// wave) so that every lane writes whole 16-byte fragment slots.  Rows at or
-// past M are zero; m0w is the wave's first row, n0 the block's first column.
-// The arithmetic is silu_mul_pairs_kernel's, (g * (1 / (1 + e^-g))) * u in
-// fp32, then rounded to fp16 as the GEMM's conversion rounds that kernel's
-// stored output, so the operand is the same bits.
+// (2j, 2j+1) are gate and up rows (W interleaved), written as the fp16
+// operand image of a following GEMM with K = N / 2 (aih_operand.h).  The
+// wave's block is one 32-column block of that operand, so each of its rows
+// gets its own block exponent; the row exponents are 0, and the image's
+// fixup pass (operand_fixup_kernel) brings every row to one exponent before
+// that GEMM.  The 32 x 32 fp32 results pass through `lds` (32 rows x 36
+// floats, private to the wave) so that every lane writes whole 16-byte
+// fragment slots.  Rows at or past M are zero; m0w is the wave's first row,
+// n0 the block's first column.  The arithmetic is silu_mul_pairs_kernel's,
+// (g * (1 / (1 + e^-g))) * u in fp32, so a row within the unscaled window
+// holds the bits the GEMM's own conversion of that kernel's output gives.
 __device__ __forceinline__ void silu_pairs_operand(const f16v &acc0, const f16v &acc1, int lane, int64_t m0w,
-                                                   int64_t n0, int64_t M, int64_t N, _Float16 *lds,
+                                                   int64_t n0, int64_t M, int64_t N, float *lds,
                                                    _Float16 *__restrict__ out)
 {
     const int fr = lane & 31, hf = lane >> 5;
-    constexpr int LS = 40;
+    constexpr int LS = 36;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         // the up value of this lane's column pair, from the odd neighbour
@@ -105,15 +86,8 @@ __device__ __forceinline__ void silu_pairs_operand(const f16v &acc0, const f16v 
         if ((fr & 1) == 0) {
             const int i = 8 * (r >> 2) + 4 * hf + (r & 3);
             const float g0 = acc0[r], g1 = acc1[r];
-            float y0 = (g0 * (1.0f / (1.0f + expf(-g0)))) * u0;
-            float y1 = (g1 * (1.0f / (1.0f + expf(-g1)))) * u1;
-            // round to fp32 first, as the separate operator's stored result is:
-            // the empty asm keeps the compiler from folding the last multiply
-            // and the conversion into one mixed-precision instruction (a single
-            // rounding straight to fp16)
-            asm("" : "+v"(y0), "+v"(y1));
-            lds[i * LS + (fr >> 1)] = (_Float16)y0;
-            lds[i * LS + 16 + (fr >> 1)] = (_Float16)y1;
+            lds[i * LS + (fr >> 1)] = (g0 * (1.0f / (1.0f + expf(-g0)))) * u0;
+            lds[i * LS + 16 + (fr >> 1)] = (g1 * (1.0f / (1.0f + expf(-g1)))) * u1;
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -121,15 +95,52 @@ __device__ __forceinline__ void silu_pairs_operand(const f16v &acc0, const f16v 
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // lane: row fr of the block, outputs 16 hf .. 16 hf + 15 (two slots)
     const int64_t m = m0w + fr;
-    const int64_t mpad = (M + 31) / 32 * 32;
-    if (m >= mpad) return;
-    const int64_t kd = N / 2, kc = kd / 16;
+    const int64_t mpad = aih_operand::mpad_of(M);
+    if (m >= mpad) return;   // both lanes of a row (fr, fr + 32) alike
+    f4 v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        v[q] = m < M ? *reinterpret_cast<const f4 *>(&lds[fr * LS + 16 * hf + 4 * q]) : f4{0.f, 0.f, 0.f, 0.f};
+    float mx = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[q].x), fabsf(v[q].y)), fmaxf(fabsf(v[q].z), fabsf(v[q].w))));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const int eb = aih_operand::block_exp(mx), e = eb == aih_operand::kZeroBlock ? 0 : eb;
+    const int64_t kd = N / 2;
     const int64_t k0 = n0 / 2 + 16 * hf;
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-        h8 v = m < M ? *reinterpret_cast<const h8 *>(&lds[fr * LS + 16 * hf + 8 * q]) : h8{};
-        const int64_t k = k0 + 8 * q;
-        *reinterpret_cast<h8 *>(out + (((m >> 5) * kc + (k >> 4)) * 64 + (m & 31) + 32 * ((k >> 3) & 1)) * 8) = v;
+        h8 h;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) h[j] = (_Float16)ldexpf(v[2 * q + j / 4][j % 4], e);
+        *reinterpret_cast<h8 *>(out + aih_operand::slot_half(m, k0 + 8 * q, kd)) = h;
+    }
+    char *const img = reinterpret_cast<char *>(out);
+    if (hf == 0) {
+        reinterpret_cast<int8_t *>(img + aih_operand::block_exp_offset(mpad, kd))[m * (kd / 32) + n0 / 64] = (int8_t)eb;
+        if (n0 == 0) reinterpret_cast<int32_t *>(img + aih_operand::row_exp_offset(mpad, kd))[m] = 0;
+    }
+}
+
+// The row exponents of the operand (aih_operand.h) undone in a wave's 32 x 32
+// accumulator: lane l holds rows 8 (r / 4) + 4 (l / 32) + r % 4 of the
+// wave's 32 rows from row mrow0, whose exponents start at E + mrow0.  `ev`,
+// loaded when the kernel started, is lane l's row l % 32 exponent: when all
+// are zero (rows within the unscaled window) nothing is done.
+typedef int32_t i4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void undo_row_exp(f16v &acc0, f16v &acc1, int32_t ev, const int32_t *E, int64_t mrow0,
+                                             int lane)
+{
+    if (__builtin_amdgcn_ballot_w64(ev != 0) == 0) return;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const i4 e = *reinterpret_cast<const i4 *>(E + mrow0 + 8 * q + 4 * (lane >> 5));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            acc0[4 * q + j] = ldexpf(acc0[4 * q + j], -e[j]);
+            acc1[4 * q + j] = ldexpf(acc1[4 * q + j], -e[j]);
+        }
     }
 }
 
@@ -236,6 +247,9 @@ qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
     int64_t mb = (m0 + 32 * wave) / 32;
     mb = mb < mblocks ? mb : mblocks - 1;
     const _Float16 *xa = Xt + (mb * kc * 64 + lane) * 8;
+    // the row exponents of the operand, after its mblocks * 32 rows of values
+    const int32_t *const E = reinterpret_cast<const int32_t *>(Xt + mblocks * 32 * K);
+    const int32_t ev = E[mb * 32 + (lane & 31)];
     struct AF { h8 a[4]; };
     auto aload = [&](int kb, AF &f) {
         kb = kb < nch ? kb : nch - 1;
@@ -291,9 +305,11 @@ qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
         }
     }
 
+    undo_row_exp(acc0, acc1, ev, E, mb * 32, lane);
     if (epi == kEpiSiluOperand) {
         // the tile buffer of super-step nss: nothing reads or writes it any more
-        silu_pairs_operand(acc0, acc1, lane, m0 + 32 * wave, n0, M, N, &wsh[nss & 1][0][0] + wave * 32 * 40,
+        silu_pairs_operand(acc0, acc1, lane, m0 + 32 * wave, n0, M, N,
+                           reinterpret_cast<float *>(&wsh[nss & 1][0][0]) + wave * 32 * 36,
                            reinterpret_cast<_Float16 *>(Y));
         return;
     }
@@ -370,11 +386,14 @@ qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
     const int fr = lane & 31, fk = 8 * (lane >> 5);
     const int64_t kc = K / 16, mblocks = (M + 31) / 32;
     const _Float16 *xa[MB];
+    const int32_t *const E = reinterpret_cast<const int32_t *>(Xt + mblocks * 32 * K);
+    int32_t ev[MB];   // the row exponents of the operand (lane: row lane % 32 of fragment j)
 #pragma unroll
     for (int j = 0; j < MB; ++j) {
         int64_t mb = (m0 + 32 * (MB * wave + j)) / 32;
         mb = mb < mblocks ? mb : mblocks - 1;
         xa[j] = Xt + (mb * kc * 64 + lane) * 8;
+        ev[j] = E[mb * 32 + (lane & 31)];
     }
     struct AF { h8 a[MB][4]; };
     auto aload = [&](int kb, AF &f) {
@@ -463,12 +482,19 @@ qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
         if (it < nss) body(std::true_type{}, it, ring[(j + 1) % PR], it + 1 < nss, it + 1 + PR < nss);
     }
 
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+        int64_t mb = (m0 + 32 * (MB * wave + j)) / 32;
+        mb = mb < mblocks ? mb : mblocks - 1;
+        undo_row_exp(acc[j][0], acc[j][1], ev[j], E, mb * 32, lane);
+    }
     if (epi == kEpiSiluOperand) {
         // after the last barrier the tile buffers are free
 #pragma unroll
         for (int j = 0; j < MB; ++j) {
             silu_pairs_operand(acc[j][0], acc[j][1], lane, m0 + 32 * (MB * wave + j), n0, M, N,
-                               &wsh[0][0][0] + wave * 32 * 40, reinterpret_cast<_Float16 *>(Y));
+                               reinterpret_cast<float *>(&wsh[0][0][0]) + wave * 32 * 36,
+                               reinterpret_cast<_Float16 *>(Y));
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");   // the block is read before it is rewritten
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -507,6 +533,53 @@ split_k_sum_kernel(const float *__restrict__ P, int S, int64_t MN, float *__rest
         f4 *y = reinterpret_cast<f4 *>(Y + i);
         *y = accumulate ? *y + s : s;
     }
+}
+
+// Before a GEMM reads an image written one 32-column block at a time
+// (aih_operand.h), every row is brought to one exponent: one wave per row.
+// A row whose block exponents are all 0 (or mark all-zero blocks) -- its
+// values within the unscaled window -- is left as it is.  Otherwise each
+// block of exponent d is scaled to the row's smallest exponent D (the block
+// of its largest values): every half multiplied by 2^(D - d) <= 1 in fp32
+// (exact) and rounded to fp16 once; then E[m] += D and the block exponents
+// become 0, so a second pass changes nothing.
+__global__ void __launch_bounds__(256)
+operand_fixup_kernel(_Float16 *__restrict__ Xt, int64_t mpad, int64_t K)
+{
+    const int lane = threadIdx.x & 63;
+    const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (m >= mpad) return;
+    const int64_t nb = K / 32;
+    char *const img = reinterpret_cast<char *>(Xt);
+    int8_t *const d = reinterpret_cast<int8_t *>(img + aih_operand::block_exp_offset(mpad, K)) + m * nb;
+    int mn = 127;
+    bool odd = false;
+    for (int64_t b = lane; b < nb; b += 64) {
+        const int v = d[b];
+        if (v != aih_operand::kZeroBlock) {
+            mn = min(mn, v);
+            odd = odd || v != 0;
+        }
+    }
+    if (__builtin_amdgcn_ballot_w64(odd) == 0) return;
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) mn = min(mn, __shfl_xor(mn, s));
+    for (int64_t b = lane; b < nb; b += 64) {
+        const int v = d[b];
+        if (v != aih_operand::kZeroBlock && v != mn) {
+            const float f = ldexpf(1.f, mn - v);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                h8 *const p = reinterpret_cast<h8 *>(Xt + aih_operand::slot_half(m, 32 * b + 8 * q, K));
+                h8 h = *p;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) h[j] = (_Float16)((float)h[j] * f);
+                *p = h;
+            }
+        }
+        d[b] = 0;
+    }
+    if (lane == 0) reinterpret_cast<int32_t *>(img + aih_operand::row_exp_offset(mpad, K))[m] += mn;
 }
 
 template <class T>
@@ -588,12 +661,14 @@ int aih_launch_qgemm_tiled(aih_ctx *ctx, int type, const void *W, int64_t N, int
 
 int aih_launch_x_tile(aih_ctx *ctx, const float *X, int64_t M, int64_t K, void *Xt)
 {
-    const int64_t mpad = (M + 31) / 32 * 32;
-    const int64_t nslots = mpad * K / 8;
-    const int64_t blocks = (nslots + 255) / 256;
-    const unsigned grid = (unsigned)(blocks < 8192 ? blocks : 8192);
-    hipLaunchKernelGGL(x_tile_kernel, dim3(grid), dim3(256), 0, ctx->stream, X, M, K, static_cast<_Float16 *>(Xt),
-                       nslots);
+    return aih_launch_x_tile_pre(ctx, AIH_PRE_NONE, X, nullptr, 0.f, M, K, Xt);
+}
+
+int aih_launch_operand_fixup(aih_ctx *ctx, void *Xt, int64_t M, int64_t K)
+{
+    const int64_t mpad = aih_operand::mpad_of(M);
+    hipLaunchKernelGGL(operand_fixup_kernel, dim3((unsigned)((mpad + 3) / 4)), dim3(256), 0, ctx->stream,
+                       static_cast<_Float16 *>(Xt), mpad, K);
     return aih_launch_status();
 }
 
@@ -603,9 +678,8 @@ int aih_launch_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K
     // K advances in 64-element steps.
     if (K % BK != 0) return AIH_E_LIMIT;
     if ((reinterpret_cast<uintptr_t>(X) & 15) != 0) return AIH_E_INVALID;
-    const int64_t mpad = (M + 31) / 32 * 32;
     void *work = nullptr;
-    int rc = aih_stage(ctx, ext, (size_t)mpad * (size_t)K * sizeof(_Float16), &work);
+    int rc = aih_stage(ctx, ext, (size_t)aih_operand::image_bytes(aih_operand::mpad_of(M), K, false), &work);
     if (rc) return rc;
     rc = aih_launch_x_tile(ctx, X, M, K, work);
     if (rc) return rc;

@@ -2,6 +2,7 @@
 // libaihost_hip.so.  This is the HIP device that replaces the reference's ROCm
 // backend (AIHost/AIHost/ICompute/ROCm/*.cs) for the quantized-matmul path.
 #include "aih_internal.h"
+#include "aih_operand.h"
 
 #include <cstring>
 #include <cstdio>
@@ -564,15 +565,28 @@ int aih_qgemm_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
     int rc = select_device(ctx);
     if (rc) return rc;
     const int epi = post == AIH_POST_ACCUMULATE ? 1 : post == AIH_POST_SILU_PAIRS_F16 ? 2 : 0;
-    if (pre == AIH_PRE_F16_OPERAND) return aih_launch_qgemm_tiled(ctx, type, W, N, K, X, M, Y, epi, true);
-    const int64_t mpad = (M + 31) / 32 * 32;
+    if (pre == AIH_PRE_F16_OPERAND) {
+        // an image written in 32-column blocks: one exponent per row first
+        void *img = const_cast<float *>(X);
+        rc = aih_launch_operand_fixup(ctx, img, M, K);
+        if (rc) return rc;
+        return aih_launch_qgemm_tiled(ctx, type, W, N, K, img, M, Y, epi, true);
+    }
     void *work = nullptr;
-    rc = aih_stage(ctx, nullptr, (size_t)mpad * (size_t)K * 2, &work);
+    rc = aih_stage(ctx, nullptr, (size_t)aih_operand::image_bytes(aih_operand::mpad_of(M), K, false), &work);
     if (rc) return rc;
     rc = pre == AIH_PRE_NONE ? aih_launch_x_tile(ctx, X, M, K, work)
                              : aih_launch_x_tile_pre(ctx, pre, X, X2, eps, M, K, work);
     if (rc) return rc;
     return aih_launch_qgemm_tiled(ctx, type, W, N, K, work, M, Y, epi, true);
+}
+
+int64_t aih_operand_bytes(int64_t M, int64_t K)
+{
+    if (M < 0 || K <= 0 || K % 64) return AIH_E_INVALID;
+    const int64_t mpad = aih_operand::mpad_of(M);
+    if (mpad > (INT64_MAX / 4) / (K + 2)) return AIH_E_LIMIT;
+    return aih_operand::image_bytes(mpad, K, true);
 }
 
 int aih_matmul_weights_q_noalloc(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,

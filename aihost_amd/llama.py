@@ -229,9 +229,11 @@ class LlamaDecoder:
         self.k, self.v = buf(P * c.kv_dim * 4), buf(P * c.kv_dim * 4)
         # prefill: gate and up (interleaved with a fused gate|up buffer), then
         # SiLU(gate) * up in self.up
-        self.gate, self.up = buf(P * 2 * c.ffn * 4), buf(P * c.ffn * 4)
-        # the attention output as the W_o GEMM's fp16 operand (fused prefill)
-        self.att16 = buf((P + 31) // 32 * 32 * c.n_heads * c.head_dim * 2)
+        # (the fused prefill keeps the down GEMM's operand image in self.gate)
+        self.gate = buf(max(P * 2 * c.ffn * 4, nat.operand_bytes(P, c.ffn)))
+        self.up = buf(P * c.ffn * 4)
+        # the attention output as the W_o GEMM's fp16 operand image (fused prefill)
+        self.att16 = buf(nat.operand_bytes(P, qd))
         # outputs of the fused Q|K|V projection (one row in decode, up to
         # max_prefill rows in the fused prefill) and of the decode gate|up
         # (SiLU-pairs) matvec

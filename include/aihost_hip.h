@@ -221,22 +221,28 @@ int aih_qmatvec(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
 /* aih_qgemm_fused only:  x[k] = SiLU(X[2k]) * X[2k+1]  (X rows of 2K floats:
  * the output of a GEMM over gate/up rows interleaved; X2 unused). */
 #define AIH_PRE_SILU_PAIRS  3
-/* aih_qgemm_fused only: X is the GEMM's fp16 operand image of M rows, as
- * AIH_POST_SILU_PAIRS_F16 writes it (X2 unused). */
+/* aih_qgemm_fused only: X is a GEMM operand image of M rows and K columns
+ * (aih_operand_bytes(M, K) bytes), as AIH_POST_SILU_PAIRS_F16 or
+ * aih_attention_operand writes it (X2 unused).  The call first gives every
+ * row of the image one power-of-two exponent, rewriting it in place; the
+ * values it holds do not change. */
 #define AIH_PRE_F16_OPERAND 4
 /* aih_qgemm_fused only: SiLU(y[m, 2i]) * y[m, 2i+1] (W holds gate and up rows
- * interleaved, N a multiple of 128), rounded to fp16 and stored in Y as the
- * fp16 operand image of a GEMM over those N/2 columns (mpad * N bytes, mpad =
- * M rounded up to 32), for a following aih_qgemm_fused with
- * pre = AIH_PRE_F16_OPERAND and K = N/2. */
+ * interleaved, N a multiple of 128), stored in Y as the operand image of a
+ * GEMM over those N/2 columns (aih_operand_bytes(M, N/2) bytes), for a
+ * following aih_qgemm_fused with pre = AIH_PRE_F16_OPERAND and K = N/2. */
 #define AIH_POST_SILU_PAIRS_F16 3
 int aih_qmatvec_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *X,
                       const float *X2, float eps, int pre, int post, float *Y);
 
 /* Prefill GEMM, dequantization fused:  Y[m*N + n] = sum_k X[m*K + k] * W[n, k].
- * X is converted once to fp16 in a context workspace (M*K*2 bytes, grown on
- * demand and kept until aih_destroy); tiles of W are dequantized into LDS as
- * fp16 and contracted on MFMA with fp32 accumulation.  K must be a multiple
+ * X is converted once to fp16 in a context workspace (about M*K*2 bytes,
+ * grown on demand and kept until aih_destroy), each row scaled by a power of
+ * two that keeps its largest value within fp16's range (rows whose largest
+ * magnitude lies in [2^-12, 2^15) are not scaled; the power of two is undone
+ * exactly in the fp32 result, so any finite fp32 row keeps 11 significant
+ * bits per value); tiles of W are dequantized into LDS as fp16 and contracted
+ * on MFMA with fp32 accumulation.  K must be a multiple
  * of 64 (else AIH_E_LIMIT) and X 16-byte aligned.  The workspace cannot grow
  * while the stream is being captured (AIH_E_LIMIT): run the largest GEMM once
  * before capturing.  A workspace replaced by a larger one stays allocated
@@ -284,12 +290,21 @@ int aih_matmul_weights_q(aih_ctx *ctx, int type, const void *W, int64_t N, int64
 int aih_qgemm_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *X,
                     const float *X2, float eps, int64_t M, int pre, int post, float *Y);
 
+/* Bytes of the fp16 operand image of an M x K activation matrix (K a
+ * multiple of 64) that AIH_POST_SILU_PAIRS_F16 and aih_attention_operand
+ * write and AIH_PRE_F16_OPERAND reads: the values in the matrix cores'
+ * fragment order, one power-of-two exponent per row and one per 32-column
+ * block of a row (the scaling that keeps every finite fp32 value within
+ * fp16's range).  A negative status for invalid sizes.  No counterpart in the
+ * reference (its activations stay fp32); needs no context and no device. */
+int64_t aih_operand_bytes(int64_t M, int64_t K);
+
 /* aih_matmul_weights_q without any allocation.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory -- code
  * being captured into a HIP graph, tight serving loops, harnesses that forbid
  * hipMalloc.  Same arguments, routing, kernels and results as
  * aih_matmul_weights_q; the staging memory those kernels need (the partial
- * sums of the 3..8-column matvec, the GEMM's fp16 copy of X: mpad * K * 2
+ * sums of the 3..8-column matvec, the GEMM's fp16 copy of X: mpad * (2K + 4)
  * bytes, mpad = M rounded up to 32) comes from one static device buffer of
  * AIH_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends, instead of
  * the context workspace.  A call that needs more returns AIH_E_SCRATCH
@@ -297,7 +312,7 @@ int aih_qgemm_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
  * K = 14336, up to 576).  Every call on one GPU shares that buffer: calls
  * that overlap on one GPU (two streams, two contexts, two threads) race and
  * must be serialized by the caller.  Nothing in it has to start at zero. */
-#define AIH_NOALLOC_SCRATCH_BYTES (16u << 20)
+#define AIH_NOALLOC_SCRATCH_BYTES ((16u << 20) + (64u << 10))
 int aih_matmul_weights_q_noalloc(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
                                  const float *X, int64_t M, float *Y);
 
@@ -393,13 +408,16 @@ int aih_attention_strided(aih_ctx *ctx, const float *Q, int64_t ldq, const float
                           int64_t scratch_floats);
 
 /* aih_attention_strided writing its output, instead of as fp32 rows, as the
- * fp16 operand image of a GEMM over its n_heads*head_dim columns: the X of
- * aih_qgemm_fused with AIH_PRE_F16_OPERAND (mpad = n_q rounded up to 32
- * rows, rows past n_q zero; mpad*n_heads*head_dim*2 bytes, 16-byte aligned).
- * For n_q > 1 the values are the ones aih_attention_strided computes,
- * rounded to fp16 as aih_qgemm_fused rounds an fp32 X, so the GEMM that
- * follows gives the bits of aih_attention_strided + aih_qgemm_fused
- * (AIH_PRE_NONE), without the fp32 rows and their conversion pass.  Every
+ * operand image of a GEMM over its n_heads*head_dim columns: the X of
+ * aih_qgemm_fused with AIH_PRE_F16_OPERAND (aih_operand_bytes(n_q,
+ * n_heads*head_dim) bytes, 16-byte aligned; rows past n_q, up to the next
+ * multiple of 32, zero).  For n_q > 1 the values are the ones
+ * aih_attention_strided computes, rounded to fp16 with a power of two per
+ * 32-column block of a row (the same rounding as aih_qgemm_fused's
+ * conversion of an fp32 X wherever both leave a value a normal fp16 number),
+ * so the GEMM that follows gives the bits of aih_attention_strided +
+ * aih_qgemm_fused (AIH_PRE_NONE) there, without the fp32 rows and their
+ * conversion pass.  Every
  * n_q uses the tiled kernel (a single row there takes the decode kernel).
  * Replaces, for a prompt, the
  * attention output that feeds the W_o MatMulWeights in

@@ -249,7 +249,10 @@ def test_attention_operand_equals_fp32_output_rounded(device, n_q, start):
     w = synth_weight(nat.Q4_K, n_out, qd, seed=5)
     bufs = [upload(device, a) for a in (qkv, kc, vc, w)]
     o = device.create_buffer(n_q * qd * 4)
-    xt = upload(device, np.full(mpad * qd, np.float16(np.nan)))   # every half must be written
+    # every half of the values must be written; the exponents follow them
+    raw = np.zeros(nat.operand_bytes(n_q, qd), np.uint8)
+    raw[:2 * mpad * qd].view(np.float16)[:] = np.float16(np.nan)
+    xt = upload(device, raw)
     y1, y2 = device.create_buffer(n_q * n_out * 4), device.create_buffer(n_q * n_out * 4)
     sf = int(L.aih_attention_scratch_floats(n_heads, max_len))
     sb = device.create_buffer(sf * 4)
@@ -265,6 +268,13 @@ def test_attention_operand_equals_fp32_output_rounded(device, n_q, start):
         nat.check(L.aih_memcpy_d2h(h, img.ctypes.data, xt.get_pointer(), img.nbytes), "d2h")
         assert np.isfinite(out).all()
         assert np.array_equal(img.view(np.uint16), _operand_image(out, mpad).view(np.uint16))
+        # rows and blocks of these values need no scaling: exponents 0, and
+        # the all-zero blocks of the rows past n_q marked -128
+        ex = np.empty(4 * mpad + mpad * qd // 32, np.uint8)
+        nat.check(L.aih_memcpy_d2h(h, ex.ctypes.data, xt.get_pointer() + 2 * mpad * qd, ex.nbytes), "d2h")
+        assert np.array_equal(ex[:4 * mpad].view(np.int32), np.zeros(mpad, np.int32))
+        blocks = ex[4 * mpad:].view(np.int8).reshape(mpad, qd // 32)
+        assert np.all(blocks[:n_q] == 0) and np.all(blocks[n_q:] == -128)
         _check(L.aih_qgemm_fused(h, nat.Q4_K, wb.get_pointer(), n_out, qd, o.get_pointer(), None, EPS, n_q,
                                  nat.PRE_NONE, nat.POST_STORE, y1.get_pointer()), "fp32 X")
         _check(L.aih_qgemm_fused(h, nat.Q4_K, wb.get_pointer(), n_out, qd, xt.get_pointer(), None, EPS, n_q,

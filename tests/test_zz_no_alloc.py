@@ -73,9 +73,10 @@ def test_noalloc_refuses_more_than_its_buffer(device):
     xb = upload(device, C.fill_normal(35, 1024 * k, 0.0, 1.0))
     yb = device.create_buffer(1024 * n * 4)
     try:
-        # the GEMM's fp16 X copy is mpad * K * 2 bytes (mpad = M rounded up to 32)
+        # the GEMM's fp16 X copy with its row exponents is mpad * (2 K + 4)
+        # bytes (mpad = M rounded up to 32)
         for m in (577, 1024):
-            assert (m + 31) // 32 * 32 * k * 2 > nat.NOALLOC_SCRATCH_BYTES
+            assert (m + 31) // 32 * 32 * (2 * k + 4) > nat.NOALLOC_SCRATCH_BYTES
             st, y = run(device, "aih_matmul_weights_q_noalloc", nat.Q4_K, wb, n, k, xb, m, yb)
             assert st == nat.AIH_E_SCRATCH, nat.strerror(st)
             assert np.all(np.isnan(y))                  # nothing ran

@@ -71,6 +71,7 @@ SIGNATURES = {
     "aih_qgemm_fused": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _vp, _f, _i64, _i, _i, _vp]),
     "aih_matmul_weights_q": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),
     "aih_operand_bytes": (_i64, [_i64, _i64]),
+    "aih_qgemm_plan": (_i, [_vp, _i64, _i64, _i64, _i, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)]),
     "aih_matmul_weights_q_noalloc": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),
     "aih_probe_stream_read": (_i, [_vp, _vp, _u64, _i, _vp]),
     "aih_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _i64, _i64, _f]),
@@ -82,6 +83,8 @@ SIGNATURES = {
     "aih_store_rows": (_i, [_vp, _vp, _i64, _i64, _vp, _i64, ctypes.c_int32, _vp]),
     "aih_silu_mul": (_i, [_vp, _vp, _vp, _vp, _i64]),
     "aih_silu_mul_pairs": (_i, [_vp, _vp, _vp, _i64, _i64]),
+    "aih_silu": (_i, [_vp, _vp, _vp, _i64]),
+    "aih_mul": (_i, [_vp, _vp, _vp, _vp, _i64]),
     "aih_add": (_i, [_vp, _vp, _vp, _vp, _i64]),
     "aih_attention_scratch_floats": (_i64, [ctypes.c_int32, ctypes.c_int32]),
     "aih_attention": (_i, [_vp, _vp, _vp, _vp, _vp, _i64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
@@ -145,6 +148,15 @@ def operand_bytes(m, k):
     if n < 0:
         raise AihError(int(n), "aih_operand_bytes")
     return n
+
+
+def qgemm_plan(handle, n, k, m, may_split=True):
+    """(tile rows, K splits) that the GEMM takes for an m x k by n product on
+    the context's device (aih_qgemm_plan)."""
+    t, s = ctypes.c_int32(), ctypes.c_int32()
+    check(lib().aih_qgemm_plan(handle, int(n), int(k), int(m), int(bool(may_split)), ctypes.byref(t),
+                               ctypes.byref(s)), "aih_qgemm_plan")
+    return t.value, s.value
 
 
 def check(status, what):

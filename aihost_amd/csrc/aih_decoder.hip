@@ -322,6 +322,37 @@ add_kernel(const float *A, const float *B, float *Y, int64_t n)
         Y[i] = A[i] + B[i];
 }
 
+// The two halves of silu_mul_kernel as the reference's separate operators:
+// SiLU in place (Y may alias X) and the element-wise product.
+__global__ void __launch_bounds__(256)
+silu_kernel(const float *X, float *Y, int64_t n)
+{
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const float x = X[i];
+        Y[i] = x * (1.0f / (1.0f + expf(-x)));
+    }
+}
+
+__global__ void __launch_bounds__(256)
+mul_kernel(const float *A, const float *B, float *Y, int64_t n)
+{
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        Y[i] = A[i] * B[i];
+}
+
+// Rows of an fp32 embedding table by device token ids (zeros for an id
+// outside [0, vocab)).
+__global__ void __launch_bounds__(256)
+embed_f32_kernel(const float *__restrict__ T, int64_t vocab, int64_t dim, const int32_t *__restrict__ ids, int64_t n,
+                 float *__restrict__ Y)
+{
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n * dim; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / dim, c = i - r * dim;
+        const int32_t id = ids[r];
+        Y[i] = id >= 0 && id < vocab ? T[(int64_t)id * dim + c] : 0.f;
+    }
+}
+
 // ---------------------------------------------------------------- attention
 // Query row i (position p_i = p0 + i) of head h attends to cache rows
 // 0..p_i of KV head h / (n_heads / n_kv_heads):
@@ -1511,6 +1542,22 @@ int aih_silu_mul_pairs(aih_ctx *ctx, const float *X, float *Y, int64_t rows, int
     return aih_launch_status();
 }
 
+int aih_silu(aih_ctx *ctx, const float *X, float *Y, int64_t n)
+{
+    if (!ctx || !X || !Y || n < 0) return AIH_E_INVALID;
+    if (n == 0) return AIH_OK;
+    hipLaunchKernelGGL(silu_kernel, dim3(grid_for(ctx, n)), dim3(256), 0, ctx->stream, X, Y, n);
+    return aih_launch_status();
+}
+
+int aih_mul(aih_ctx *ctx, const float *A, const float *B, float *Y, int64_t n)
+{
+    if (!ctx || !A || !B || !Y || n < 0) return AIH_E_INVALID;
+    if (n == 0) return AIH_OK;
+    hipLaunchKernelGGL(mul_kernel, dim3(grid_for(ctx, n)), dim3(256), 0, ctx->stream, A, B, Y, n);
+    return aih_launch_status();
+}
+
 int aih_add(aih_ctx *ctx, const float *A, const float *B, float *Y, int64_t n)
 {
     if (!ctx || !A || !B || !Y || n < 0) return AIH_E_INVALID;
@@ -1623,6 +1670,12 @@ int aih_embed_q(aih_ctx *ctx, int type, const void *table, int64_t vocab, int64_
                 float *Y)
 {
     if (!ctx || !table || !ids || !Y || vocab <= 0 || dim <= 0 || n < 0) return AIH_E_INVALID;
+    if (type == AIH_TYPE_F32) {
+        if (n == 0) return AIH_OK;
+        hipLaunchKernelGGL(embed_f32_kernel, dim3(grid_for(ctx, n * dim)), dim3(256), 0, ctx->stream,
+                           static_cast<const float *>(table), vocab, dim, ids, n, Y);
+        return aih_launch_status();
+    }
     const aih_block_geom g = aih_geom(type);
     if (!aih_is_quant(type)) return AIH_E_UNSUPPORTED;
     if (dim % g.elems) return AIH_E_INVALID;

@@ -523,15 +523,22 @@ qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
 
 // The splits of a GEMM split over K: Y = P_0 + P_1 + ... (in that order),
 // added into Y (Y + sum, the order of the accumulate epilogue) when
-// `accumulate`.  Four elements per thread.
+// `accumulate`.  Four elements per thread (16-byte accesses of Y when it is
+// 16-byte aligned).
+template <bool VEC>
 __global__ void __launch_bounds__(256)
 split_k_sum_kernel(const float *__restrict__ P, int S, int64_t MN, float *__restrict__ Y, int accumulate)
 {
     for (int64_t i = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x); i < MN; i += 4 * (int64_t)gridDim.x * 256) {
         f4 s = *reinterpret_cast<const f4 *>(P + i);
         for (int z = 1; z < S; ++z) s += *reinterpret_cast<const f4 *>(P + (int64_t)z * MN + i);
-        f4 *y = reinterpret_cast<f4 *>(Y + i);
-        *y = accumulate ? *y + s : s;
+        if (VEC) {
+            f4 *y = reinterpret_cast<f4 *>(Y + i);
+            *y = accumulate ? *y + s : s;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) Y[i + j] = accumulate ? Y[i + j] + s[j] : s[j];
+        }
     }
 }
 
@@ -582,59 +589,93 @@ operand_fixup_kernel(_Float16 *__restrict__ Xt, int64_t mpad, int64_t K)
     if (lane == 0) reinterpret_cast<int32_t *>(img + aih_operand::row_exp_offset(mpad, K))[m] += mn;
 }
 
+// The tiling of a GEMM: rows per workgroup tile (128, 256 or 512) and, for
+// 512-row tiles, the number of K splits (splits > 1: partial sums in the
+// second workspace, then split_k_sum_kernel) of ssper super-steps each.
+struct GemmPlan {
+    int tile = 128;
+    int splits = 1;
+    int ssper = 0;
+};
+
+// 256-row tiles halve the dequantization per output and 512-row tiles halve
+// it again; a workgroup of them takes about 1.25 and 2.35 times as long as
+// one of 128 rows (measured on MI355X).  The shape with the fewest such
+// rounds of workgroups over the device's CUs wins (ties to the smaller tile).
+// Costs in units of 1/20 of a 128-row workgroup.  Products of more than 256
+// rows whose 512-row tiles leave CUs idle split K over workgroups: S splits
+// of at least two whole super-steps, partial sums in the second workspace,
+// then a summing pass (estimated at 5 TB/s over the partials, Y and the
+// output, plus 2 us of launch; a 128-row workgroup takes about 29 us per
+// 4096 of K).  The plan depends only on the shape, the epilogue, the CU count
+// and whether the call may split, never on what the context has allocated.
+GemmPlan plan_gemm(int64_t cu_count, int64_t N, int64_t K, int64_t M, int epi, bool may_split)
+{
+    const int64_t gx = (N + BN - 1) / BN, gy = (M + BM - 1) / BM, gy2 = (M + BM2 - 1) / BM2;
+    const int64_t gy4 = (M + 2 * BM2 - 1) / (2 * BM2);
+    const int64_t cus = cu_count > 0 ? cu_count : 256;
+    auto rounds = [&](int64_t wgs) { return (double)((wgs + cus - 1) / cus); };
+    const double c1 = 20 * rounds(gx * gy), c2 = 25 * rounds(gx * gy2), c4 = 47 * rounds(gx * gy4);
+    const int nss = (int)((K / 64 + SC - 1) / SC);
+    GemmPlan p;
+    p.ssper = nss;
+    if (may_split && epi != kEpiSiluOperand && M > BM2 && gx * gy4 < cus && M * N % 4 == 0) {
+        const int want = (int)std::min<int64_t>(std::min<int64_t>(cus / (gx * gy4), nss / 2), 8);
+        if (want >= 2) {
+            const int ssper = (nss + want - 1) / want;
+            const int S = (nss + ssper - 1) / ssper;
+            const double unit_us = 29.0 * (double)K / 4096.0 / 20.0;
+            const double sum_us = (double)(S + 2) * (double)(M * N) * 4.0 / 5e12 * 1e6 + 2.0;
+            const double cs = 47 * rounds(gx * gy4 * S) * (double)ssper / (double)nss + sum_us / unit_us;
+            if (S > 1 && cs < c1 && cs < c2 && cs < c4) {
+                p.tile = 512;
+                p.splits = S;
+                p.ssper = ssper;
+                return p;
+            }
+        }
+    }
+    p.tile = c4 < c2 && c4 < c1 ? 512 : c2 < c1 ? 256 : 128;
+    return p;
+}
+
 template <class T>
 int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
            const _Float16 *Xh, int64_t M, float *Y, int epi, bool may_split)
 {
     const int64_t gx = (N + BN - 1) / BN, gy = (M + BM - 1) / BM, gy2 = (M + BM2 - 1) / BM2;
-    if (gy > 65535 || gx > 0x7FFFFFFF) return AIH_E_LIMIT;
-    // 256-row tiles halve the dequantization per output and 512-row tiles
-    // halve it again; a workgroup of them takes about 1.25 and 2.35 times as
-    // long as one of 128 rows (measured on MI355X).  The shape with the
-    // fewest such rounds of workgroups over the device's CUs wins (ties to
-    // the smaller tile).  Costs in units of 1/20 of a 128-row workgroup.
     const int64_t gy4 = (M + 2 * BM2 - 1) / (2 * BM2);
-    const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
-    auto rounds = [&](int64_t wgs) { return (double)((wgs + cus - 1) / cus); };
-    const double c1 = 20 * rounds(gx * gy), c2 = 25 * rounds(gx * gy2), c4 = 47 * rounds(gx * gy4);
-    // Products of more than 256 rows whose 512-row tiles leave CUs idle split
-    // K over workgroups: S splits of at least two whole super-steps, partial
-    // sums in the second workspace, then a summing pass (estimated at 5 TB/s
-    // over the partials, Y and the output, plus 2 us of launch; a 128-row
-    // workgroup takes about 29 us per 4096 of K)
-    const int nss = (int)((K / 64 + SC - 1) / SC);
-    int S = 1, ssper = nss;
-    double cs = 1e30;
-    if (may_split && epi != kEpiSiluOperand && M > BM2 && gx * gy4 < cus && M * N % 4 == 0 &&
-        (reinterpret_cast<uintptr_t>(Y) & 15) == 0) {
-        const int want = (int)std::min<int64_t>(std::min<int64_t>(cus / (gx * gy4), nss / 2), 8);
-        if (want >= 2) {
-            ssper = (nss + want - 1) / want;
-            S = (nss + ssper - 1) / ssper;
-            const double unit_us = 29.0 * (double)K / 4096.0 / 20.0;
-            const double sum_us = (double)(S + 2) * (double)(M * N) * 4.0 / 5e12 * 1e6 + 2.0;
-            cs = 47 * rounds(gx * gy4 * S) * (double)ssper / (double)nss + sum_us / unit_us;
-        }
+    if (gy > 65535 || gx > 0x7FFFFFFF) return AIH_E_LIMIT;
+    const GemmPlan p = plan_gemm(ctx->cu_count, N, K, M, epi, may_split);
+    if (p.splits > 1) {
+        // the split's partial sums: a shape that splits always splits (a
+        // workspace that cannot grow here, as during a graph capture, is an
+        // error, not a silent change of summation order)
+        void *ws = nullptr;
+        int rc = aih_workspace2(ctx, (size_t)p.splits * (size_t)(M * N) * sizeof(float), &ws);
+        if (rc) return rc;
+        hipLaunchKernelGGL((qgemm256_kernel<T, 2, 2>), dim3((unsigned)gx, (unsigned)gy4, (unsigned)p.splits),
+                           dim3(512), 0, ctx->stream, W, N, K, row_bytes, Xh, M, Y, epi, static_cast<float *>(ws),
+                           p.ssper);
+        rc = aih_launch_status();
+        if (rc) return rc;
+        const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
+        const int64_t groups = (M * N / 4 + 255) / 256;
+        const dim3 grid((unsigned)std::min<int64_t>(groups, 8 * cus));
+        if (reinterpret_cast<uintptr_t>(Y) % 16 == 0)
+            hipLaunchKernelGGL(split_k_sum_kernel<true>, grid, dim3(256), 0, ctx->stream,
+                               static_cast<const float *>(ws), p.splits, M * N, Y, epi == kEpiAccumulate ? 1 : 0);
+        else
+            hipLaunchKernelGGL(split_k_sum_kernel<false>, grid, dim3(256), 0, ctx->stream,
+                               static_cast<const float *>(ws), p.splits, M * N, Y, epi == kEpiAccumulate ? 1 : 0);
+        return aih_launch_status();
     }
-    if (S > 1 && cs < c1 && cs < c2 && cs < c4) {
-        void *p = nullptr;
-        if (aih_workspace2(ctx, (size_t)S * (size_t)(M * N) * sizeof(float), &p) == AIH_OK) {
-            hipLaunchKernelGGL((qgemm256_kernel<T, 2, 2>), dim3((unsigned)gx, (unsigned)gy4, (unsigned)S), dim3(512),
-                               0, ctx->stream, W, N, K, row_bytes, Xh, M, Y, epi, static_cast<float *>(p), ssper);
-            int rc = aih_launch_status();
-            if (rc) return rc;
-            const int64_t groups = (M * N / 4 + 255) / 256;
-            hipLaunchKernelGGL(split_k_sum_kernel, dim3((unsigned)std::min<int64_t>(groups, 8 * cus)), dim3(256), 0,
-                               ctx->stream, static_cast<const float *>(p), S, M * N, Y, epi == kEpiAccumulate ? 1 : 0);
-            return aih_launch_status();
-        }
-    }
-    if (c4 < c2 && c4 < c1)
+    if (p.tile == 512)
         hipLaunchKernelGGL((qgemm256_kernel<T, 2, 2>), dim3((unsigned)gx, (unsigned)gy4), dim3(512), 0, ctx->stream,
-                           W, N, K, row_bytes, Xh, M, Y, epi, nullptr, nss);
-    else if (c2 < c1)
+                           W, N, K, row_bytes, Xh, M, Y, epi, nullptr, p.ssper);
+    else if (p.tile == 256)
         hipLaunchKernelGGL((qgemm256_kernel<T, 1, SC>), dim3((unsigned)gx, (unsigned)gy2), dim3(512), 0, ctx->stream,
-                           W, N, K, row_bytes, Xh, M, Y, epi, nullptr, nss);
+                           W, N, K, row_bytes, Xh, M, Y, epi, nullptr, p.ssper);
     else
         hipLaunchKernelGGL((qgemm_kernel<T>), dim3((unsigned)gx, (unsigned)gy), dim3(512), 0, ctx->stream,
                            W, N, K, row_bytes, Xh, M, Y, epi);
@@ -684,4 +725,14 @@ int aih_launch_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K
     rc = aih_launch_x_tile(ctx, X, M, K, work);
     if (rc) return rc;
     return aih_launch_qgemm_tiled(ctx, type, W, N, K, work, M, Y, 0, may_split && ext == nullptr);
+}
+
+extern "C" int aih_qgemm_plan(aih_ctx *ctx, int64_t N, int64_t K, int64_t M, int may_split, int32_t *tile_rows,
+                              int32_t *splits)
+{
+    if (!ctx || !tile_rows || !splits || N <= 0 || M <= 0 || K <= 0 || K % BK) return AIH_E_INVALID;
+    const GemmPlan p = plan_gemm(ctx->cu_count, N, K, M, kEpiStore, may_split != 0);
+    *tile_rows = p.tile;
+    *splits = p.splits;
+    return AIH_OK;
 }

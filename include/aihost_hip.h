@@ -248,14 +248,24 @@ int aih_qmatvec_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t 
  * before capturing.  A workspace replaced by a larger one stays allocated
  * until aih_destroy, so graphs captured earlier stay valid.  A product of
  * more than 256 rows whose tiles would leave CUs idle splits K over
- * workgroups: its partial sums (splits * M * N floats, Y 16-byte aligned) go
+ * workgroups (aih_qgemm_plan): its partial sums (splits * M * N floats) go
  * to a second context workspace under the same rules and are added in a
- * fixed order, so a result depends only on the shape, not on the call;
- * where that workspace cannot grow, the product runs unsplit (the sums then
- * differ by fp32 rounding of their order).  Replaces TempF32 +
- * ComputeOps.MatMulWeights for M > 8. */
+ * fixed order, so a result depends only on the shape (and the device's CU
+ * count), not on the call; where that workspace cannot grow (during a
+ * capture, out of memory), the call fails like the X workspace's.  Replaces
+ * TempF32 + ComputeOps.MatMulWeights for M > 8. */
 int aih_qgemm(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
               const float *X, int64_t M, float *Y);
+
+/* The tiling aih_qgemm and aih_qgemm_fused choose for an M x K by N product
+ * on this context's device: rows per workgroup tile (128, 256 or 512) and
+ * the number of K splits (1 = none), for a call that may split
+ * (may_split != 0: aih_qgemm, aih_qgemm_fused with AIH_POST_STORE or
+ * AIH_POST_ACCUMULATE) or may not (aih_matmul_weights_q and its
+ * allocation-free twin).  K a multiple of 64.  No counterpart in the
+ * reference: it lets tests and tools see which kernel a shape reaches. */
+int aih_qgemm_plan(aih_ctx *ctx, int64_t N, int64_t K, int64_t M, int may_split, int32_t *tile_rows,
+                   int32_t *splits);
 
 /* ComputeOps.MatMulWeights semantics for a quantized weight: routes M <= 8 to
  * aih_qmatvec and larger M to aih_qgemm, never split over K (the results of
@@ -371,6 +381,15 @@ int aih_silu_mul(aih_ctx *ctx, const float *G, const float *U, float *Y, int64_t
  * in X, n in Y). */
 int aih_silu_mul_pairs(aih_ctx *ctx, const float *X, float *Y, int64_t rows, int64_t n);
 
+/* Y = SiLU(X) = X * (1 / (1 + exp(-X))), element-wise (Y may alias X).
+ * Replaces ComputeOps.SiLU (ComputeOps.cs:493-510, shader ComputeShaders.cs:280-292),
+ * which works in place. */
+int aih_silu(aih_ctx *ctx, const float *X, float *Y, int64_t n);
+
+/* Y = A * B, element-wise (Y may alias A or B).  Replaces ComputeOps.Multiply
+ * (ComputeOps.cs:360-387, shader ComputeShaders.cs:294-306). */
+int aih_mul(aih_ctx *ctx, const float *A, const float *B, float *Y, int64_t n);
+
 /* Y = A + B, element-wise (Y may alias A or B).  Replaces ComputeOps.Add
  * (ComputeOps.cs:389). */
 int aih_add(aih_ctx *ctx, const float *A, const float *B, float *Y, int64_t n);
@@ -447,7 +466,11 @@ int aih_attention_decode_qkv(aih_ctx *ctx, const float *QKV, float *Kc, float *V
  * dim] table of `type` blocks (ids from device memory; an id outside
  * [0, vocab) gives zeros).  Bit-exact to aih_dequantize (IEEE fp16 scales).
  * Replaces ComputeOps.EmbeddingLookupFromQuantized (ComputeOps.cs:1399-1454),
- * which dequantizes the whole table below 512 MiB. */
+ * which dequantizes the whole table below 512 MiB.  type = AIH_TYPE_F32
+ * gathers rows of an fp32 table: ComputeOps.EmbeddingLookup
+ * (ComputeOps.cs:1780-1800, shader ComputeShaders.cs:499-515; there a
+ * negative id leaves its row unwritten and one past the table reads beyond
+ * it). */
 int aih_embed_q(aih_ctx *ctx, int type, const void *table, int64_t vocab, int64_t dim, const int32_t *ids, int64_t n,
                 float *Y);
 

@@ -99,13 +99,17 @@ def attention(q, kc, vc, positions, n_heads, n_kv_heads, head_dim, scale=None):
     k = np.asarray(kc, dtype=np.float64).reshape(-1, n_kv_heads, head_dim)
     v = np.asarray(vc, dtype=np.float64).reshape(-1, n_kv_heads, head_dim)
     group = n_heads // n_kv_heads
+    pos = np.asarray(positions)
+    L = int(pos.max()) + 1
+    # row r sees cache rows 0..pos[r]: later keys get weight exactly 0
+    mask = np.arange(L)[None, :] > pos[:, None]
     out = np.empty_like(q)
     for h in range(n_heads):
         kvh = h // group
-        for r, p in enumerate(positions):
-            s = (k[: p + 1, kvh, :] @ q[r, h, :]) * float(scale)
-            s = np.exp(s - s.max())
-            out[r, h, :] = (s / s.sum()) @ v[: p + 1, kvh, :]
+        s = (q[:, h, :] @ k[:L, kvh, :].T) * float(scale)
+        s[mask] = -np.inf
+        s = np.exp(s - s.max(axis=1, keepdims=True))
+        out[:, h, :] = (s / s.sum(axis=1, keepdims=True)) @ v[:L, kvh, :]
     return out.reshape(len(positions), n_heads * head_dim).astype(f32)
 
 

@@ -148,6 +148,40 @@ def test_silu_mul(device, bufs):
     assert np.max(np.abs(y - ref) / (np.abs(ref) + 1e-30)) < 2e-6
 
 
+def test_silu_and_mul_separately(device, bufs):
+    """aih_silu (in place) then aih_mul: the reference's SiLU and Multiply
+    operators one after the other, bit for bit the fused aih_silu_mul."""
+    g = np.concatenate([rnd(19, 14336, scale=3.0), np.array([0.0, 88.0, -88.0, -200.0, 20.0], np.float32)])
+    u = rnd(20, g.size)
+    G, U, F = bufs.up(g), bufs.up(u), bufs.up(g)
+    nat.check(L.aih_silu(device.handle, G, G, g.size), "silu in place")
+    s = bufs.read(G, g.size)
+    ref = ol.silu_mul(g, np.ones_like(g))
+    assert np.max(np.abs(s - ref) / (np.abs(ref) + 1e-30)) < 2e-6
+    nat.check(L.aih_mul(device.handle, G, U, G, g.size), "mul in place")
+    assert np.array_equal(bufs.read(G, g.size), s * u)
+    nat.check(L.aih_silu_mul(device.handle, F, U, F, g.size), "silu_mul")
+    assert np.array_equal(bufs.read(G, g.size).view(np.uint32), bufs.read(F, g.size).view(np.uint32))
+    assert L.aih_silu(device.handle, G, G, -1) == nat.AIH_E_INVALID
+    assert L.aih_mul(device.handle, None, U, G, 4) == nat.AIH_E_INVALID
+    assert L.aih_mul(device.handle, G, U, G, 0) == nat.AIH_OK
+
+
+def test_embed_f32_table(device, bufs):
+    """aih_embed_q on an fp32 table (ComputeOps.EmbeddingLookup): rows by id,
+    zeros for ids outside the table."""
+    vocab, dim = 300, 4096
+    tab = rnd(21, vocab, dim)
+    ids = np.array([5, 0, 299, 5, 300, -3, 17], np.int32)
+    T, I = bufs.up(tab), bufs.up(ids)
+    Y = bufs.empty(len(ids) * dim * 4)
+    nat.check(L.aih_embed_q(device.handle, nat.F32, T, vocab, dim, I, len(ids), Y), "embed f32")
+    y = bufs.read(Y, len(ids) * dim).reshape(len(ids), dim)
+    ok = (ids >= 0) & (ids < vocab)
+    assert np.array_equal(y[ok], tab[ids[ok]])
+    assert not y[~ok].any()
+
+
 def test_silu_mul_pairs(device, bufs):
     # rows of interleaved (gate, up) columns, as a GEMM over gate/up rows
     # interleaved writes them; bit-exact to aih_silu_mul on the split halves

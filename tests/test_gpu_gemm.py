@@ -58,6 +58,10 @@ def test_shapes(device, orc, qtype, n, k, m):
     (nat.Q8_0, 28000, 832, 450), (nat.Q4_0, 28672, 576, 257),
 ])
 def test_wide_tiles(device, orc, qtype, n, k, m):
+    tile, splits = nat.qgemm_plan(device.handle, n, k, m)
+    want = 512 if n > 20000 else 256
+    if (tile, splits) != (want, 1):
+        pytest.skip("on this device's CU count the shape takes %d-row tiles, %d splits" % (tile, splits))
     w = synth_weight(qtype, n, k, seed=n + k)
     x = x_of(m, k, seed=m * 3 + k)
     y = qgemm(device, qtype, w, n, k, x)
@@ -74,6 +78,10 @@ def test_wide_tiles(device, orc, qtype, n, k, m):
     (nat.Q8_0, 512, 4160, 300), (nat.Q4_0, 256, 2112, 290),
 ])
 def test_split_k(device, orc, qtype, n, k, m):
+    tile, splits = nat.qgemm_plan(device.handle, n, k, m)
+    if splits < 2:
+        pytest.skip("on this device's CU count the shape does not split K (%d-row tiles)" % tile)
+    assert nat.qgemm_plan(device.handle, n, k, m, may_split=False)[1] == 1
     w = synth_weight(qtype, n, k, seed=n + k + 1)
     x = x_of(m, k, seed=m + 5)
     y = qgemm(device, qtype, w, n, k, x)
@@ -122,9 +130,10 @@ def test_matmul_weights_routing(device, orc):
 
 
 def test_gemm_rows_match_matvec(device):
-    # Both paths round x to fp16; the GEMM also rounds each dequantized weight
-    # to fp16 (the matvec applies the scales in fp32), which alone moves the
-    # result by about 2e-4 normwise.  The two paths agree within that.
+    # The GEMM rounds x (times a power of two per row) and each dequantized
+    # weight to fp16; the matvec multiplies the codes exactly by a 22-bit
+    # fixed-point x and applies the scales in fp32.  The GEMM's two roundings
+    # move the result by about 2e-4 normwise; the two paths agree within that.
     from gpu_util import qmatvec
     n, k, m = 256, 4096, 16
     w = synth_weight(nat.Q6_K, n, k)
@@ -153,3 +162,56 @@ def test_argument_errors(device):
     finally:
         for b in (wb, xb, yb):
             b.dispose()
+
+
+def test_split_shape_same_bits_eager_and_replayed(device):
+    """A shape that splits K gives the same bits eagerly and from a replayed
+    graph (on a context that ran it once before the capture, so both
+    workspaces are sized); a fresh context cannot record it (AIH_E_LIMIT,
+    the workspaces cannot grow during a capture) rather than recording an
+    unsplit product."""
+    import ctypes
+    n, k, m = 1024, 14336, 300
+    if nat.qgemm_plan(device.handle, n, k, m)[1] < 2:
+        pytest.skip("on this device's CU count the shape does not split K")
+    L = nat.lib()
+    w = synth_weight(nat.Q4_K, n, k, seed=7)
+    x = x_of(m, k, seed=8)
+    fresh = C.HipComputeDevice(0)
+    bufs = []
+    try:
+        for dev in (device, fresh):
+            wb, xb, yb = upload(dev, w), upload(dev, x), dev.create_buffer(m * n * 4)
+            bufs.append((dev, wb, xb, yb))
+        dev, wb, xb, yb = bufs[0]
+        h = dev.handle
+        args = (nat.Q4_K, wb.get_pointer(), n, k, xb.get_pointer(), m, yb.get_pointer())
+        nat.check(L.aih_qgemm(h, *args), "eager")
+        eager = yb.read_range(0, m * n, np.float32).copy()
+        nat.check(L.aih_capture_begin(h), "capture")
+        st = L.aih_qgemm(h, *args)
+        g = ctypes.c_void_p()
+        nat.check(L.aih_capture_end(h, ctypes.byref(g)), "capture end")
+        nat.check(st, "captured")
+        try:
+            for _ in range(3):
+                nat.check(L.aih_memset(h, yb.get_pointer(), 0xFF, m * n * 4), "memset")
+                nat.check(L.aih_graph_launch(h, g.value), "replay")
+                dev.synchronize()
+                assert np.array_equal(yb.read_range(0, m * n, np.float32).view(np.uint32), eager.view(np.uint32))
+        finally:
+            L.aih_graph_destroy(g.value)
+        dev, wb, xb, yb = bufs[1]
+        h = dev.handle
+        nat.check(L.aih_capture_begin(h), "capture")
+        st = L.aih_qgemm(h, nat.Q4_K, wb.get_pointer(), n, k, xb.get_pointer(), m, yb.get_pointer())
+        g = ctypes.c_void_p()
+        nat.check(L.aih_capture_end(h, ctypes.byref(g)), "capture end")
+        if g.value:
+            L.aih_graph_destroy(g.value)
+        assert st == nat.AIH_E_LIMIT, nat.strerror(st)
+    finally:
+        for dev, wb, xb, yb in bufs:
+            for b in (wb, xb, yb):
+                b.dispose()
+        fresh.dispose()

@@ -174,7 +174,7 @@ def test_padded_strides_leave_gaps_untouched(device, orc):
     assert np.all(np.isnan(y[:, n:]))  # memset 0xFF pattern untouched
 
 
-@pytest.mark.parametrize("batch", [2, 5])   # dot2 kernel (fp32 scales), MFMA kernel (fp16 weights)
+@pytest.mark.parametrize("batch", [2, 5])   # integer-dot kernel (batch 1-2), matrix-core kernel (3-8)
 def test_subnormal_and_extreme_scales(device, orc, batch):
     # random bytes with small finite scales: exercises every code value
     rng = np.random.default_rng(5)

@@ -32,7 +32,8 @@ dequantized matrices once).
         (the only rounding that differs) is 5.9e-3 from the exact oracle on
         the prefill logits at this seed and 3.5e-3 to 4.2e-3 on the decode
         steps, about the size it is at 16 tokens: the per-product rounding
-        does not grow with the prompt.  Bound TOL_FP16.
+        does not grow with the prompt.  Measured on the GPU 5.8e-3, then
+        4.2e-3 to 3.5e-3.  Bound TOL_FP16.
   * The benchmark's workload, a 512-token prompt and 128 greedy tokens:
     graph replays give the same tokens and final logits, bit for bit, as the
     same steps launched eagerly.

@@ -363,11 +363,26 @@ constexpr int kHD = 128;      // head_dim supported by the attention kernels
 constexpr int kSub = 64;      // keys per decode sub-chunk (one pass of the score step)
 constexpr int kMaxSplit = 64; // decode splits per head (upper bound)
 constexpr int kQTile = 64;    // queries per prefill workgroup
+constexpr int kSplitKeys = 64;  // keys per decode split while splits stay under kMaxSplit
 
+// Decode splits of a cache of max_len rows: ranges of 64 keys until there
+// are kMaxSplit of them, then longer ranges.  (16-key ranges, one wave per
+// split, gave 320 workgroups instead of 80 at 640 rows and 8 KV heads, but
+// the partial kernel stayed at 8.6 us against 8.1 -- it is bound by its
+// memory round trips, not by its parallelism -- and the combine over four
+// times the splits went from 2.6 to 4.0 us.)
 int32_t decode_splits(int32_t max_len)
 {
-    const int32_t n = (max_len + kSub - 1) / kSub;
+    const int32_t n = (max_len + kSplitKeys - 1) / kSplitKeys;
     return n < kMaxSplit ? n : kMaxSplit;
+}
+
+// Waves per workgroup of the grouped decode kernel: a split's keys in
+// sub-chunks of 16 per wave, at most four waves.
+int decode_waves(int32_t max_len, int32_t n_split)
+{
+    const int32_t chunk = (max_len + n_split - 1) / n_split;
+    return chunk <= 16 ? 1 : chunk <= 32 ? 2 : 4;
 }
 
 // Decode (one query row), split over keys.  Workgroup (h, s) of 256 threads
@@ -490,19 +505,20 @@ attn_decode_partial(const float *__restrict__ Q, const float *__restrict__ Kc, c
 // that of rope_qkv_kernel, so the FUSE and plain forms give the same bits.
 // Plain: the query rows are Q (already rotated) and every key comes from the
 // cache.
-template <int G, bool FUSE>
-__global__ void __launch_bounds__(256)
+template <int G, bool FUSE, int NW>
+__global__ void __launch_bounds__(64 * NW)
 attn_decode_gqa(const float *__restrict__ Qsrc, float *Kc, float *Vc, float *__restrict__ part, int32_t n_heads,
                 int32_t n_kv_heads, int32_t start, const int32_t *pos, const float *__restrict__ table,
                 int32_t table_rows, int32_t cache_rows, float scale, int32_t n_split)
 {
     constexpr int half = kHD / 2;
-    constexpr int QP = (G * half + 255) / 256;   // query pairs per thread
+    constexpr int NT = 64 * NW;                 // threads
+    constexpr int QP = (G * half + NT - 1) / NT;   // query pairs per thread
     __shared__ f4 qs[G][kHD / 4];
     __shared__ f4 kn[kHD / 4], vn[kHD / 4];
-    __shared__ float ps[4][G][16];
-    __shared__ float wm[4][G], wl[4][G];
-    __shared__ float wacc[4][G][kHD];
+    __shared__ float ps[NW][G][16];
+    __shared__ float wm[NW][G], wl[NW][G];
+    __shared__ float wacc[NW][G][kHD];
     const int kvh = blockIdx.x, s = blockIdx.y, t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int kk = lane >> 2, part4 = lane & 3;
     const int64_t kv_stride = (int64_t)n_kv_heads * kHD;
@@ -542,7 +558,7 @@ attn_decode_gqa(const float *__restrict__ Qsrc, float *Kc, float *Vc, float *__r
     // query heads into LDS (rotated here when FUSE), the new key row when owned
 #pragma unroll
     for (int i = 0; i < QP; ++i) {
-        const int e = t + 256 * i;
+        const int e = t + NT * i;
         if (e < G * half) {
             const int g = e / half, pi = e % half;
             const float *x = Qsrc + (int64_t)(kvh * G + g) * kHD + 2 * pi;
@@ -561,20 +577,24 @@ attn_decode_gqa(const float *__restrict__ Qsrc, float *Kc, float *Vc, float *__r
     if (own) {
         const float *kx = Qsrc + (int64_t)n_heads * kHD + (int64_t)kvh * kHD;
         const float *vx = kx + kv_stride;
-        if (t < half) {
-            const float c = tp[2 * t], sn = tp[2 * t + 1];
-            const float x0 = kx[2 * t], x1 = kx[2 * t + 1];
+        // key pair e (rotated) by threads e, value quad e by threads half + e
+        // (by threads e too when the workgroup has fewer than half + kHD / 4)
+        constexpr int v0 = NT >= half + kHD / 4 ? half : 0;
+        for (int e = t; e < half; e += NT) {
+            const float c = tp[2 * e], sn = tp[2 * e + 1];
+            const float x0 = kx[2 * e], x1 = kx[2 * e + 1];
             const float y0 = x0 * c - x1 * sn, y1 = x0 * sn + x1 * c;
-            float *kq = reinterpret_cast<float *>(kn) + 2 * t;
+            float *kq = reinterpret_cast<float *>(kn) + 2 * e;
             kq[0] = y0;
             kq[1] = y1;
-            float *kc = Kc + (int64_t)p * kv_stride + (int64_t)kvh * kHD + 2 * t;
+            float *kc = Kc + (int64_t)p * kv_stride + (int64_t)kvh * kHD + 2 * e;
             kc[0] = y0;
             kc[1] = y1;
-        } else if (t < half + kHD / 4) {
-            const f4 vv = reinterpret_cast<const f4 *>(vx)[t - half];
-            vn[t - half] = vv;
-            reinterpret_cast<f4 *>(Vc + (int64_t)p * kv_stride + (int64_t)kvh * kHD)[t - half] = vv;
+        }
+        for (int e = t - v0; e >= 0 && e < kHD / 4; e += NT) {
+            const f4 vv = reinterpret_cast<const f4 *>(vx)[e];
+            vn[e] = vv;
+            reinterpret_cast<f4 *>(Vc + (int64_t)p * kv_stride + (int64_t)kvh * kHD)[e] = vv;
         }
     }
     __syncthreads();
@@ -587,7 +607,7 @@ attn_decode_gqa(const float *__restrict__ Qsrc, float *Kc, float *Vc, float *__r
         l[g] = 0.f;
         acc[g] = float2{0.f, 0.f};
     }
-    for (int32_t c0 = j0; c0 < j1; c0 += 64) {
+    for (int32_t c0 = j0; c0 < j1; c0 += 16 * NW) {
         const int32_t jk = c0 + 16 * w + kk;              // this thread's key
         if (own && jk == p) {
 #pragma unroll
@@ -652,11 +672,11 @@ attn_decode_gqa(const float *__restrict__ Qsrc, float *Kc, float *Vc, float *__r
                 acc[g].y = acc[g].y * corr[gb] + a.y;
             }
         }
-        if (c0 + 64 < j1) load_k(c0 + 64);   // the next sub-chunk's keys
-        if (c0 + 64 < j1) load_v(c0 + 64);
+        if (c0 + 16 * NW < j1) load_k(c0 + 16 * NW);   // the next sub-chunk's keys
+        if (c0 + 16 * NW < j1) load_v(c0 + 16 * NW);
     }
 
-    // merge the four waves: M = max of the wave maxima; weights e^(m_w - M)
+    // merge the NW waves: M = max of the wave maxima; weights e^(m_w - M)
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         if (lane == 0) {
@@ -667,12 +687,14 @@ attn_decode_gqa(const float *__restrict__ Qsrc, float *Kc, float *Vc, float *__r
         wacc[w][g][2 * lane + 1] = acc[g].y;
     }
     __syncthreads();
-    for (int e = t; e < G * kHD; e += 256) {
+    for (int e = t; e < G * kHD; e += NT) {
         const int g = e / kHD, d = e % kHD;
-        const float M = fmaxf(fmaxf(wm[0][g], wm[1][g]), fmaxf(wm[2][g], wm[3][g]));
+        float M = wm[0][g];
+#pragma unroll
+        for (int ww = 1; ww < NW; ++ww) M = fmaxf(M, wm[ww][g]);
         float o = 0.f, lt = 0.f;
 #pragma unroll
-        for (int ww = 0; ww < 4; ++ww) {
+        for (int ww = 0; ww < NW; ++ww) {
             const float f = wm[ww][g] == -INFINITY ? 0.f : expf(wm[ww][g] - M);
             o = fmaf(wacc[ww][g][d], f, o);
             lt = fmaf(wl[ww][g], f, lt);
@@ -1403,23 +1425,39 @@ namespace {
 
 // Grouped decode attention for query groups of 1, 2, 4 or 8 heads
 // (AIH_E_UNSUPPORTED otherwise); FUSE selects aih_attention_decode_qkv's form.
+template <bool FUSE, int NW>
+int launch_gqa_nw(aih_ctx *ctx, int group, dim3 grid, const float *Qsrc, float *Kc, float *Vc, float *part,
+                  int32_t n_heads, int32_t n_kv_heads, int32_t start, const int32_t *pos, const float *table,
+                  int32_t table_rows, int32_t cache_rows, float scale, int32_t n_split)
+{
+    const dim3 block(64 * NW);
+    switch (group) {
+    case 1: hipLaunchKernelGGL((attn_decode_gqa<1, FUSE, NW>), grid, block, 0, ctx->stream, Qsrc, Kc, Vc, part,
+                               n_heads, n_kv_heads, start, pos, table, table_rows, cache_rows, scale, n_split); break;
+    case 2: hipLaunchKernelGGL((attn_decode_gqa<2, FUSE, NW>), grid, block, 0, ctx->stream, Qsrc, Kc, Vc, part,
+                               n_heads, n_kv_heads, start, pos, table, table_rows, cache_rows, scale, n_split); break;
+    case 4: hipLaunchKernelGGL((attn_decode_gqa<4, FUSE, NW>), grid, block, 0, ctx->stream, Qsrc, Kc, Vc, part,
+                               n_heads, n_kv_heads, start, pos, table, table_rows, cache_rows, scale, n_split); break;
+    case 8: hipLaunchKernelGGL((attn_decode_gqa<8, FUSE, NW>), grid, block, 0, ctx->stream, Qsrc, Kc, Vc, part,
+                               n_heads, n_kv_heads, start, pos, table, table_rows, cache_rows, scale, n_split); break;
+    default: return AIH_E_UNSUPPORTED;
+    }
+    return aih_launch_status();
+}
+
 template <bool FUSE>
 int launch_gqa(aih_ctx *ctx, int group, dim3 grid, const float *Qsrc, float *Kc, float *Vc, float *part,
                int32_t n_heads, int32_t n_kv_heads, int32_t start, const int32_t *pos, const float *table,
                int32_t table_rows, int32_t cache_rows, float scale, int32_t n_split)
 {
-    switch (group) {
-    case 1: hipLaunchKernelGGL((attn_decode_gqa<1, FUSE>), grid, dim3(256), 0, ctx->stream, Qsrc, Kc, Vc, part,
-                               n_heads, n_kv_heads, start, pos, table, table_rows, cache_rows, scale, n_split); break;
-    case 2: hipLaunchKernelGGL((attn_decode_gqa<2, FUSE>), grid, dim3(256), 0, ctx->stream, Qsrc, Kc, Vc, part,
-                               n_heads, n_kv_heads, start, pos, table, table_rows, cache_rows, scale, n_split); break;
-    case 4: hipLaunchKernelGGL((attn_decode_gqa<4, FUSE>), grid, dim3(256), 0, ctx->stream, Qsrc, Kc, Vc, part,
-                               n_heads, n_kv_heads, start, pos, table, table_rows, cache_rows, scale, n_split); break;
-    case 8: hipLaunchKernelGGL((attn_decode_gqa<8, FUSE>), grid, dim3(256), 0, ctx->stream, Qsrc, Kc, Vc, part,
-                               n_heads, n_kv_heads, start, pos, table, table_rows, cache_rows, scale, n_split); break;
-    default: return AIH_E_UNSUPPORTED;
+    switch (decode_waves(cache_rows, n_split)) {
+    case 1: return launch_gqa_nw<FUSE, 1>(ctx, group, grid, Qsrc, Kc, Vc, part, n_heads, n_kv_heads, start, pos, table,
+                                          table_rows, cache_rows, scale, n_split);
+    case 2: return launch_gqa_nw<FUSE, 2>(ctx, group, grid, Qsrc, Kc, Vc, part, n_heads, n_kv_heads, start, pos, table,
+                                          table_rows, cache_rows, scale, n_split);
+    default: return launch_gqa_nw<FUSE, 4>(ctx, group, grid, Qsrc, Kc, Vc, part, n_heads, n_kv_heads, start, pos,
+                                           table, table_rows, cache_rows, scale, n_split);
     }
-    return aih_launch_status();
 }
 
 }  // namespace

@@ -556,16 +556,23 @@ operand_fixup_kernel(_Float16 *__restrict__ Xt, int64_t mpad, int64_t K)
     const int lane = threadIdx.x & 63;
     const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (m >= mpad) return;
-    const int64_t nb = K / 32;
+    const int64_t nb = K / 32;   // a multiple of 2 (K % 64 == 0)
     char *const img = reinterpret_cast<char *>(Xt);
     int8_t *const d = reinterpret_cast<int8_t *>(img + aih_operand::block_exp_offset(mpad, K)) + m * nb;
     int mn = 127;
     bool odd = false;
-    for (int64_t b = lane; b < nb; b += 64) {
-        const int v = d[b];
-        if (v != aih_operand::kZeroBlock) {
-            mn = min(mn, v);
-            odd = odd || v != 0;
+    // the row's exponents two at a time (rows start 2-byte aligned), the loads
+    // of four passes issued together (K up to 16384 in one round trip)
+#pragma unroll 4
+    for (int64_t b = 2 * lane; b < nb; b += 128) {
+        const uint16_t w2 = *reinterpret_cast<const uint16_t *>(d + b);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int v = (int8_t)(w2 >> (8 * j));
+            if (v != aih_operand::kZeroBlock) {
+                mn = min(mn, v);
+                odd = odd || v != 0;
+            }
         }
     }
     if (__builtin_amdgcn_ballot_w64(odd) == 0) return;

@@ -422,9 +422,10 @@ class LlamaDecoder:
         self.head(self.x + (n - 1) * c.dim * 4, self.pos, n - 1)
         return self.read_token() if read else None
 
-    def decode_step(self):
-        """One greedy decode step reading its token and position from device
-        memory (capturable into a graph)."""
+    def _step(self):
+        """The launches of one greedy decode step, reading its token and
+        position from device memory (what capture() records; no host
+        bookkeeping)."""
         c = self.cfg
         qt, tb, vocab, dim = self.w["token_embd"]
         nat.check(self.L.aih_embed_q(self.h, qt, tb, vocab, dim, self.token, 1, self.x), "embed")
@@ -433,13 +434,13 @@ class LlamaDecoder:
         self.head(self.x, self.pos, self.n_prompt - 1)
 
     def capture(self):
-        """Record decode_step into a HIP graph (after prefill)."""
+        """Record one decode step (_step) into a HIP graph (after prefill)."""
         if self.graph is not None:
             return self.graph
         g = ctypes.c_void_p()
         nat.check(self.L.aih_capture_begin(self.h), "aih_capture_begin")
         try:
-            self.decode_step()
+            self._step()
         finally:
             st = self.L.aih_capture_end(self.h, ctypes.byref(g))
         nat.check(st, "aih_capture_end")
@@ -463,8 +464,13 @@ class LlamaDecoder:
                 self.position += 1
         else:
             for _ in range(steps):
-                self.decode_step()
+                self._step()
                 self.position += 1
+
+    def decode_step(self):
+        """One eager greedy decode step (decode(1, use_graph=False)): counted
+        against max_len like every other step."""
+        self.decode(1, use_graph=False)
 
     def read_token(self):
         t = np.empty(1, dtype=np.int32)

@@ -119,12 +119,16 @@ def test_limits(device, model):
         dec.prefill(np.zeros(16, np.int32))
         with pytest.raises(ValueError):
             dec.decode(5)
-        dec.decode(2, use_graph=False)        # positions 16, 17
+        dec.decode(1, use_graph=False)        # position 16
+        dec.decode_step()                     # position 17: counted like decode()
+        assert dec.position == 18
         with pytest.raises(ValueError):       # steps already decoded count
             dec.decode(3)
         dec.decode(2)                         # positions 18, 19: the last cache row
         with pytest.raises(ValueError):
             dec.decode(1, use_graph=False)
+        with pytest.raises(ValueError):
+            dec.decode_step()
         assert dec.position == 20
     finally:
         dec.dispose()

@@ -1284,7 +1284,9 @@ argmax_kernel(const float *__restrict__ X, int64_t n, int32_t *token, int32_t *p
 //   PRE = AIH_PRE_SILU_MUL    x = SiLU(X) * X2                        (X2: M x K)
 //   PRE = AIH_PRE_SILU_PAIRS  x[k] = SiLU(X[2k]) * X[2k+1]            (X: M x 2K)
 // Rows of up to 8 * 256 * kRowIt values stay in registers between the maximum
-// and the rounding; longer rows are computed twice.
+// and the rounding; longer rows are computed twice.  (For AIH_PRE_NONE, at
+// 512 x 4096 on MI355X: 7.3 us, against 6.2 us for a conversion without the
+// row maximum, one 8-value slot per thread, and 8.7 us with one wave per row.)
 constexpr int kRowIt = 8;
 
 template <int NT>

@@ -144,6 +144,51 @@ __device__ __forceinline__ void undo_row_exp(f16v &acc0, f16v &acc1, int32_t ev,
     }
 }
 
+// A wave's two 32 x 32 accumulators stored into Y (rows mrow0 .., columns
+// n0 + lane % 32 and n0 + 32 + lane % 32), or added into it (Y + acc, the
+// operand order of aih_add).  A block wholly inside Y is written without
+// per-value guards, and for the add all 32 of its lane's Y values are loaded
+// before the first add, so that they are in flight together rather than one
+// round trip per register.  On MI355X, 4096 x 4096 x 512 per call: the
+// accumulate epilogue 42.5 -> 33.5-34.4 us (the guarded form cost 3-5 us
+// over a plain store).
+__device__ __forceinline__ void store_tile(const f16v &acc0, const f16v &acc1, int lane, int64_t mrow0, int64_t n0,
+                                           int64_t M, int64_t N, float *__restrict__ Y, bool accumulate)
+{
+    const int64_t na = n0 + (lane & 31), nb = na + 32;
+    auto row = [&](int r) { return mrow0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); };
+    if (mrow0 + 32 <= M && n0 + 64 <= N) {
+        if (accumulate) {
+            float ya[16], yb[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                ya[r] = Y[row(r) * N + na];
+                yb[r] = Y[row(r) * N + nb];
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                Y[row(r) * N + na] = ya[r] + acc0[r];
+                Y[row(r) * N + nb] = yb[r] + acc1[r];
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                Y[row(r) * N + na] = acc0[r];
+                Y[row(r) * N + nb] = acc1[r];
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int64_t m = row(r);
+        if (m < M) {
+            if (na < N) Y[m * N + na] = accumulate ? Y[m * N + na] + acc0[r] : acc0[r];
+            if (nb < N) Y[m * N + nb] = accumulate ? Y[m * N + nb] + acc1[r] : acc1[r];
+        }
+    }
+}
+
 // Eight waves per workgroup in two roles, one of each on every SIMD; the
 // workgroup owns a 128 (M) x 64 (N) tile of Y and walks K in super-steps of
 // 256 (a Q4_K/Q6_K super-block, 8 blocks of Q8_0/Q4_0), with one LDS barrier
@@ -313,16 +358,7 @@ qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
                            reinterpret_cast<_Float16 *>(Y));
         return;
     }
-    const int64_t na = n0 + fr, nb = n0 + 32 + fr;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int i = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        const int64_t m = m0 + 32 * wave + i;
-        if (m < M) {
-            if (na < N) Y[m * N + na] = epi == kEpiAccumulate ? Y[m * N + na] + acc0[r] : acc0[r];
-            if (nb < N) Y[m * N + nb] = epi == kEpiAccumulate ? Y[m * N + nb] + acc1[r] : acc1[r];
-        }
-    }
+    store_tile(acc0, acc1, lane, m0 + 32 * wave, n0, M, N, Y, epi == kEpiAccumulate);
 }
 
 // Wide tiles for large products: a workgroup of eight waves owns a 256 MB (M)
@@ -501,24 +537,12 @@ qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
         }
         return;
     }
-    const int64_t na = n0 + fr, nb = n0 + 32 + fr;
+    // a split's partial sums are stored (the summing pass adds them into Y)
     float *const Pz = P ? P + (int64_t)blockIdx.z * M * N : nullptr;
 #pragma unroll
     for (int j = 0; j < MB; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int i = 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            const int64_t m = m0 + 32 * (MB * wave + j) + i;
-            if (m < M) {
-                if (Pz) {
-                    if (na < N) Pz[m * N + na] = acc[j][0][r];
-                    if (nb < N) Pz[m * N + nb] = acc[j][1][r];
-                } else {
-                    if (na < N) Y[m * N + na] = epi == kEpiAccumulate ? Y[m * N + na] + acc[j][0][r] : acc[j][0][r];
-                    if (nb < N) Y[m * N + nb] = epi == kEpiAccumulate ? Y[m * N + nb] + acc[j][1][r] : acc[j][1][r];
-                }
-            }
-        }
+        store_tile(acc[j][0], acc[j][1], lane, m0 + 32 * (MB * wave + j), n0, M, N, Pz ? Pz : Y,
+                   !Pz && epi == kEpiAccumulate);
 }
 
 // The splits of a GEMM split over K: Y = P_0 + P_1 + ... (in that order),

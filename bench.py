@@ -590,6 +590,11 @@ def main():
                             "(the %s; the host has %d CPUs)" % (reps, el, nt, src, os.cpu_count())}
     dev.dispose()
 
+    # the matvec's per-launch time over the faster of the two plain streams of
+    # its bytes measured in this run (1.0 = as fast as the best stream)
+    streams = [v["us_per_launch"] for key, v in extra.items() if key.startswith("stream_read_")]
+    vs_stream = round(ms_kernel * 1e3 / min(streams), 4) if streams else None
+
     out = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -618,7 +623,8 @@ def main():
                      "timing": "kernel_us: HIP events around the timed graph replays on the library's stream, per "
                                "launch: back-to-back kernels, each with its launch's fixed cost, plus the start-up "
                                "of each replay (one replay at --steps <= 120: about 0.3 us per launch at 20)",
-                     "bytes_per_launch": nbytes},
+                     "bytes_per_launch": nbytes,
+                     "vs_best_stream": vs_stream},
         "cpu_baseline": cpu,
         "cpu_baseline_threads": cpu_mt,
         "decode": decode,

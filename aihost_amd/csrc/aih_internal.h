@@ -4,9 +4,36 @@
 #include <hip/hip_runtime.h>
 #include <cstdint>
 #include <cstddef>
+#include <condition_variable>
+#include <memory>
 #include <mutex>
+#include <thread>
 #include <unordered_map>
 #include <vector>
+
+// Host threads that split a large host memcpy (the fill of a pinned staging
+// slot) into parts, so that the copy into pinned memory keeps up with the DMA
+// engine.  Workers start on first use and stop when the pool is destroyed.
+class aih_copy_pool {
+public:
+    ~aih_copy_pool();
+    // memcpy(dst, src, bytes) by up to `threads` threads (this one included);
+    // false when no worker could be started (the caller then copies alone).
+    bool copy(void *dst, const void *src, size_t bytes, int threads);
+
+private:
+    void worker(int index);
+    std::mutex mu;
+    std::condition_variable start_cv, done_cv;
+    std::vector<std::thread> workers;
+    char *job_dst = nullptr;
+    const char *job_src = nullptr;
+    size_t job_bytes = 0;
+    int job_parts = 0;
+    unsigned long long generation = 0;
+    int pending = 0;
+    bool stopping = false;
+};
 
 #include "../../include/aihost_hip.h"
 
@@ -61,6 +88,8 @@ struct aih_ctx {
     // Device address of this GPU's static staging buffer (the allocation-free
     // entry point's), set by aih_init.
     void *noalloc_scratch = nullptr;
+    // Host threads for filling the staging slots (aih_memcpy_h2d).
+    std::unique_ptr<aih_copy_pool> copier;
 };
 
 // Device workspace of at least `bytes` on the context's device.  Growing it

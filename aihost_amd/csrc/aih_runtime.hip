@@ -116,6 +116,72 @@ int aih_workspace2(aih_ctx *ctx, size_t bytes, void **out)
     return grow_workspace(ctx, ctx->work2, ctx->work2_bytes, bytes, out);
 }
 
+aih_copy_pool::~aih_copy_pool()
+{
+    {
+        std::lock_guard<std::mutex> g(mu);
+        stopping = true;
+    }
+    start_cv.notify_all();
+    for (auto &t : workers) t.join();
+}
+
+// Part `part` of `parts` of the current job, on 4 KiB boundaries.
+static void copy_part(char *dst, const char *src, size_t bytes, int part, int parts)
+{
+    const size_t per = ((bytes + parts - 1) / parts + 4095) & ~(size_t)4095;
+    const size_t a = std::min(bytes, per * (size_t)part), b = std::min(bytes, a + per);
+    if (b > a) std::memcpy(dst + a, src + a, b - a);
+}
+
+void aih_copy_pool::worker(int index)
+{
+    unsigned long long seen = 0;
+    for (;;) {
+        char *d;
+        const char *s;
+        size_t n;
+        int parts;
+        {
+            std::unique_lock<std::mutex> g(mu);
+            start_cv.wait(g, [&] { return stopping || generation != seen; });
+            if (stopping) return;
+            seen = generation;
+            d = job_dst, s = job_src, n = job_bytes, parts = job_parts;
+        }
+        if (index + 1 < parts) copy_part(d, s, n, index + 1, parts);
+        {
+            std::lock_guard<std::mutex> g(mu);
+            if (--pending == 0) done_cv.notify_one();
+        }
+    }
+}
+
+bool aih_copy_pool::copy(void *dst, const void *src, size_t bytes, int threads)
+{
+    try {
+        while ((int)workers.size() < threads - 1) workers.emplace_back(&aih_copy_pool::worker, this,
+                                                                      (int)workers.size());
+    } catch (...) {
+        if (workers.empty()) return false;
+    }
+    const int parts = (int)workers.size() + 1;
+    {
+        std::lock_guard<std::mutex> g(mu);
+        job_dst = static_cast<char *>(dst);
+        job_src = static_cast<const char *>(src);
+        job_bytes = bytes;
+        job_parts = parts;
+        pending = (int)workers.size();
+        ++generation;
+    }
+    start_cv.notify_all();
+    copy_part(static_cast<char *>(dst), static_cast<const char *>(src), bytes, 0, parts);
+    std::unique_lock<std::mutex> g(mu);
+    done_cv.wait(g, [&] { return pending == 0; });
+    return true;
+}
+
 int aih_stage(aih_ctx *ctx, const aih_scratch *ext, size_t bytes, void **out)
 {
     if (!ext) return aih_workspace(ctx, bytes, out);
@@ -253,6 +319,11 @@ int aih_memset(aih_ctx *ctx, void *dptr, int value, size_t bytes)
     return AIH_OK;
 }
 
+// Staging fills of at least this many bytes are split over kCopyThreads host
+// threads.
+constexpr size_t kParallelCopyBytes = 2u << 20;
+constexpr int kCopyThreads = 4;
+
 int aih_memcpy_h2d(aih_ctx *ctx, void *dst, const void *src, size_t bytes)
 {
     if (!ctx || ((!dst || !src) && bytes)) return AIH_E_INVALID;
@@ -271,7 +342,18 @@ int aih_memcpy_h2d(aih_ctx *ctx, void *dst, const void *src, size_t bytes)
             AIH_TRY(hipEventSynchronize(ctx->stage_done[slot]));
             ctx->stage_pending[slot] = false;
         }
-        std::memcpy(ctx->stage[slot], s + off, len);
+        // large fills are split over host threads; a pool that cannot start
+        // leaves the copy to this thread
+        bool done = false;
+        if (len >= kParallelCopyBytes) {
+            if (!ctx->copier) ctx->copier.reset(new (std::nothrow) aih_copy_pool());
+            try {
+                if (ctx->copier) done = ctx->copier->copy(ctx->stage[slot], s + off, len, kCopyThreads);
+            } catch (...) {
+                done = false;   // the same bytes are copied again below
+            }
+        }
+        if (!done) std::memcpy(ctx->stage[slot], s + off, len);
         AIH_TRY(hipMemcpyAsync(d + off, ctx->stage[slot], len, hipMemcpyHostToDevice, ctx->stream));
         AIH_TRY(hipEventRecord(ctx->stage_done[slot], ctx->stream));
         ctx->stage_pending[slot] = true;

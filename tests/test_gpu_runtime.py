@@ -69,6 +69,19 @@ def test_upload_tensor_verbatim(device):
     t.dispose()
 
 
+def test_large_upload_verbatim(device):
+    """A transfer of several staging slots, each filled by the host copy
+    threads (slot fills of 2 MiB or more are split over them), arrives byte
+    for byte; so does a second one of another length through the same pool."""
+    rng = np.random.default_rng(7)
+    for n in ((40 << 20) + 12345, (3 << 20) + 7):
+        data = rng.integers(0, 256, n, dtype=np.uint8)
+        b = device.create_buffer(n)
+        assert nat.lib().aih_upload_tensor(device.handle, b.get_pointer(), data.ctypes.data, n) == 0
+        assert np.array_equal(b.read(np.uint8), data)
+        b.dispose()
+
+
 def test_events_time_the_stream(device):
     L = nat.lib()
     b = device.create_buffer(64 << 20)

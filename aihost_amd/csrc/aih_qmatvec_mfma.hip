@@ -93,13 +93,16 @@ __device__ __forceinline__ float f16_bits(uint32_t v)
 {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xFFFFu));
 }
-// (a & mask) | b as one v_and_or_b32 (the mask in an SGPR: a VOP3 encoding
-// takes no literal operand).
+// (a & mask) | b, which the compiler emits as one v_and_or_b32 (mask in an
+// SGPR).  It is written in C, not as inline asm: the compiler's hazard
+// tracking does not see an inline-asm VGPR write, and gfx950 needs 2 wait
+// states between a VALU write and an MFMA reading that VGPR.  The asm form
+// left 1 in places (4 to 13 per Q6_K kernel instantiation), and a build whose
+// schedule differed only elsewhere in the kernel produced wrong Q6_K partial
+// sums at 5..8 columns.
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t b)
 {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(mask), "v"(b));
-    return r;
+    return (a & mask) | b;
 }
 
 // Fragment of 8 codes from two packed words (w0: elements j..j+3 in bytes

@@ -33,9 +33,16 @@ namespace {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
+// Read by dev_pos when the caller passes no position; never written.
+__device__ int32_t no_pos = 0;
+
+// start + *pos, or start when pos is null.  The load goes through a pointer
+// that is never null, so it is not behind a branch: a scalar load inside a
+// branch is waited for before the branch closes, which would put the round
+// trip ahead of every vector load issued after it.
 __device__ __forceinline__ int32_t dev_pos(int32_t start, const int32_t *pos)
 {
-    return pos ? start + *pos : start;
+    return start + *(pos ? pos : &no_pos);
 }
 
 // Cross-lane steps on the DPP path: a few cycles each, where __shfl_xor goes
@@ -363,16 +370,18 @@ constexpr int kHD = 128;      // head_dim supported by the attention kernels
 constexpr int kSub = 64;      // keys per decode sub-chunk (one pass of the score step)
 constexpr int kMaxSplit = 64; // decode splits per head (upper bound)
 constexpr int kQTile = 64;    // queries per prefill workgroup
-constexpr int kSplitKeys = 64;  // keys per decode split while splits stay under kMaxSplit
+constexpr int kSplitKeys = 64;  // keys per decode split of attn_decode_gqa
+constexpr int kShortKeys = 16;  // keys per decode split of attn_decode_short
+constexpr int kShortWaves = 4;  // waves per workgroup of attn_decode_short (at most)
 
-// Decode splits of a cache of max_len rows: ranges of 64 keys until there
-// are kMaxSplit of them, then longer ranges.  (16-key ranges, one wave per
-// split, gave 320 workgroups instead of 80 at 640 rows and 8 KV heads, but
-// the partial kernel stayed at 8.6 us against 8.1 -- it is bound by its
-// memory round trips, not by its parallelism -- and the combine over four
-// times the splits went from 2.6 to 4.0 us.)
+// Decode splits of a cache of max_len rows: ranges of kShortKeys keys
+// (attn_decode_short) while there are at most kMaxSplit of them, else
+// ranges of 64 keys (attn_decode_gqa) until there are kMaxSplit of those,
+// then longer ranges.
 int32_t decode_splits(int32_t max_len)
 {
+    const int32_t ns = (max_len + kShortKeys - 1) / kShortKeys;
+    if (ns <= kMaxSplit) return ns;
     const int32_t n = (max_len + kSplitKeys - 1) / kSplitKeys;
     return n < kMaxSplit ? n : kMaxSplit;
 }
@@ -527,7 +536,40 @@ attn_decode_gqa(const float *__restrict__ Qsrc, float *Kc, float *Vc, float *__r
     const float *kbase = Kc + (int64_t)kvh * kHD + part4 * 32;
     const float *vbase = Vc + (int64_t)kvh * kHD + 2 * lane;
 
-    // first sub-chunk's K and V rows: issued before the position is read
+    // Loads are issued in the order their data is needed and none waits for
+    // the position: the position itself (a scalar load, counted apart from
+    // the vector loads), the query pairs and the new key and value rows, the
+    // first sub-chunk's K and V rows, and last the rotation table's row p.
+    // Vector loads complete in issue order, so the wait for the table also
+    // waits for the K and V rows, which the scores need next anyway.
+    // (Loading the query and the new rows after the position, as the plain
+    // program order would, put up to three more round trips in a row.)
+    const int32_t p = dev_pos(start, pos);
+    float qx[QP][2];
+#pragma unroll
+    for (int i = 0; i < QP; ++i) {
+        const int e = t + NT * i;
+        if (e < G * half) {
+            const float *x = Qsrc + (int64_t)(kvh * G + e / half) * kHD + 2 * (e % half);
+            qx[i][0] = x[0];
+            qx[i][1] = x[1];
+        }
+    }
+    // FUSE: key pair t of the new row by threads t < half, value quad t - v0
+    // by threads v0 .. v0 + kHD / 4 - 1 (v0 = half, or 0 when the workgroup
+    // has fewer than half + kHD / 4 threads)
+    constexpr int v0 = NT >= half + kHD / 4 ? half : 0;
+    const bool kt = FUSE && t < half, vt = FUSE && t >= v0 && t - v0 < kHD / 4;
+    const float *kx = Qsrc + (int64_t)n_heads * kHD + (int64_t)kvh * kHD;
+    const float *vx = kx + kv_stride;
+    float knew[2] = {0.f, 0.f};
+    f4 vnew = {0.f, 0.f, 0.f, 0.f};
+    if (kt) {
+        knew[0] = kx[2 * t];
+        knew[1] = kx[2 * t + 1];
+    }
+    if (vt) vnew = reinterpret_cast<const f4 *>(vx)[t - v0];
+
     f4 k[8];
     float2 v[16];
     auto load_k = [&](int32_t c0) {
@@ -548,24 +590,36 @@ attn_decode_gqa(const float *__restrict__ Qsrc, float *Kc, float *Vc, float *__r
     load_k(j0);
     load_v(j0);
 
-    const int32_t p = dev_pos(start, pos);
     const int32_t L = max(0, min(p + 1, cache_rows));
     const int32_t j1 = min(jc, L);                      // active keys: j0 .. j1-1
     const bool own = FUSE && j0 <= p && p < j1;        // this split holds the new key
     const bool rot = p >= 0 && p < table_rows;
     const float *tp = table + 2 * (int64_t)(rot ? p : 0) * half;
+    float cq[QP][2], ck[2] = {1.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < QP; ++i) {
+        const int e = t + NT * i;
+        cq[i][0] = 1.f;
+        cq[i][1] = 0.f;
+        if (FUSE && rot && e < G * half) {
+            cq[i][0] = tp[2 * (e % half)];
+            cq[i][1] = tp[2 * (e % half) + 1];
+        }
+    }
+    if (kt) {
+        ck[0] = tp[2 * t];
+        ck[1] = tp[2 * t + 1];
+    }
 
     // query heads into LDS (rotated here when FUSE), the new key row when owned
 #pragma unroll
     for (int i = 0; i < QP; ++i) {
         const int e = t + NT * i;
         if (e < G * half) {
-            const int g = e / half, pi = e % half;
-            const float *x = Qsrc + (int64_t)(kvh * G + g) * kHD + 2 * pi;
-            const float x0 = x[0], x1 = x[1];
-            float *y = reinterpret_cast<float *>(&qs[g][0]) + 2 * pi;
+            const float x0 = qx[i][0], x1 = qx[i][1];
+            float *y = reinterpret_cast<float *>(&qs[e / half][0]) + 2 * (e % half);
             if (FUSE && rot) {
-                const float c = tp[2 * pi], sn = tp[2 * pi + 1];
+                const float c = cq[i][0], sn = cq[i][1];
                 y[0] = x0 * c - x1 * sn;
                 y[1] = x0 * sn + x1 * c;
             } else {
@@ -574,28 +628,21 @@ attn_decode_gqa(const float *__restrict__ Qsrc, float *Kc, float *Vc, float *__r
             }
         }
     }
+    // the new key, rotated (stored into the cache at the end: a barrier waits
+    // for every store issued before it)
+    if (kt) {
+        const float c = ck[0], sn = ck[1];
+        const float x0 = knew[0], x1 = knew[1];
+        knew[0] = x0 * c - x1 * sn;
+        knew[1] = x0 * sn + x1 * c;
+    }
     if (own) {
-        const float *kx = Qsrc + (int64_t)n_heads * kHD + (int64_t)kvh * kHD;
-        const float *vx = kx + kv_stride;
-        // key pair e (rotated) by threads e, value quad e by threads half + e
-        // (by threads e too when the workgroup has fewer than half + kHD / 4)
-        constexpr int v0 = NT >= half + kHD / 4 ? half : 0;
-        for (int e = t; e < half; e += NT) {
-            const float c = tp[2 * e], sn = tp[2 * e + 1];
-            const float x0 = kx[2 * e], x1 = kx[2 * e + 1];
-            const float y0 = x0 * c - x1 * sn, y1 = x0 * sn + x1 * c;
-            float *kq = reinterpret_cast<float *>(kn) + 2 * e;
-            kq[0] = y0;
-            kq[1] = y1;
-            float *kc = Kc + (int64_t)p * kv_stride + (int64_t)kvh * kHD + 2 * e;
-            kc[0] = y0;
-            kc[1] = y1;
+        if (kt) {
+            float *kq = reinterpret_cast<float *>(kn) + 2 * t;
+            kq[0] = knew[0];
+            kq[1] = knew[1];
         }
-        for (int e = t - v0; e >= 0 && e < kHD / 4; e += NT) {
-            const f4 vv = reinterpret_cast<const f4 *>(vx)[e];
-            vn[e] = vv;
-            reinterpret_cast<f4 *>(Vc + (int64_t)p * kv_stride + (int64_t)kvh * kHD)[e] = vv;
-        }
+        if (vt) vn[t - v0] = vnew;
     }
     __syncthreads();
 
@@ -706,31 +753,319 @@ attn_decode_gqa(const float *__restrict__ Qsrc, float *Kc, float *Vc, float *__r
             mine[1] = lt;
         }
     }
+    // the split holding key p stores the new key and value rows into the
+    // caches (no other workgroup of this launch reads row p)
+    if (own) {
+        if (kt) {
+            float *kc = Kc + (int64_t)p * kv_stride + (int64_t)kvh * kHD + 2 * t;
+            kc[0] = knew[0];
+            kc[1] = knew[1];
+        }
+        if (vt) reinterpret_cast<f4 *>(Vc + (int64_t)p * kv_stride + (int64_t)kvh * kHD)[t - v0] = vnew;
+    }
+}
+
+// Maximum / sum over aligned groups of N lanes (N = 8, 16, 32 or 64),
+// returned to every lane of the group: DPP within rows of 16, then lane
+// permutes across rows.
+template <int N>
+__device__ __forceinline__ float group_max(float v)
+{
+    v = fmaxf(v, xor1(v));
+    v = fmaxf(v, xor2(v));
+    v = fmaxf(v, __builtin_amdgcn_update_dpp(0.0f, v, 0x141, 0xF, 0xF, false));   // row_half_mirror
+    if (N >= 16) v = fmaxf(v, __builtin_amdgcn_update_dpp(0.0f, v, 0x140, 0xF, 0xF, false));   // row_mirror
+    if (N >= 32) v = fmaxf(v, __shfl_xor(v, 16));
+    if (N >= 64) v = fmaxf(v, __shfl_xor(v, 32));
+    return v;
+}
+template <int N>
+__device__ __forceinline__ float group_sum(float v)
+{
+    v += xor1(v);
+    v += xor2(v);
+    v += __builtin_amdgcn_update_dpp(0.0f, v, 0x141, 0xF, 0xF, false);
+    if (N >= 16) v += __builtin_amdgcn_update_dpp(0.0f, v, 0x140, 0xF, 0xF, false);
+    if (N >= 32) v += __shfl_xor(v, 16);
+    if (N >= 64) v += __shfl_xor(v, 32);
+    return v;
+}
+
+// Decode attention over short splits (at most kShortKeys keys each): the
+// G = n_heads / n_kv_heads query heads of KV head kvh over the keys of split
+// s, in one memory round trip and short dependency chains, so that many
+// small workgroups spread the work over the CUs (attn_decode_gqa's 64-key
+// splits leave one wave per SIMD on a few CUs, with a serial chain of
+// reductions per query head).
+//
+// Lane layout: dq = lane % 4 (a quarter of the head dims), kk = (lane / 4)
+// % KW (a key), g = lane / (4 KW) (a query head), KW = 16 / G keys per wave
+// and sub-step.  Each lane forms the 32-dim partial dot of its quarter, the
+// four quarters are summed by DPP (the same products and order as
+// attn_decode_gqa, so the scores have the same bits), the online softmax of
+// head g is reduced over its 4 KW lanes, and for P.V lane l holds dims
+// 2l, 2l + 1 of every head.  A workgroup of NW waves covers NW KW SUB keys;
+// its K and V rows are all loaded before anything waits.  The new row's
+// RoPE, its cache store and the rotation of the queries are those of
+// attn_decode_gqa (FUSE); the waves are merged through LDS at the end.
+template <int G, bool FUSE, int NW, int SUB>
+__global__ void __launch_bounds__(64 * NW)
+attn_decode_short(const float *__restrict__ Qsrc, float *Kc, float *Vc, float *__restrict__ part, int32_t n_heads,
+                  int32_t n_kv_heads, int32_t start, const int32_t *pos, const float *__restrict__ table,
+                  int32_t table_rows, int32_t cache_rows, float scale, int32_t n_split)
+{
+    constexpr int half = kHD / 2;
+    constexpr int NT = 64 * NW;
+    constexpr int KW = 16 / G;                      // keys per wave and sub-step
+    constexpr int QP = (G * half + NT - 1) / NT;    // query pairs per thread
+    constexpr int QR = kHD + 4;                     // LDS row of a query head (padded)
+    __shared__ __align__(16) float qs[G][QR];
+    __shared__ f4 kn[kHD / 4], vn[kHD / 4];
+    __shared__ __align__(16) float ps[NW][KW][G];
+    __shared__ float wm[NW][G], wl[NW][G];
+    __shared__ float wacc[NW][G][kHD];
+    const int kvh = blockIdx.x, s = blockIdx.y, t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int dq = lane & 3, kk = (lane >> 2) % KW, g = (lane >> 2) / KW;
+    const int64_t kv_stride = (int64_t)n_kv_heads * kHD;
+    const int32_t chunk = (cache_rows + n_split - 1) / n_split;      // <= NW * KW * SUB (host)
+    const int32_t j0 = s * chunk, jc = min(j0 + chunk, cache_rows);   // the split, whatever p
+
+    // loads in the order of attn_decode_gqa: position, query pairs, the new
+    // row, K and V, and the rotation table's row p last
+    const int32_t p = dev_pos(start, pos);
+    float qx[QP][2];
+#pragma unroll
+    for (int i = 0; i < QP; ++i) {
+        const int e = t + NT * i;
+        if (e < G * half) {
+            const float *x = Qsrc + (int64_t)(kvh * G + e / half) * kHD + 2 * (e % half);
+            qx[i][0] = x[0];
+            qx[i][1] = x[1];
+        }
+    }
+    constexpr int v0 = NT >= half + kHD / 4 ? half : 0;
+    const bool kt = FUSE && t < half, vt = FUSE && t >= v0 && t - v0 < kHD / 4;
+    const float *kx = Qsrc + (int64_t)n_heads * kHD + (int64_t)kvh * kHD;
+    const float *vx = kx + kv_stride;
+    float knew[2] = {0.f, 0.f};
+    f4 vnew = {0.f, 0.f, 0.f, 0.f};
+    if (kt) {
+        knew[0] = kx[2 * t];
+        knew[1] = kx[2 * t + 1];
+    }
+    if (vt) vnew = reinterpret_cast<const f4 *>(vx)[t - v0];
+
+    // key of this lane in sub-step sb; the wave's KW keys of sub-step sb
+    auto key_of = [&](int sb) { return j0 + (sb * NW + w) * KW + kk; };
+    auto vkey_of = [&](int sb, int i) { return j0 + (sb * NW + w) * KW + i; };
+    f4 k[SUB][8];
+    float2 v[SUB][KW];
+#pragma unroll
+    for (int sb = 0; sb < SUB; ++sb) {
+        const int32_t j = key_of(sb);
+        if (j < jc) {
+            const f4 *k4 = reinterpret_cast<const f4 *>(Kc + (int64_t)j * kv_stride + (int64_t)kvh * kHD + dq * 32);
+#pragma unroll
+            for (int d = 0; d < 8; ++d) k[sb][d] = k4[d];
+        }
+#pragma unroll
+        for (int i = 0; i < KW; ++i) {
+            const int32_t jv = vkey_of(sb, i);
+            v[sb][i] = jv < jc ? *reinterpret_cast<const float2 *>(Vc + (int64_t)jv * kv_stride + (int64_t)kvh * kHD +
+                                                                   2 * lane)
+                               : float2{0.f, 0.f};
+        }
+    }
+
+    const int32_t L = max(0, min(p + 1, cache_rows));
+    const int32_t j1 = min(jc, L);                      // active keys: j0 .. j1-1
+    const bool own = FUSE && j0 <= p && p < j1;
+    const bool rot = p >= 0 && p < table_rows;
+    const float *tp = table + 2 * (int64_t)(rot ? p : 0) * half;
+    float cq[QP][2], ck[2] = {1.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < QP; ++i) {
+        const int e = t + NT * i;
+        cq[i][0] = 1.f;
+        cq[i][1] = 0.f;
+        if (FUSE && rot && e < G * half) {
+            cq[i][0] = tp[2 * (e % half)];
+            cq[i][1] = tp[2 * (e % half) + 1];
+        }
+    }
+    if (kt) {
+        ck[0] = tp[2 * t];
+        ck[1] = tp[2 * t + 1];
+    }
+#pragma unroll
+    for (int i = 0; i < QP; ++i) {
+        const int e = t + NT * i;
+        if (e < G * half) {
+            const float x0 = qx[i][0], x1 = qx[i][1];
+            float *y = &qs[e / half][2 * (e % half)];
+            if (FUSE && rot) {
+                const float c = cq[i][0], sn = cq[i][1];
+                y[0] = x0 * c - x1 * sn;
+                y[1] = x0 * sn + x1 * c;
+            } else {
+                y[0] = x0;
+                y[1] = x1;
+            }
+        }
+    }
+    if (kt) {
+        const float c = ck[0], sn = ck[1];
+        const float x0 = knew[0], x1 = knew[1];
+        knew[0] = x0 * c - x1 * sn;
+        knew[1] = x0 * sn + x1 * c;
+    }
+    if (own) {
+        if (kt) {
+            float *kq = reinterpret_cast<float *>(kn) + 2 * t;
+            kq[0] = knew[0];
+            kq[1] = knew[1];
+        }
+        if (vt) vn[t - v0] = vnew;
+    }
+    __syncthreads();
+
+    float m_l = -INFINITY, l_l = 0.f;   // running max and sum of head g (same in all its lanes)
+    float2 acc[G];
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg) acc[gg] = float2{0.f, 0.f};
+#pragma unroll
+    for (int sb = 0; sb < SUB; ++sb) {
+        const int32_t jk = key_of(sb);
+        if (own && jk == p) {
+#pragma unroll
+            for (int d = 0; d < 8; ++d) k[sb][d] = kn[dq * 8 + d];
+        }
+#pragma unroll
+        for (int i = 0; i < KW; ++i) {
+            const int32_t jv = vkey_of(sb, i);
+            if (own && jv == p) v[sb][i] = reinterpret_cast<const float2 *>(vn)[lane];
+            // rows past p were loaded before p was known: weight 0 and value 0
+            // (a stale row may hold NaN)
+            if (jv >= j1) v[sb][i] = float2{0.f, 0.f};
+        }
+        float a = 0.f;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            const f4 q = *reinterpret_cast<const f4 *>(&qs[g][dq * 32 + 4 * d]);
+            a = fmaf(q.x, k[sb][d].x, a);
+            a = fmaf(q.y, k[sb][d].y, a);
+            a = fmaf(q.z, k[sb][d].z, a);
+            a = fmaf(q.w, k[sb][d].w, a);
+        }
+        a += xor1(a);
+        a += xor2(a);
+        const float sc = jk < j1 ? a * scale : -INFINITY;
+        const float mn = fmaxf(m_l, group_max<4 * KW>(sc));
+        const float e = jk < j1 ? expf(sc - mn) : 0.f;
+        const float corr = mn == -INFINITY ? 1.f : expf(m_l - mn);
+        l_l = l_l * corr + group_sum<4 * KW>(dq == 0 ? e : 0.f);
+        m_l = mn;
+        if (dq == 0) ps[w][kk][g] = e;
+        // ps[w] is written and read by this wave only (LDS order within a wave)
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg) {
+            const float cg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(corr), 4 * KW * gg));
+            float2 pv = {0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < KW; ++i) {
+                const float pi = ps[w][i][gg];
+                pv.x = fmaf(pi, v[sb][i].x, pv.x);
+                pv.y = fmaf(pi, v[sb][i].y, pv.y);
+            }
+            acc[gg].x = acc[gg].x * cg + pv.x;
+            acc[gg].y = acc[gg].y * cg + pv.y;
+        }
+    }
+
+    if constexpr (NW == 1) {
+        // one wave: its partial is the split's (the merge below would
+        // multiply by e^0 = 1)
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg) {
+            const float mg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m_l), 4 * KW * gg));
+            const float lg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l_l), 4 * KW * gg));
+            float *mine = part + ((int64_t)(kvh * G + gg) * n_split + s) * (kHD + 2);
+            *reinterpret_cast<float2 *>(mine + 2 + 2 * lane) = acc[gg];
+            if (lane == 0) {
+                mine[0] = mg;     // -inf for a split with no key at or before p
+                mine[1] = lg;
+            }
+        }
+    } else {
+        // merge the NW waves: M = max of the wave maxima; weights e^(m_w - M)
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg) {
+            const float mg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m_l), 4 * KW * gg));
+            const float lg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(l_l), 4 * KW * gg));
+            if (lane == 0) {
+                wm[w][gg] = mg;
+                wl[w][gg] = lg;
+            }
+            wacc[w][gg][2 * lane] = acc[gg].x;
+            wacc[w][gg][2 * lane + 1] = acc[gg].y;
+        }
+        __syncthreads();
+        for (int e = t; e < G * kHD; e += NT) {
+            const int gg = e / kHD, d = e % kHD;
+            float M = wm[0][gg];
+#pragma unroll
+            for (int ww = 1; ww < NW; ++ww) M = fmaxf(M, wm[ww][gg]);
+            float o = 0.f, lt = 0.f;
+#pragma unroll
+            for (int ww = 0; ww < NW; ++ww) {
+                const float f = wm[ww][gg] == -INFINITY ? 0.f : expf(wm[ww][gg] - M);
+                o = fmaf(wacc[ww][gg][d], f, o);
+                lt = fmaf(wl[ww][gg], f, lt);
+            }
+            float *mine = part + ((int64_t)(kvh * G + gg) * n_split + s) * (kHD + 2);
+            mine[2 + d] = o;
+            if (d == 0) {
+                mine[0] = M;          // -inf for a split with no key at or before p
+                mine[1] = lt;
+            }
+        }
+    }
+    if (own) {
+        if (kt) {
+            float *kc = Kc + (int64_t)p * kv_stride + (int64_t)kvh * kHD + 2 * t;
+            kc[0] = knew[0];
+            kc[1] = knew[1];
+        }
+        if (vt) reinterpret_cast<f4 *>(Vc + (int64_t)p * kv_stride + (int64_t)kvh * kHD)[t - v0] = vnew;
+    }
 }
 
 // Combine the splits of head h: o = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M).
-// The accumulators of the first kPre splits are loaded together with every
-// split's (m, l) (one memory round trip), the weights go through LDS, and
-// the accumulators of further splits are read eight at a time.
+// NS >= n_split: every split's accumulator element and (m, l) is loaded at
+// once, with no branch (indices past n_split re-read the last split, whose
+// weight is then 0), so the loads take one memory round trip; the weights go
+// through LDS.  The products are summed in split order (the terms past
+// n_split are +0 and change nothing).
+template <int NS>
 __global__ void __launch_bounds__(kHD)
 attn_decode_combine(const float *__restrict__ part, float *__restrict__ O, int32_t n_split)
 {
-    constexpr int kPre = 16;
-    __shared__ float ws[kMaxSplit];
+    __shared__ float ws[NS];
     __shared__ float red[2];
     const int h = blockIdx.x, t = threadIdx.x;
     const float *ph = part + (int64_t)h * n_split * (kHD + 2);
-    float vp[kPre];
+    float vp[NS];
 #pragma unroll
-    for (int u = 0; u < kPre; ++u) vp[u] = u < n_split ? ph[u * (kHD + 2) + 2 + t] : 0.f;
-    const float mt = t < n_split ? ph[t * (kHD + 2)] : -INFINITY;
-    const float lt = t < n_split ? ph[t * (kHD + 2) + 1] : 0.f;
+    for (int u = 0; u < NS; ++u) vp[u] = ph[(u < n_split ? u : n_split - 1) * (kHD + 2) + 2 + t];
+    const int tu = t < n_split ? t : n_split - 1;
+    const float mt = t < n_split ? ph[tu * (kHD + 2)] : -INFINITY;
+    const float lt = t < n_split ? ph[tu * (kHD + 2) + 1] : 0.f;
     float M = wave_max(mt);
     if ((t & 63) == 0) red[t >> 6] = M;
     __syncthreads();
     M = fmaxf(red[0], red[1]);
     const float w = mt == -INFINITY ? 0.f : expf(mt - M);
-    if (t < n_split) ws[t] = w;
+    if (t < NS) ws[t] = w;
     float lw = wave_sum(lt * w);
     __syncthreads();
     if ((t & 63) == 0) red[t >> 6] = lw;
@@ -738,15 +1073,17 @@ attn_decode_combine(const float *__restrict__ part, float *__restrict__ O, int32
     const float lsum = red[0] + red[1];
     float a = 0.f;
 #pragma unroll
-    for (int u = 0; u < kPre; ++u) a = fmaf(vp[u], u < n_split ? ws[u] : 0.f, a);
-    for (int i0 = kPre; i0 < n_split; i0 += 8) {
-        float v[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = i0 + u < n_split ? ph[(i0 + u) * (kHD + 2) + 2 + t] : 0.f;
-#pragma unroll
-        for (int u = 0; u < 8; ++u) a = fmaf(v[u], i0 + u < n_split ? ws[i0 + u] : 0.f, a);
-    }
+    for (int u = 0; u < NS; ++u) a = fmaf(u < n_split ? vp[u] : 0.f, ws[u], a);
     O[(int64_t)h * kHD + t] = lsum > 0.f ? a / lsum : 0.f;
+}
+
+// The combine for n_split <= kMaxSplit splits of n_heads heads.
+void launch_combine(aih_ctx *ctx, const float *part, float *O, int32_t n_heads, int32_t n_split)
+{
+    const dim3 grid(n_heads), block(kHD);
+    if (n_split <= 16) hipLaunchKernelGGL(attn_decode_combine<16>, grid, block, 0, ctx->stream, part, O, n_split);
+    else if (n_split <= 32) hipLaunchKernelGGL(attn_decode_combine<32>, grid, block, 0, ctx->stream, part, O, n_split);
+    else hipLaunchKernelGGL(attn_decode_combine<kMaxSplit>, grid, block, 0, ctx->stream, part, O, n_split);
 }
 
 // Prefill on the fp16 matrix cores with split operands.  Every fp32
@@ -1453,11 +1790,40 @@ int launch_gqa_nw(aih_ctx *ctx, int group, dim3 grid, const float *Qsrc, float *
     return aih_launch_status();
 }
 
+// The short-split kernel: kShortKeys keys per workgroup = NW waves x 16 / G
+// keys x SUB sub-steps, NW = min(G, 4).
+template <bool FUSE, int G>
+void launch_short(aih_ctx *ctx, dim3 grid, const float *Qsrc, float *Kc, float *Vc, float *part, int32_t n_heads,
+                  int32_t n_kv_heads, int32_t start, const int32_t *pos, const float *table, int32_t table_rows,
+                  int32_t cache_rows, float scale, int32_t n_split)
+{
+    constexpr int NWMIN = kShortKeys * G / 64 > 1 ? kShortKeys * G / 64 : 1;   // at most 4 sub-steps
+    constexpr int NW = G < kShortWaves ? G : kShortWaves > NWMIN ? kShortWaves : NWMIN;
+    constexpr int SUB = kShortKeys * G / (16 * NW);
+    static_assert(NW * (16 / G) * SUB == kShortKeys, "short split geometry");
+    hipLaunchKernelGGL((attn_decode_short<G, FUSE, NW, SUB>), grid, dim3(64 * NW), 0, ctx->stream, Qsrc, Kc, Vc, part,
+                       n_heads, n_kv_heads, start, pos, table, table_rows, cache_rows, scale, n_split);
+}
+
 template <bool FUSE>
 int launch_gqa(aih_ctx *ctx, int group, dim3 grid, const float *Qsrc, float *Kc, float *Vc, float *part,
                int32_t n_heads, int32_t n_kv_heads, int32_t start, const int32_t *pos, const float *table,
                int32_t table_rows, int32_t cache_rows, float scale, int32_t n_split)
 {
+    if ((cache_rows + n_split - 1) / n_split <= kShortKeys) {
+        switch (group) {
+        case 1: launch_short<FUSE, 1>(ctx, grid, Qsrc, Kc, Vc, part, n_heads, n_kv_heads, start, pos, table,
+                                      table_rows, cache_rows, scale, n_split); break;
+        case 2: launch_short<FUSE, 2>(ctx, grid, Qsrc, Kc, Vc, part, n_heads, n_kv_heads, start, pos, table,
+                                      table_rows, cache_rows, scale, n_split); break;
+        case 4: launch_short<FUSE, 4>(ctx, grid, Qsrc, Kc, Vc, part, n_heads, n_kv_heads, start, pos, table,
+                                      table_rows, cache_rows, scale, n_split); break;
+        case 8: launch_short<FUSE, 8>(ctx, grid, Qsrc, Kc, Vc, part, n_heads, n_kv_heads, start, pos, table,
+                                      table_rows, cache_rows, scale, n_split); break;
+        default: return AIH_E_UNSUPPORTED;
+        }
+        return aih_launch_status();
+    }
     switch (decode_waves(cache_rows, n_split)) {
     case 1: return launch_gqa_nw<FUSE, 1>(ctx, group, grid, Qsrc, Kc, Vc, part, n_heads, n_kv_heads, start, pos, table,
                                           table_rows, cache_rows, scale, n_split);
@@ -1668,7 +2034,7 @@ int aih_attention_strided(aih_ctx *ctx, const float *Q, int64_t ldq, const float
             rc = aih_launch_status();
         }
         if (rc) return rc;
-        hipLaunchKernelGGL(attn_decode_combine, dim3(n_heads), dim3(kHD), 0, ctx->stream, scratch, O, n_split);
+        launch_combine(ctx, scratch, O, n_heads, n_split);
         return aih_launch_status();
     }
     return prefill_attention(ctx, Q, ldq, Kc, Vc, O, nullptr, n_q, n_heads, n_kv_heads, start, pos, max_len, scale);
@@ -1708,7 +2074,7 @@ int aih_attention_decode_qkv(aih_ctx *ctx, const float *QKV, float *Kc, float *V
     const int rc = launch_gqa<true>(ctx, n_heads / n_kv_heads, dim3(n_kv_heads, n_split), QKV, Kc, Vc, scratch,
                                     n_heads, n_kv_heads, start, pos, table, table_rows, max_len, scale, n_split);
     if (rc) return rc;
-    hipLaunchKernelGGL(attn_decode_combine, dim3(n_heads), dim3(kHD), 0, ctx->stream, scratch, O, n_split);
+    launch_combine(ctx, scratch, O, n_heads, n_split);
     return aih_launch_status();
 }
 

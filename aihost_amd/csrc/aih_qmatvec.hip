@@ -630,8 +630,25 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
     const int ng = (int)ngroups, g = (int)gridDim.x;
     const int c0 = !FUSED && g % 8 == 0 ? (int)(blockIdx.x % 8) * (g / 8) + (int)(blockIdx.x / 8)
                                         : (int)blockIdx.x;
+    // Lane i of the team's first wave stores row (c0 + i*g)*TEAMS + team.
+    const int64_t n = (c0 + (int64_t)lane * g) * TEAMS + team;
+    // The accumulate epilogue's old Y values are loaded here, before the
+    // weights (lanes past the team's rows re-read row N - 1), so that the
+    // kernel does not end on a round trip to Y.
+    float yold[B];
+    if (FUSED && fz.post == kPostAccumulate) {
+#pragma unroll
+        for (int b = 0; b < B; ++b) yold[b] = Y[b * ldy + (n < N ? n : N - 1)];
+    }
     uint32_t ra[T::kRaw], rb[T::kRaw];
+    // The fused decode-step kernels, whose x arrives late (written by the
+    // previous kernel, behind a norm weight last read a token ago), also
+    // load their second row here: the whole 8B-shaped decode step ran 0.5%
+    // faster (1.450 -> 1.444 ms per token).  The plain kernel loads it after
+    // the conversion (below).
+    constexpr bool EARLY2 = FUSED && !SPREAD;
     if constexpr (!SPREAD) load_group(c0, ra);
+    if constexpr (EARLY2) load_group(c0 + g < ng ? c0 + g : c0, rb);
     // keep the weight loads here, in flight during the conversion below
     __builtin_amdgcn_sched_barrier(0);
 
@@ -662,10 +679,10 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
                 const float q = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
                 ss[b] += valid(k) ? q : 0.f;
             }
-            float t = ss[b];
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) t += __shfl_xor(t, o);
-            if (lane == 0) red[wave][b] = t;
+            // DPP steps (a few cycles each; six LDS-permute shuffles cost
+            // about a hundred cycles of latency apiece)
+            const float t = wave_sum_to_lane63(ss[b]);
+            if (lane == 63) red[wave][b] = t;
         }
         if constexpr (SPREAD) {
             __builtin_amdgcn_sched_barrier(0);
@@ -826,8 +843,9 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
     // rows are computed after it with exact loads, so no past-the-end load
     // is issued after the final row (its latency would then be exposed).
     // The second row is loaded only now: issued before the conversion as
-    // well, it measured 0.35 us slower on MI355X for teams of 3-4 rows.
-    load_group(c0 + g < ng ? c0 + g : c0, rb);
+    // well, it measured 0.35 us slower on MI355X for teams of 3-4 rows of
+    // the plain kernel.
+    if constexpr (!EARLY2) load_group(c0 + g < ng ? c0 + g : c0, rb);
     __builtin_amdgcn_sched_barrier(0);
     int c = c0;   // ra holds row group c, rb row group c + g
     while (c + 3 * g < ng) {
@@ -868,7 +886,6 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
             }
         }
     }
-    const int64_t n = (c0 + (int64_t)lane * g) * TEAMS + team;
     if constexpr (FUSED && TEAMS % 2 == 0) {
         if (fz.post == kPostSiluPairs) {
             __shared__ float pair_y[TEAMS][64];
@@ -884,7 +901,7 @@ qmatvec_kernel(const uint8_t *W, int64_t N, int64_t row_bytes, Geom geo,
     if (leader && lane < kept && n < N) {
 #pragma unroll
         for (int b = 0; b < B; ++b)
-            Y[b * ldy + n] = FUSED && fz.post == kPostAccumulate ? Y[b * ldy + n] + yb[b] : yb[b];
+            Y[b * ldy + n] = FUSED && fz.post == kPostAccumulate ? yold[b] + yb[b] : yb[b];
     }
 }
 

@@ -169,6 +169,12 @@ struct G4K32 {
     }
     // chunk column of out[q] for half ph
     __device__ static constexpr int col(int ph, int q) { return 16 * ph + 8 * (q & 1) + 32 * (q >> 1); }
+    // LDS position (in 16-byte granules) of chunk granule g = 8 pc + col / 8:
+    // with g = 16a + 8b + 4c + 2d + e, position e + 2d + 4b + 8a + 16c, so
+    // that the eight lanes of a row store one piece q to eight positions of
+    // one parity, 16 apart from none: with rows 33 granules apart, the 16
+    // lanes of two rows then reach 16 different bank groups.
+    __device__ static constexpr int swz(int g) { return (g & 3) | (((g >> 3) & 3) << 2) | (((g >> 2) & 1) << 4); }
 };
 
 // Q6_K: chunk c covers half h = (c % 4) / 2 of block c / 4, quarters
@@ -314,6 +320,12 @@ struct Pair32 {
     }
     __device__ static void piece(const Raw &r, int c, int ph, h8 out[4]);
     __device__ static constexpr int col(int ph, int q) { return 32 * ph + 8 * q; }
+    // LDS position of chunk granule g = 16a + 8b + 4ph + 2q1 + q0 (see
+    // G4K32::swz): q0 + 2ph + 4b + 8a + 16q1
+    __device__ static constexpr int swz(int g)
+    {
+        return (g & 1) | (((g >> 2) & 1) << 1) | (((g >> 3) & 3) << 2) | (((g >> 1) & 1) << 4);
+    }
 };
 
 // The GEMM producers' piece type for format T.

@@ -249,9 +249,12 @@ qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
                 h8 lo, hi;
                 piece16h<T>(r[i], c, ps, lo, hi);
                 if (decltype(tail)::value && c >= nch) lo = hi = h8{};
-                _Float16 *d = &wsh[buf][16 * pw + 4 * i + rl][64 * pc + 16 * ps];
-                *reinterpret_cast<h8 *>(d) = lo;
-                *reinterpret_cast<h8 *>(d + 8) = hi;
+                // chunk granules 8 pc + 2 ps (lo) and + 1 (hi) at LDS
+                // granules 4 pc + ps and 16 + 4 pc + ps: the 16 lanes of a
+                // row store 256 contiguous bytes (no bank conflict)
+                _Float16 *d = &wsh[buf][16 * pw + 4 * i + rl][0];
+                *reinterpret_cast<h8 *>(d + 8 * (4 * pc + ps)) = lo;
+                *reinterpret_cast<h8 *>(d + 8 * (16 + 4 * pc + ps)) = hi;
             }
         };
         typename T::Raw ring[PR][4];
@@ -309,8 +312,8 @@ qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
     auto bload = [&](int buf, int t, BF &b) {
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-            b.b0[kk] = *reinterpret_cast<const h8 *>(&wsh[buf][fr][64 * t + 16 * kk + fk]);
-            b.b1[kk] = *reinterpret_cast<const h8 *>(&wsh[buf][32 + fr][64 * t + 16 * kk + fk]);
+            b.b0[kk] = *reinterpret_cast<const h8 *>(&wsh[buf][fr][8 * (2 * fk + 4 * t + kk)]);
+            b.b1[kk] = *reinterpret_cast<const h8 *>(&wsh[buf][32 + fr][8 * (2 * fk + 4 * t + kk)]);
         }
     };
     auto mm = [&](const AF &f, const BF &b) {
@@ -412,10 +415,11 @@ qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
         const int c = (ss0 + ss) * SC + pc;
         h8 o[4];
         Pc::piece(r[0], c, ph, o);
-        _Float16 *d = &wsh[buf][8 * wave + rl][64 * pc];
+        _Float16 *d = &wsh[buf][8 * wave + rl][0];
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-            *reinterpret_cast<h8 *>(d + Pc::col(ph, q)) = decltype(tail)::value && c >= nch ? h8{} : o[q];
+            *reinterpret_cast<h8 *>(d + 8 * Pc::swz(8 * pc + Pc::col(ph, q) / 8)) =
+                decltype(tail)::value && c >= nch ? h8{} : o[q];
     };
 
     // multiplication share: rows 32 MB wave .. +32 MB - 1 of the M tile
@@ -445,8 +449,8 @@ qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
     auto bload = [&](int buf, int t, BF &b) {
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-            b.b0[kk] = *reinterpret_cast<const h8 *>(&wsh[buf][fr][64 * t + 16 * kk + fk]);
-            b.b1[kk] = *reinterpret_cast<const h8 *>(&wsh[buf][32 + fr][64 * t + 16 * kk + fk]);
+            b.b0[kk] = *reinterpret_cast<const h8 *>(&wsh[buf][fr][8 * Pc::swz(8 * t + 2 * kk + fk / 8)]);
+            b.b1[kk] = *reinterpret_cast<const h8 *>(&wsh[buf][32 + fr][8 * Pc::swz(8 * t + 2 * kk + fk / 8)]);
         }
     };
     auto mm = [&](const AF &f, const BF &b) {

@@ -485,6 +485,10 @@ qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
         };
         if (BD == 2) bload(buf, 0, bb[0]);
         if (valu_first) deq();
+        // the multiplying half at raised wave priority, so that the SIMD
+        // issues its MFMAs ahead of the other wave's dequantization when both
+        // are ready (6144 x 4096 and 28672 x 4096 at M = 512: 2% faster)
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int t = 0; t < SC; ++t) {
             if (BD == 1)
@@ -496,6 +500,7 @@ qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
             aload(SC * it + t + AD, f[t % AD]);
             __builtin_amdgcn_sched_barrier(0);
         }
+        __builtin_amdgcn_s_setprio(0);
         if (!valu_first) deq();
         __builtin_amdgcn_sched_barrier(0);
         lds_barrier();

@@ -371,8 +371,8 @@ constexpr int kSub = 64;      // keys per decode sub-chunk (one pass of the scor
 constexpr int kMaxSplit = 64; // decode splits per head (upper bound)
 constexpr int kQTile = 64;    // queries per prefill workgroup
 constexpr int kSplitKeys = 64;  // keys per decode split of attn_decode_gqa
-constexpr int kShortKeys = 16;  // keys per decode split of attn_decode_short
-constexpr int kShortWaves = 4;  // waves per workgroup of attn_decode_short (at most)
+constexpr int kShortKeys = 32;  // keys per decode split of attn_decode_short
+constexpr int kShortWaves = 8;  // waves per workgroup of attn_decode_short (at most)
 
 // Decode splits of a cache of max_len rows: ranges of kShortKeys keys
 // (attn_decode_short) while there are at most kMaxSplit of them, else
@@ -1791,14 +1791,16 @@ int launch_gqa_nw(aih_ctx *ctx, int group, dim3 grid, const float *Qsrc, float *
 }
 
 // The short-split kernel: kShortKeys keys per workgroup = NW waves x 16 / G
-// keys x SUB sub-steps, NW = min(G, 4).
+// keys x SUB sub-steps, NW = min(2 G, 8).  (Groups of 4 heads at 640 cache
+// rows, decode step of the 8B-shaped decoder: 8 waves x 4 keys ran 1.431
+// ms per token, 4 waves x 4 keys 1.449, 8 waves x 8 keys 1.486 and 16
+// waves x 4 keys 1.515.)
 template <bool FUSE, int G>
 void launch_short(aih_ctx *ctx, dim3 grid, const float *Qsrc, float *Kc, float *Vc, float *part, int32_t n_heads,
                   int32_t n_kv_heads, int32_t start, const int32_t *pos, const float *table, int32_t table_rows,
                   int32_t cache_rows, float scale, int32_t n_split)
 {
-    constexpr int NWMIN = kShortKeys * G / 64 > 1 ? kShortKeys * G / 64 : 1;   // at most 4 sub-steps
-    constexpr int NW = G < kShortWaves ? G : kShortWaves > NWMIN ? kShortWaves : NWMIN;
+    constexpr int NW = kShortKeys * G / 16 < kShortWaves ? kShortKeys * G / 16 : kShortWaves;
     constexpr int SUB = kShortKeys * G / (16 * NW);
     static_assert(NW * (16 / G) * SUB == kShortKeys, "short split geometry");
     hipLaunchKernelGGL((attn_decode_short<G, FUSE, NW, SUB>), grid, dim3(64 * NW), 0, ctx->stream, Qsrc, Kc, Vc, part,

@@ -70,6 +70,8 @@ SIGNATURES = {
     "aih_qgemm": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),
     "aih_qgemm_fused": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _vp, _f, _i64, _i, _i, _vp]),
     "aih_matmul_weights_q": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),
+    "aih_qgemm_qkv_rope": (_i, [_vp, _i, _vp, _i64, _vp, _vp, _f, _i64, _i, _vp, _vp, _vp, ctypes.c_int32,
+                                ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _vp, _vp, ctypes.c_int32, _i64]),
     "aih_operand_bytes": (_i64, [_i64, _i64]),
     "aih_qgemm_plan": (_i, [_vp, _i64, _i64, _i64, _i, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)]),
     "aih_matmul_weights_q_noalloc": (_i, [_vp, _i, _vp, _i64, _i64, _vp, _i64, _vp]),

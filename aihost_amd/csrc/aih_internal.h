@@ -146,10 +146,24 @@ int aih_launch_x_tile(aih_ctx *ctx, const float *X, int64_t M, int64_t K, void *
 int aih_launch_x_tile_pre(aih_ctx *ctx, int pre, const float *X, const float *X2, float eps, int64_t M, int64_t K,
                           void *Xt);
 int aih_launch_operand_fixup(aih_ctx *ctx, void *Xt, int64_t M, int64_t K);
+// The Q|K|V epilogue (epi 3): for output columns [0, qd) the rotated queries
+// into Y, for [qd, qd + kvd) the rotated keys and for [qd + kvd, qd + 2 kvd)
+// the values into the caches at row p = start (+ *pos) + m, with the
+// arithmetic and the row conditions of aih_rope_qkv.
+struct aih_rope_qkv_args {
+    float *Kc = nullptr, *Vc = nullptr;
+    const float *table = nullptr;
+    const int32_t *pos = nullptr;
+    int64_t cache_rows = 0;
+    int32_t start = 0, qd = 0, kvd = 0, head_dim = 0, table_rows = 0;
+};
+
 // may_split: the GEMM may split K over workgroups, with partial sums in the
 // second workspace and a reduction (never with caller-provided staging).
+// rope: the epilogue's arguments for epi 3 (else unused).
 int aih_launch_qgemm_tiled(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const void *Xt,
-                           int64_t M, float *Y, int epi, bool may_split = false);
+                           int64_t M, float *Y, int epi, bool may_split = false,
+                           const aih_rope_qkv_args *rope = nullptr);
 int aih_launch_qmatvec_mfma(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
                             const float *X, int64_t ldx, float *Y, int64_t ldy, int batch,
                             const aih_scratch *ext = nullptr);

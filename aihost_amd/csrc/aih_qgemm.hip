@@ -58,7 +58,7 @@ __device__ __forceinline__ void lds_barrier()
 }
 
 // Epilogues: 0 store Y, 1 add into Y, 2 the SiLU-pairs operand (below).
-constexpr int kEpiStore = 0, kEpiAccumulate = 1, kEpiSiluOperand = 2;
+constexpr int kEpiStore = 0, kEpiAccumulate = 1, kEpiSiluOperand = 2, kEpiRopeQKV = 3;
 
 // SiLU(gate) * up of a wave's 32 x 64 output block whose column pairs
 // (2j, 2j+1) are gate and up rows (W interleaved), written as the fp16
@@ -189,6 +189,78 @@ __device__ __forceinline__ void store_tile(const f16v &acc0, const f16v &acc1, i
     }
 }
 
+// The Q|K|V epilogue (aih_rope_qkv_args): a wave's two 32 x 32 blocks
+// (rows mrow0 .., columns n0 + lane % 32 and + 32) rotated and stored as
+// aih_rope_qkv would rotate and store the stored product: for query and key
+// columns the pair (2i, 2i + 1) of a head (adjacent lanes) becomes
+// (x0 c - x1 s, x0 s + x1 c) with (c, s) the table's row p, pair i; queries
+// go to Y (unrotated when p is outside the table), keys and values to the
+// caches' row p (nothing outside the table or past the cache).  The head
+// boundaries fall on multiples of 32 columns, so a block is one kind.
+__device__ __forceinline__ void rope_qkv_block(const f16v acc, int lane, int64_t mrow0, int64_t nb0, int64_t M,
+                                               int64_t N, float *__restrict__ Y, const aih_rope_qkv_args ra)
+{
+#pragma clang fp contract(off)
+    if (nb0 >= N) return;
+    const int32_t p0 = ra.start + (ra.pos ? *ra.pos : 0);
+    const int64_t n = nb0 + (lane & 31);
+    // query, key or value: the same for the whole block (wave-uniform)
+    const int kind = nb0 < ra.qd ? 0 : nb0 < (int64_t)ra.qd + ra.kvd ? 1 : 2;
+    const int64_t cn = kind == 0 ? n : kind == 1 ? n - ra.qd : n - ra.qd - ra.kvd;
+    auto row = [&](int r) { return mrow0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); };
+    if (kind == 2) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t m = row(r), p = (int64_t)p0 + m;
+            if (m < M && p >= 0 && p < ra.table_rows && p < ra.cache_rows) ra.Vc[p * ra.kvd + cn] = acc[r];
+        }
+        return;
+    }
+    // the rows' cos/sin, all loads issued before the first use (rows outside
+    // the table read row 0 and are not rotated)
+    const int half = ra.head_dim / 2;
+    const int i = (int)(cn % ra.head_dim) / 2;
+    float cv[16], sv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int64_t p = (int64_t)p0 + row(r);
+        const int64_t pt = p >= 0 && p < ra.table_rows ? p : 0;
+        const float2 t = *reinterpret_cast<const float2 *>(ra.table + 2 * (pt * half + i));
+        cv[r] = t.x;
+        sv[r] = t.y;
+    }
+    const bool odd = lane & 1;
+    float v[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        // the pair's other element, from the neighbouring lane
+        const float other = __builtin_amdgcn_update_dpp(0.0f, acc[r], 0xB1, 0xF, 0xF, false);
+        const float x0 = odd ? other : acc[r], x1 = odd ? acc[r] : other;
+        v[r] = odd ? x0 * sv[r] + x1 * cv[r] : x0 * cv[r] - x1 * sv[r];
+    }
+    if (kind == 0) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t m = row(r), p = (int64_t)p0 + m;
+            if (m < M) Y[m * N + n] = p >= 0 && p < ra.table_rows ? v[r] : acc[r];
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t m = row(r), p = (int64_t)p0 + m;
+            if (m < M && p >= 0 && p < ra.table_rows && p < ra.cache_rows) ra.Kc[p * ra.kvd + cn] = v[r];
+        }
+    }
+}
+
+__device__ __forceinline__ void rope_qkv_tile(const f16v &acc0, const f16v &acc1, int lane, int64_t mrow0, int64_t n0,
+                                              int64_t M, int64_t N, float *__restrict__ Y,
+                                              const aih_rope_qkv_args ra)
+{
+    rope_qkv_block(acc0, lane, mrow0, n0, M, N, Y, ra);
+    rope_qkv_block(acc1, lane, mrow0, n0 + 32, M, N, Y, ra);
+}
+
 // Eight waves per workgroup in two roles, one of each on every SIMD; the
 // workgroup owns a 128 (M) x 64 (N) tile of Y and walks K in super-steps of
 // 256 (a Q4_K/Q6_K super-block, 8 blocks of Q8_0/Q4_0), with one LDS barrier
@@ -215,7 +287,7 @@ template <> struct GRing<G6K> { static constexpr int PR = 2; };
 template <class T>
 __global__ void __launch_bounds__(512)
 qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
-             const _Float16 *__restrict__ Xt, int64_t M, float *__restrict__ Y, int epi)
+             const _Float16 *__restrict__ Xt, int64_t M, float *__restrict__ Y, int epi, aih_rope_qkv_args ra)
 {
     constexpr int PR = GRing<T>::PR;
     __shared__ __align__(16) _Float16 wsh[2][BN][LD2];
@@ -361,6 +433,10 @@ qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
                            reinterpret_cast<_Float16 *>(Y));
         return;
     }
+    if (epi == kEpiRopeQKV) {
+        rope_qkv_tile(acc0, acc1, lane, m0 + 32 * wave, n0, M, N, Y, ra);
+        return;
+    }
     store_tile(acc0, acc1, lane, m0 + 32 * wave, n0, M, N, Y, epi == kEpiAccumulate);
 }
 
@@ -386,7 +462,7 @@ template <class T, int MB, int AD>
 __global__ void __launch_bounds__(512)
 qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
                 const _Float16 *__restrict__ Xt, int64_t M, float *__restrict__ Y, int epi,
-                float *__restrict__ P, int ssper)
+                float *__restrict__ P, int ssper, aih_rope_qkv_args ra)
 {
     static_assert(SC % AD == 0, "A ring depth divides a super-step");
     constexpr int PR = PR256;
@@ -546,6 +622,11 @@ qgemm256_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
         }
         return;
     }
+    if (epi == kEpiRopeQKV) {   // never split (the plan does not split this epilogue)
+#pragma unroll
+        for (int j = 0; j < MB; ++j) rope_qkv_tile(acc[j][0], acc[j][1], lane, m0 + 32 * (MB * wave + j), n0, M, N, Y, ra);
+        return;
+    }
     // a split's partial sums are stored (the summing pass adds them into Y)
     float *const Pz = P ? P + (int64_t)blockIdx.z * M * N : nullptr;
 #pragma unroll
@@ -659,7 +740,7 @@ GemmPlan plan_gemm(int64_t cu_count, int64_t N, int64_t K, int64_t M, int epi, b
     const int nss = (int)((K / 64 + SC - 1) / SC);
     GemmPlan p;
     p.ssper = nss;
-    if (may_split && epi != kEpiSiluOperand && M > BM2 && gx * gy4 < cus && M * N % 4 == 0) {
+    if (may_split && epi != kEpiSiluOperand && epi != kEpiRopeQKV && M > BM2 && gx * gy4 < cus && M * N % 4 == 0) {
         const int want = (int)std::min<int64_t>(std::min<int64_t>(cus / (gx * gy4), nss / 2), 8);
         if (want >= 2) {
             const int ssper = (nss + want - 1) / want;
@@ -681,7 +762,7 @@ GemmPlan plan_gemm(int64_t cu_count, int64_t N, int64_t K, int64_t M, int epi, b
 
 template <class T>
 int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
-           const _Float16 *Xh, int64_t M, float *Y, int epi, bool may_split)
+           const _Float16 *Xh, int64_t M, float *Y, int epi, bool may_split, const aih_rope_qkv_args &ra)
 {
     const int64_t gx = (N + BN - 1) / BN, gy = (M + BM - 1) / BM, gy2 = (M + BM2 - 1) / BM2;
     const int64_t gy4 = (M + 2 * BM2 - 1) / (2 * BM2);
@@ -696,7 +777,7 @@ int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t row_byt
         if (rc) return rc;
         hipLaunchKernelGGL((qgemm256_kernel<T, 2, 2>), dim3((unsigned)gx, (unsigned)gy4, (unsigned)p.splits),
                            dim3(512), 0, ctx->stream, W, N, K, row_bytes, Xh, M, Y, epi, static_cast<float *>(ws),
-                           p.ssper);
+                           p.ssper, ra);
         rc = aih_launch_status();
         if (rc) return rc;
         const int64_t cus = ctx->cu_count > 0 ? ctx->cu_count : 256;
@@ -712,30 +793,31 @@ int launch(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t row_byt
     }
     if (p.tile == 512)
         hipLaunchKernelGGL((qgemm256_kernel<T, 2, 2>), dim3((unsigned)gx, (unsigned)gy4), dim3(512), 0, ctx->stream,
-                           W, N, K, row_bytes, Xh, M, Y, epi, nullptr, p.ssper);
+                           W, N, K, row_bytes, Xh, M, Y, epi, nullptr, p.ssper, ra);
     else if (p.tile == 256)
         hipLaunchKernelGGL((qgemm256_kernel<T, 1, SC>), dim3((unsigned)gx, (unsigned)gy2), dim3(512), 0, ctx->stream,
-                           W, N, K, row_bytes, Xh, M, Y, epi, nullptr, p.ssper);
+                           W, N, K, row_bytes, Xh, M, Y, epi, nullptr, p.ssper, ra);
     else
         hipLaunchKernelGGL((qgemm_kernel<T>), dim3((unsigned)gx, (unsigned)gy), dim3(512), 0, ctx->stream,
-                           W, N, K, row_bytes, Xh, M, Y, epi);
+                           W, N, K, row_bytes, Xh, M, Y, epi, ra);
     return aih_launch_status();
 }
 
 }  // namespace
 
 int aih_launch_qgemm_tiled(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const void *Xtv,
-                           int64_t M, float *Y, int epi, bool may_split)
+                           int64_t M, float *Y, int epi, bool may_split, const aih_rope_qkv_args *rope)
 {
+    const aih_rope_qkv_args ra = rope ? *rope : aih_rope_qkv_args{};
     if (K % BK != 0) return AIH_E_LIMIT;
     const int64_t rb = aih_row_bytes(type, K);
     const uint8_t *w = static_cast<const uint8_t *>(W);
     const _Float16 *Xt = static_cast<const _Float16 *>(Xtv);
     switch (type) {
-    case AIH_TYPE_Q4_K: return launch<G4K>(ctx, w, N, K, rb, Xt, M, Y, epi, may_split);
-    case AIH_TYPE_Q6_K: return launch<G6K>(ctx, w, N, K, rb, Xt, M, Y, epi, may_split);
-    case AIH_TYPE_Q8_0: return launch<G80>(ctx, w, N, K, rb, Xt, M, Y, epi, may_split);
-    case AIH_TYPE_Q4_0: return launch<G40>(ctx, w, N, K, rb, Xt, M, Y, epi, may_split);
+    case AIH_TYPE_Q4_K: return launch<G4K>(ctx, w, N, K, rb, Xt, M, Y, epi, may_split, ra);
+    case AIH_TYPE_Q6_K: return launch<G6K>(ctx, w, N, K, rb, Xt, M, Y, epi, may_split, ra);
+    case AIH_TYPE_Q8_0: return launch<G80>(ctx, w, N, K, rb, Xt, M, Y, epi, may_split, ra);
+    case AIH_TYPE_Q4_0: return launch<G40>(ctx, w, N, K, rb, Xt, M, Y, epi, may_split, ra);
     default: return AIH_E_UNSUPPORTED;
     }
 }

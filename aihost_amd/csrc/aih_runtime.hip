@@ -663,6 +663,51 @@ int aih_qgemm_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K,
     return aih_launch_qgemm_tiled(ctx, type, W, N, K, work, M, Y, epi, true);
 }
 
+int aih_qgemm_qkv_rope(aih_ctx *ctx, int type, const void *W, int64_t K, const float *X, const float *X2, float eps,
+                       int64_t M, int pre, float *Q, float *Kc, float *Vc, int32_t n_heads, int32_t n_kv_heads,
+                       int32_t head_dim, int32_t start, const int32_t *pos, const float *table, int32_t table_rows,
+                       int64_t cache_rows)
+{
+    if (!ctx) return AIH_E_INVALID;
+    if (!aih_is_quant(type)) return AIH_E_UNSUPPORTED;
+    aih_block_geom g = aih_geom(type);
+    if (M < 0 || K <= 0 || K % g.elems) return AIH_E_INVALID;
+    if (n_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || head_dim % 2) return AIH_E_INVALID;
+    if (pre != AIH_PRE_NONE && pre != AIH_PRE_RMSNORM) return AIH_E_INVALID;
+    if (pre == AIH_PRE_RMSNORM && !X2) return AIH_E_INVALID;
+    // a 32-column block of the product is all queries, all keys or all values
+    if (head_dim % 32) return AIH_E_UNSUPPORTED;
+    const int64_t qd = (int64_t)n_heads * head_dim, kvd = (int64_t)n_kv_heads * head_dim;
+    if (qd + 2 * kvd > 0x7FFFFFFF) return AIH_E_LIMIT;
+    if (!M) return AIH_OK;
+    if (!W || !X || !Q || !Kc || !Vc || !table) return AIH_E_INVALID;
+    if (!pos && (start < 0 || start + M > table_rows || start + M > cache_rows)) return AIH_E_LIMIT;
+    if (K % 64 != 0) return AIH_E_LIMIT;
+    if (reinterpret_cast<uintptr_t>(X) % 16 || (X2 && reinterpret_cast<uintptr_t>(X2) % 16) ||
+        reinterpret_cast<uintptr_t>(table) % 8)
+        return AIH_E_INVALID;
+    int rc = select_device(ctx);
+    if (rc) return rc;
+    void *work = nullptr;
+    rc = aih_stage(ctx, nullptr, (size_t)aih_operand::image_bytes(aih_operand::mpad_of(M), K, false), &work);
+    if (rc) return rc;
+    rc = pre == AIH_PRE_NONE ? aih_launch_x_tile(ctx, X, M, K, work)
+                             : aih_launch_x_tile_pre(ctx, pre, X, X2, eps, M, K, work);
+    if (rc) return rc;
+    aih_rope_qkv_args ra;
+    ra.Kc = Kc;
+    ra.Vc = Vc;
+    ra.table = table;
+    ra.pos = pos;
+    ra.cache_rows = cache_rows;
+    ra.start = start;
+    ra.qd = (int32_t)qd;
+    ra.kvd = (int32_t)kvd;
+    ra.head_dim = head_dim;
+    ra.table_rows = table_rows;
+    return aih_launch_qgemm_tiled(ctx, type, W, qd + 2 * kvd, K, work, M, Q, 3, false, &ra);
+}
+
 int64_t aih_operand_bytes(int64_t M, int64_t K)
 {
     if (M < 0 || K <= 0 || K % 64) return AIH_E_INVALID;

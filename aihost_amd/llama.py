@@ -294,9 +294,9 @@ class LlamaDecoder:
                   "fused GEMM %s" % name)
 
     def _prefill_layer_fused(self, l, rows, start, pos):
-        """One layer over `rows` > 8 prompt rows in six GEMM-centred steps: the
-        Q|K|V GEMM with the attention RMSNorm computed into its operand, RoPE
-        and the cache store, attention reading the query block in place and
+        """One layer over `rows` > 8 prompt rows in five GEMM-centred steps: the
+        Q|K|V GEMM with the attention RMSNorm computed into its operand and
+        RoPE and the cache store in its epilogue, attention reading the query block in place and
         writing the W_o GEMM's fp16 operand, the W_o GEMM adding into x, the gate|up GEMM with the FFN RMSNorm in its
         operand and SiLU(gate)*up written as the down GEMM's fp16 operand, the
         down GEMM adding into x.
@@ -308,12 +308,14 @@ class LlamaDecoder:
         c, L, h, p = self.cfg, self.L, self.h, "blk.%d." % l
         qd = c.n_heads * c.head_dim
         ld = qd + 2 * c.kv_dim
-        self._mmx(p + "attn_qkv", self.x, self.w.ptr(p + "attn_norm"), nat.PRE_RMSNORM, nat.POST_STORE, rows,
-                  self.qkv)
-        q, k, v = self.qkv, self.qkv + qd * 4, self.qkv + (qd + c.kv_dim) * 4
-        nat.check(L.aih_rope_qkv(h, q, ld, k, ld, v, ld, self.kc[l], self.vc[l], rows, c.n_heads, c.n_kv_heads,
-                                 c.head_dim, start, pos, self.table, self.max_len, self.max_len),
-                  "rope q, k -> cache, v -> cache")
+        # the Q|K|V GEMM with RoPE and the cache store in its epilogue (aih_qgemm_fused + aih_rope_qkv)
+        qt, wp, n, k = self.w[p + "attn_qkv"]
+        assert n == ld
+        nat.check(L.aih_qgemm_qkv_rope(h, qt, wp, k, self.x, self.w.ptr(p + "attn_norm"), c.eps, rows,
+                                       nat.PRE_RMSNORM, self.qkv, self.kc[l], self.vc[l], c.n_heads, c.n_kv_heads,
+                                       c.head_dim, start, pos, self.table, self.max_len, self.max_len),
+                  "Q|K|V GEMM + rope -> cache")
+        q = self.qkv
         nat.check(L.aih_attention_operand(h, q, ld, self.kc[l], self.vc[l], self.att16, rows, c.n_heads,
                                           c.n_kv_heads, c.head_dim, start, pos, self.max_len, self.scale),
                   "attention")

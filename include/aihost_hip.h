@@ -300,6 +300,25 @@ int aih_matmul_weights_q(aih_ctx *ctx, int type, const void *W, int64_t N, int64
 int aih_qgemm_fused(aih_ctx *ctx, int type, const void *W, int64_t N, int64_t K, const float *X,
                     const float *X2, float eps, int64_t M, int pre, int post, float *Y);
 
+/* The prompt's Q|K|V projection with the position steps in its epilogue:
+ * the same results, bit for bit, as aih_qgemm_fused(type, W, N = q_dim +
+ * 2 kv_dim, K, X, X2, eps, M, pre, AIH_POST_STORE, Q) followed by
+ * aih_rope_qkv(Q, N, Q + q_dim, N, Q + q_dim + kv_dim, N, Kc, Vc, M, n_heads,
+ * n_kv_heads, head_dim, start, pos, table, table_rows, cache_rows), with
+ * q_dim = n_heads*head_dim and kv_dim = n_kv_heads*head_dim, but one GEMM
+ * launch writes the rotated queries into Q (M rows of N floats) and the
+ * rotated keys and the values straight into the caches; the key and value
+ * columns of Q are not written.  pre is AIH_PRE_NONE or AIH_PRE_RMSNORM;
+ * head_dim a multiple of 32 (else AIH_E_UNSUPPORTED); X, X2 16-byte and table
+ * 8-byte aligned.  Replaces, for a
+ * prompt, the Q/K/V MatMulWeights, ApplyRoPEFull and the KV cache append of
+ * ComputeOps.TransformerLayer (ComputeOps.cs:1250-1356, ComputeOps.cs:959-979,
+ * InferenceEngine.cs:598-622). */
+int aih_qgemm_qkv_rope(aih_ctx *ctx, int type, const void *W, int64_t K, const float *X, const float *X2, float eps,
+                       int64_t M, int pre, float *Q, float *Kc, float *Vc, int32_t n_heads, int32_t n_kv_heads,
+                       int32_t head_dim, int32_t start, const int32_t *pos, const float *table, int32_t table_rows,
+                       int64_t cache_rows);
+
 /* Bytes of the fp16 operand image of an M x K activation matrix (K a
  * multiple of 64) that AIH_POST_SILU_PAIRS_F16 and aih_attention_operand
  * write and AIH_PRE_F16_OPERAND reads: the values in the matrix cores'

@@ -8,6 +8,7 @@
   aih_attention on a contiguous copy;
 - aih_attention_operand vs aih_attention_strided's fp32 output rounded into
   the GEMM operand layout, and the W_o GEMM from either;
+- aih_qgemm_qkv_rope vs aih_qgemm_fused + aih_rope_qkv (queries and caches);
 - a decoder prefill through the fused layer vs the same prompt through the
   separate operators: logits and K/V caches identical.
 """
@@ -182,6 +183,90 @@ def test_qgemm_fused_argument_errors(device):
             b.dispose()
 
 
+# (n_heads, n_kv_heads, K, M, start, device position, table rows, cache rows, pre, type): the 128-row and
+# wider tiles, a device position, and positions past the cache (no K/V store) and past the table (queries
+# left unrotated, nothing stored)
+QKV_CASES = [(4, 2, 256, 40, 0, None, 64, 64, nat.PRE_RMSNORM, nat.Q4_K),
+             (8, 2, 512, 300, 5, None, 400, 400, nat.PRE_NONE, nat.Q6_K),
+             (32, 8, 4096, 512, 0, 3, 640, 640, nat.PRE_RMSNORM, nat.Q4_K),
+             (4, 2, 256, 70, 0, 40, 100, 80, nat.PRE_RMSNORM, nat.Q8_0)]
+
+
+@pytest.mark.parametrize("nh,nkv,k,m,start,dpos,trows,crows,pre,qtype", QKV_CASES)
+def test_qkv_rope_gemm_equals_gemm_then_rope(device, nh, nkv, k, m, start, dpos, trows, crows, pre, qtype):
+    """aih_qgemm_qkv_rope against aih_qgemm_fused (store) + aih_rope_qkv: the
+    rotated queries and both caches bit for bit; the key and value columns of
+    its Q are left as they were."""
+    L, h = nat.lib(), device.handle
+    hd = 128
+    qd, kvd = nh * hd, nkv * hd
+    n = qd + 2 * kvd
+    rng = np.random.default_rng(nh + k + m)
+    w = synth_weight(qtype, n, k, seed=k + 1)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    nw = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    cache0 = rng.standard_normal((crows, kvd)).astype(np.float32)
+    q0 = np.full((m, n), 7.0, np.float32)
+    bufs = [upload(device, a) for a in (w, x, nw, cache0, cache0, cache0, cache0, q0, q0)]
+    wb, xb, nb, ka, va, kb, vb, qa, qb = bufs
+    tb = device.create_buffer(trows * hd * 4)
+    pb = upload(device, np.array([dpos if dpos is not None else 0], np.int32))
+    try:
+        _check(L.aih_rope_table(h, tb.get_pointer(), trows, hd, 10000.0), "rope table")
+        pos = pb.get_pointer() if dpos is not None else None
+        x2 = nb.get_pointer() if pre == nat.PRE_RMSNORM else None
+        _check(L.aih_qgemm_fused(h, qtype, wb.get_pointer(), n, k, xb.get_pointer(), x2, EPS, m, pre,
+                                 nat.POST_STORE, qa.get_pointer()), "qgemm_fused")
+        qp = qa.get_pointer()
+        _check(L.aih_rope_qkv(h, qp, n, qp + qd * 4, n, qp + (qd + kvd) * 4, n, ka.get_pointer(), va.get_pointer(), m,
+                              nh, nkv, hd, start, pos, tb.get_pointer(), trows, crows), "rope_qkv")
+        _check(L.aih_qgemm_qkv_rope(h, qtype, wb.get_pointer(), k, xb.get_pointer(), x2, EPS, m, pre,
+                                    qb.get_pointer(), kb.get_pointer(), vb.get_pointer(), nh, nkv, hd, start, pos,
+                                    tb.get_pointer(), trows, crows), "qgemm_qkv_rope")
+        qa_h, qb_h = _read(qa, m * n).reshape(m, n), _read(qb, m * n).reshape(m, n)
+        assert np.isfinite(qa_h).all()
+        assert np.array_equal(qb_h[:, :qd].view(np.uint32), qa_h[:, :qd].view(np.uint32)), \
+            "%d of %d queries differ" % (int(np.sum(qb_h[:, :qd] != qa_h[:, :qd])), m * qd)
+        assert np.all(qb_h[:, qd:] == 7.0)
+        for a_, b_, what in ((ka, kb, "K"), (va, vb, "V")):
+            ca, cb = _read(a_, crows * kvd), _read(b_, crows * kvd)
+            assert np.array_equal(cb.view(np.uint32), ca.view(np.uint32)), "%s cache: %d differ" % (
+                what, int(np.sum(ca != cb)))
+        p0 = start + (dpos or 0)
+        stored = [r for r in range(m) if 0 <= p0 + r < min(trows, crows)]
+        if stored:
+            assert not np.array_equal(_read(kb, crows * kvd).reshape(crows, kvd)[p0 + stored[0]],
+                                      cache0[p0 + stored[0]]), "row %d was not stored" % (p0 + stored[0])
+    finally:
+        for b_ in bufs + [tb, pb]:
+            b_.dispose()
+
+
+def test_qkv_rope_gemm_argument_errors(device):
+    L, h = nat.lib(), device.handle
+    wb = upload(device, synth_weight(nat.Q4_K, 1024, 256))
+    xb = device.create_buffer(16 * 1024 * 4)
+    try:
+        w, x = wb.get_pointer(), xb.get_pointer()
+        f = L.aih_qgemm_qkv_rope
+        # head_dim 48: a 32-column block could hold the end of the queries
+        assert f(h, nat.Q4_K, w, 256, x, None, EPS, 8, 0, x, x, x, 8, 4, 48, 0, None, x, 64, 64) == \
+            nat.AIH_E_UNSUPPORTED
+        assert f(h, nat.Q4_K, w, 256, x, None, EPS, 8, nat.PRE_SILU_MUL, x, x, x, 4, 2, 128, 0, None, x, 64, 64) == \
+            nat.AIH_E_INVALID
+        assert f(h, nat.Q4_K, w, 256, x, None, EPS, 8, nat.PRE_RMSNORM, x, x, x, 4, 2, 128, 0, None, x, 64, 64) == \
+            nat.AIH_E_INVALID                                            # RMSNorm without weights
+        assert f(h, nat.Q4_K, w, 256, x, None, EPS, 8, 0, x, x, x, 4, 2, 128, 60, None, x, 64, 64) == \
+            nat.AIH_E_LIMIT                                              # rows past the cache
+        assert f(h, nat.F32, w, 256, x, None, EPS, 8, 0, x, x, x, 4, 2, 128, 0, None, x, 64, 64) == \
+            nat.AIH_E_UNSUPPORTED
+        assert f(h, nat.Q4_K, w, 256, x, None, EPS, 0, 0, x, x, x, 4, 2, 128, 0, None, x, 64, 64) == nat.AIH_OK
+        device.synchronize()
+    finally:
+        wb.dispose()
+        xb.dispose()
+
+
 @pytest.mark.parametrize("n_q,start", [(100, 0), (70, 30)])
 def test_attention_strided_equals_contiguous(device, n_q, start):
     L, h = nat.lib(), device.handle
@@ -309,7 +394,9 @@ def test_fused_prefill_layer_equals_separate_operators(device):
                 dec.fused_prefill = fused
                 tok = dec.prefill(ids)
                 logits = dec.read_logits()
-                caches = [np.concatenate([_read_ptr(device, b, 96 * CFG.kv_dim) for b in (dec.kc[l], dec.vc[l])])
+                # the rows the prompt wrote (the rest of a cache is whatever the
+                # allocation held: never read, as attention masks keys past p)
+                caches = [np.concatenate([_read_ptr(device, b, len(ids) * CFG.kv_dim) for b in (dec.kc[l], dec.vc[l])])
                           for l in range(CFG.n_layers)]
                 out.append((tok, logits, caches))
             finally:

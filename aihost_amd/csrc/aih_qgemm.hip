@@ -266,11 +266,14 @@ __device__ __forceinline__ void rope_qkv_tile(const f16v &acc0, const f16v &acc1
 // 256 (a Q4_K/Q6_K super-block, 8 blocks of Q8_0/Q4_0), with one LDS barrier
 // per super-step and two tile buffers.
 //   Producers (waves 4..7) dequantize the next super-step of the 64 weight
-//   rows into LDS: wave p owns rows 16p .. 16p+15, and its 16 lanes per row
-//   take pieces 0..15 of the row's 256-k span (four rows per load, each read
-//   as one contiguous span; four lanes per row, one 64-k step at a time, put
-//   16 rows under every load).  Their packed loads run PR super-steps ahead
-//   in a ring of register sets.
+//   rows into LDS: wave p owns rows 16p .. 16p+15.  For Q4_K, Q4_0 and Q8_0
+//   eight lanes per row take 32 weights each (the wide-tile kernel's pieces
+//   and LDS positions: two row groups of 8 per wave); for Q6_K sixteen lanes
+//   per row take pieces 0..15 of the row's 256-k span (four row groups of 4,
+//   each row read as one contiguous span), which measured faster there
+//   (4096 x 4096 x 512: 39.9 against 40.5 us per call; the 32-weight form
+//   gave Q4_0 36.2 -> 34.6 and Q8_0 36.5 -> 35.9).  Their packed loads run
+//   PR super-steps ahead in a ring of register sets.
 //   Consumers (waves 0..3): wave w owns rows 32w .. 32w+31 of the M tile and
 //   all 64 columns (two 32x32 accumulators sharing each A fragment).  A
 //   fragments come straight from the tiled fp16 copy of X, one super-step
@@ -280,9 +283,21 @@ __device__ __forceinline__ void rope_qkv_tile(const f16v &acc0, const f16v &acc1
 constexpr int SK = 256;            // k per super-step (one barrier)
 constexpr int SC = SK / 64;        // 64-k steps per super-step
 constexpr int LD2 = SK + 8;        // LDS row stride in halves (16-byte pad against bank conflicts)
-// producer ring depth in super-steps (Q6_K's larger raw sets: 2, within 256 registers)
-template <class T> struct GRing { static constexpr int PR = 3; };
-template <> struct GRing<G6K> { static constexpr int PR = 2; };
+// producer ring depth in super-steps (Q6_K's larger raw sets: 2, within 256
+// registers) and piece layout (P32: 32-weight pieces, else 16-weight)
+template <class T> struct GRing { static constexpr int PR = 3; static constexpr bool P32 = true; };
+template <> struct GRing<G6K> { static constexpr int PR = 2; static constexpr bool P32 = false; };
+
+// LDS position (in 16-byte granules) of chunk granule g of a super-step (the
+// k values 8g .. 8g+7): the 32-weight pieces' swizzle, or for 16-weight
+// pieces s of chunk c (granules 8c + 2s, + 1) 4c + s and 16 + 4c + s, so that
+// the 16 lanes of a row store 256 contiguous bytes
+template <class T, bool P32 = GRing<T>::P32> struct BPos {
+    __device__ static constexpr int pos(int g) { return Piece32<T>::type::swz(g); }
+};
+template <class T> struct BPos<T, false> {
+    __device__ static constexpr int pos(int g) { return 16 * (g & 1) + 4 * (g >> 3) + ((g >> 1) & 3); }
+};
 
 template <class T>
 __global__ void __launch_bounds__(512)
@@ -290,6 +305,10 @@ qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
              const _Float16 *__restrict__ Xt, int64_t M, float *__restrict__ Y, int epi, aih_rope_qkv_args ra)
 {
     constexpr int PR = GRing<T>::PR;
+    constexpr bool P32 = GRing<T>::P32;
+    typedef typename Piece32<T>::type Pc;
+    typedef std::conditional_t<P32, typename Pc::Raw, typename T::Raw> Raw;
+    constexpr int NR = P32 ? 2 : 4;   // row groups per producer wave
     __shared__ __align__(16) _Float16 wsh[2][BN][LD2];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
@@ -297,39 +316,50 @@ qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
     const int nss = (nch + SC - 1) / SC;
 
     if (wave >= 4) {
+        // rows 16 pw + (16 / NR) i + rl; P32: chunk pc, half ps of it (32
+        // weights); else chunk pc, piece ps (16 weights)
         const int pw = wave - 4;
-        const int rl = lane >> 4, p = lane & 15, pc = p >> 2, ps = p & 3;
-        const uint8_t *wrow[4];
+        constexpr int LPR = 64 * NR / 16;   // lanes per row
+        const int rl = lane / LPR, p = lane % LPR, pc = p / (LPR / 4), ps = p % (LPR / 4);
+        const uint8_t *wrow[NR];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int64_t wn = n0 + 16 * pw + 4 * i + rl;
+        for (int i = 0; i < NR; ++i) {
+            const int64_t wn = n0 + 16 * pw + (16 / NR) * i + rl;
             wrow[i] = W + (wn < N ? wn : N - 1) * row_bytes;
         }
-        auto gload = [&](int ss, typename T::Raw *r) {
+        auto gload = [&](int ss, Raw *r) {
             int c = ss * SC + pc;
             c = c < nch ? c : nch - 1;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) T::load(wrow[i], c, ps, r[i]);
+            for (int i = 0; i < NR; ++i) {
+                if constexpr (P32) Pc::load(wrow[i], c, ps, r[i]);
+                else T::load(wrow[i], c, ps, r[i]);
+            }
         };
         // chunks past K exist only in a last, partial super-step, staged as
         // zeros: only the stages after the main loop test for them
-        auto stage = [&](auto tail, int ss, int buf, const typename T::Raw *r) {
+        auto stage = [&](auto tail, int ss, int buf, const Raw *r) {
             asm volatile("" : "+s"(ss));
             const int c = ss * SC + pc;
+            const bool zero = decltype(tail)::value && c >= nch;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                h8 lo, hi;
-                piece16h<T>(r[i], c, ps, lo, hi);
-                if (decltype(tail)::value && c >= nch) lo = hi = h8{};
-                // chunk granules 8 pc + 2 ps (lo) and + 1 (hi) at LDS
-                // granules 4 pc + ps and 16 + 4 pc + ps: the 16 lanes of a
-                // row store 256 contiguous bytes (no bank conflict)
-                _Float16 *d = &wsh[buf][16 * pw + 4 * i + rl][0];
-                *reinterpret_cast<h8 *>(d + 8 * (4 * pc + ps)) = lo;
-                *reinterpret_cast<h8 *>(d + 8 * (16 + 4 * pc + ps)) = hi;
+            for (int i = 0; i < NR; ++i) {
+                _Float16 *d = &wsh[buf][16 * pw + (16 / NR) * i + rl][0];
+                if constexpr (P32) {
+                    h8 o[4];
+                    Pc::piece(r[i], c, ps, o);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        *reinterpret_cast<h8 *>(d + 8 * Pc::swz(8 * pc + Pc::col(ps, q) / 8)) = zero ? h8{} : o[q];
+                } else {
+                    h8 lo, hi;
+                    piece16h<T>(r[i], c, ps, lo, hi);
+                    *reinterpret_cast<h8 *>(d + 8 * BPos<T>::pos(8 * pc + 2 * ps)) = zero ? h8{} : lo;
+                    *reinterpret_cast<h8 *>(d + 8 * BPos<T>::pos(8 * pc + 2 * ps + 1)) = zero ? h8{} : hi;
+                }
             }
         };
-        typename T::Raw ring[PR][4];
+        Raw ring[PR][NR];
 #pragma unroll
         for (int j = 0; j < PR; ++j) gload(j, ring[j]);
         __builtin_amdgcn_sched_barrier(0);
@@ -384,8 +414,8 @@ qgemm_kernel(const uint8_t *W, int64_t N, int64_t K, int64_t row_bytes,
     auto bload = [&](int buf, int t, BF &b) {
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-            b.b0[kk] = *reinterpret_cast<const h8 *>(&wsh[buf][fr][8 * (2 * fk + 4 * t + kk)]);
-            b.b1[kk] = *reinterpret_cast<const h8 *>(&wsh[buf][32 + fr][8 * (2 * fk + 4 * t + kk)]);
+            b.b0[kk] = *reinterpret_cast<const h8 *>(&wsh[buf][fr][8 * BPos<T>::pos(8 * t + 2 * kk + fk / 8)]);
+            b.b1[kk] = *reinterpret_cast<const h8 *>(&wsh[buf][32 + fr][8 * BPos<T>::pos(8 * t + 2 * kk + fk / 8)]);
         }
     };
     auto mm = [&](const AF &f, const BF &b) {

@@ -579,12 +579,21 @@ int launch_t(aih_ctx *ctx, const uint8_t *W, int64_t N, int64_t K, int64_t row_b
     if (ntiles > 0x7FFFFFFF || nunits > 0x7FFFFFFF) return AIH_E_LIMIT;
     // buffer resources: a tile's rows and all of X within 31-bit offsets
     if (RWG * row_bytes > 0x7FFFFFFF || ((int64_t)(batch - 1) * ldx + K) * 4 > 0x7FFFFFFF) return AIH_E_LIMIT;
-    // Splits: about two workgroups per CU (four waves each).
+    // Splits of K: at least about two workgroups per CU (four waves each),
+    // and at least min(8, units / 2) splits, since small per-workgroup K
+    // ranges measured faster at every shape but the widest K (per call on
+    // MI355X, 8 columns: Q4_0 14336 x 4096 41.2 -> 32.6 us, Q4_K 14336 x 4096
+    // 22.2 -> 20.1 us, the Q6_K 32000 x 4096 head at 5 columns 42.2 -> 39.7
+    // us; Q6_K 4096 x 14336 keeps its 8 splits of 7 units).  The partial sums stay
+    // within the allocation-free entry point's buffer, so that both entry
+    // points split a shape alike.
     const int64_t cu = ctx->cu_count > 0 ? ctx->cu_count : 256;
-    int64_t S = std::min<int64_t>(nunits, std::max<int64_t>(1, (2 * cu + ntiles - 1) / ntiles));
+    const int64_t np = ntiles * RWG;
+    int64_t S = std::max<int64_t>((2 * cu + ntiles - 1) / ntiles, std::min<int64_t>(8, (nunits + 1) / 2));
+    S = std::min<int64_t>(S, nunits);
+    S = std::max<int64_t>(1, std::min<int64_t>(S, (int64_t)(AIH_NOALLOC_SCRATCH_BYTES / ((size_t)batch * np * sizeof(float)))));
     int64_t per = (nunits + S - 1) / S;
     S = (nunits + per - 1) / per;
-    const int64_t np = ntiles * RWG;
     float *P = nullptr;
     if (S > 1) {
         void *ws = nullptr;

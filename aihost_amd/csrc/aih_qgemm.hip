@@ -278,8 +278,9 @@ __device__ __forceinline__ void rope_qkv_tile(const f16v &acc0, const f16v &acc1
 //   all 64 columns (two 32x32 accumulators sharing each A fragment).  A
 //   fragments come straight from the tiled fp16 copy of X, one super-step
 //   ahead; B fragments from LDS.
-// On MI355X this ran the 4096 x 4096 x 512 Q4_K product in 38 us per call
-// (with the X conversion), against 42 us for one barrier per 64 k.
+// On MI355X the 4096 x 4096 x 512 Q4_K product takes 35-37 us per call (the
+// kernel 27-28 us, the X conversion 7.5 us), against 42 us for an earlier
+// form with one barrier per 64 k.
 constexpr int SK = 256;            // k per super-step (one barrier)
 constexpr int SC = SK / 64;        // 64-k steps per super-step
 constexpr int LD2 = SK + 8;        // LDS row stride in halves (16-byte pad against bank conflicts)

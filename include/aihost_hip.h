@@ -187,7 +187,9 @@ int aih_dequantize(aih_ctx *ctx, int type, const void *q, float *out,
 
 /* Decode matvec, dequantization fused:
  *   Y[b*ldy + n] = sum_k X[b*ldx + k] * W[n, k],   b < batch (1..8), n < N.
- * K must be a whole number of blocks.  fp32 accumulation.  For batch 3..8, K
+ * K must be a multiple of 64 (a whole number of blocks; the kernels read
+ * 64-element units) and at most 65536, else AIH_E_LIMIT.  fp32
+ * accumulation.  For batch 3..8, K
  * is split over workgroups and the partial sums (splits x batch x N floats)
  * go through the context workspace (see aih_qgemm); a call captured into a
  * graph before the workspace is large enough runs with one split instead.

@@ -154,6 +154,28 @@ def _read_image(device, buf, m, k):
     return vals, E.copy(), d.copy()
 
 
+def _write_image(device, vals, E, d, m, k):
+    """An operand image buffer holding rows `vals` (mpad x k fp16), row
+    exponents E and block exponents d (the layout _read_image reads)."""
+    mpad = (m + 31) // 32 * 32
+    raw = np.zeros(nat.operand_bytes(m, k), np.uint8)
+    halves = raw[:2 * mpad * k].view(np.float16)
+    halves[_slots(mpad, k).ravel()] = vals.reshape(-1)
+    raw[2 * mpad * k:2 * mpad * k + 4 * mpad] = np.ascontiguousarray(E, np.int32).view(np.uint8)
+    raw[2 * mpad * k + 4 * mpad:] = np.ascontiguousarray(d, np.int8).reshape(-1).view(np.uint8)
+    return upload(device, raw)
+
+
+def _gemm_from_image(device, qtype, w_buf, n, k, img, m):
+    y = device.create_buffer(m * n * 4)
+    try:
+        nat.check(nat.lib().aih_qgemm_fused(device.handle, qtype, w_buf.get_pointer(), n, k, img.get_pointer(), None,
+                                            EPS, m, nat.PRE_F16_OPERAND, nat.POST_STORE, y.get_pointer()), "gemm")
+        return y.read_range(0, m * n, np.float32).reshape(m, n)
+    finally:
+        y.dispose()
+
+
 def _expected_block_image(v, mpad):
     """Values of rows v rounded to fp16 at their block exponents (rows past
     M zero), and those exponents."""
@@ -186,8 +208,9 @@ def test_silu_operand_image_and_down_gemm(device, orc, scale):
     reading that image: the image holds SiLU(gate)*up of the separate
     operators (aih_rmsnorm, aih_qgemm, aih_silu_mul_pairs) rounded at its block
     exponents, bit for bit; the down GEMM first gives every row one exponent
-    (checked bit for bit) and its output matches the oracle on the separate
-    path's fp32 operand.  Norm weights scaled by 1e3 put the SiLU output far
+    (checked bit for bit, and its output is bit for bit that of the same GEMM
+    on the host's one-exponent image) and its output matches the oracle on
+    the separate path's fp32 operand.  Norm weights scaled by 1e3 put the SiLU output far
     above 65504, by 1e-4 far below 2^-12."""
     L, h = nat.lib(), device.handle
     d, f, m = 512, 1024, 100
@@ -225,6 +248,12 @@ def test_silu_operand_image_and_down_gemm(device, orc, scale):
         assert np.array_equal(E2, wantE)
         assert np.array_equal(vals2.view(np.uint16), want2.view(np.uint16))
         yh = y.read_range(0, m * d, np.float32).reshape(m, d)
+        fixed = _write_image(device, want2, wantE, want_d2, m, f)
+        try:
+            y_fixed = _gemm_from_image(device, nat.Q6_K, wdn, d, f, fixed, m)
+        finally:
+            fixed.dispose()
+        assert np.array_equal(yh.view(np.uint32), y_fixed.view(np.uint32))
         nrm, mx = check_rows(yh, orc.matvec(nat.Q6_K, w_dn, d, f, uh, nthreads=8), 1e-3, "down, scale %g" % scale)
         print("scale %g: down GEMM from the image normwise %.3g max %.3g" % (scale, nrm, mx))
     finally:
@@ -275,6 +304,14 @@ def test_attention_operand_image_wide_range(device, orc, vscale):
         nat.check(L.aih_qgemm_fused(h, nat.Q4_K, wb.get_pointer(), n_out, qd, img.get_pointer(), None, EPS, n_q,
                                     nat.PRE_F16_OPERAND, nat.POST_STORE, y.get_pointer()), "W_o")
         yh = y.read_range(0, n_q * n_out, np.float32).reshape(n_q, n_out)
+        # bit for bit the GEMM of the host's one-exponent image
+        want2, wantE, want_d2 = _expected_after_fixup(vals, dd)
+        fixed = _write_image(device, want2, wantE, want_d2, n_q, qd)
+        try:
+            y_fixed = _gemm_from_image(device, nat.Q4_K, wb, n_out, qd, fixed, n_q)
+        finally:
+            fixed.dispose()
+        assert np.array_equal(yh.view(np.uint32), y_fixed.view(np.uint32))
         check_rows(yh, orc.matvec(nat.Q4_K, w, n_out, qd, out, nthreads=8), 1e-3, "W_o, V x %g" % vscale)
     finally:
         for b in bufs + [o, img, y, sb]:
